@@ -1,0 +1,308 @@
+#!/usr/bin/env python3
+"""Benchmark of the fused 4-bit dequant-GEMV on one MI355X.
+
+A "step" is one fused dequant-GEMV call over one layer for one batch of activations,
+with the packed weight and x already resident in HBM.  The default workload is the
+north-star layer: GF4 (Jenks-16 codebooks, group 128), K=8192 -> N=28672, batch 1
+Prints ONE JSON line (the contract in the repo README);
+``--sweep`` additionally writes one line per config shape to ``--sweep-out``.
+
+Throughput = algorithmic bytes per call / time per call, with
+GF4 bytes = N*K/2 + N*(K/128)*32 + B*K*2 + B*N*2 and
+E2M1 bytes = N*K/2 + N*(K/32) + B*K*2 + B*N*2 (each byte counted once).
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import os
+import platform
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+import torch
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+from if_i_could_turn_back_time_amd import PackedWeight, fwht_block_for  # noqa: E402
+from if_i_could_turn_back_time_amd import _capi as C  # noqa: E402
+
+PEAK_GBS = 8000.0
+METRIC = "achieved HBM GB/s (% of roofline) & µs/call, 4-bit dequant-GEMV at batch 1"
+
+# name -> (fmt, K, N, B, generator, fwht)
+WORKLOADS = {
+    "gf4_k8192_n28672_b1": ("gf4", 8192, 28672, 1, "cfg4", False),
+    "gf4_k28672_n8192_b1": ("gf4", 28672, 8192, 1, "cfg4", False),
+    "gf4_k8192_n28672_b2": ("gf4", 8192, 28672, 2, "cfg4", False),
+    "gf4_k8192_n28672_b4": ("gf4", 8192, 28672, 4, "cfg4", False),
+    "gf4_k28672_n8192_b2": ("gf4", 28672, 8192, 2, "cfg4", False),
+    "gf4_k4096_n4096_b1": ("gf4", 4096, 4096, 1, "cfg1", False),
+    "e2m1_k4096_n4096_b1": ("e2m1", 4096, 4096, 1, "cfg2", False),
+    "e2m1_k4096_n11008_b1": ("e2m1", 4096, 11008, 1, "cfg2", False),
+    "e2m1_k11008_n4096_b1": ("e2m1", 11008, 4096, 1, "cfg2", False),
+    "gf4fwht_k4096_n4096_b1": ("gf4", 4096, 4096, 1, "cfg1", True),
+    "gf4fwht_k4096_n11008_b1": ("gf4", 4096, 11008, 1, "cfg1", True),
+    "gf4fwht_k11008_n4096_b1": ("gf4", 11008, 4096, 1, "cfg1", True),
+}
+DEFAULT = "gf4_k8192_n28672_b1"
+
+
+def synth(kind: str, N: int, K: int, B: int, xdtype):
+    """Seeded synthetic inputs (CPU generator, seed 0; order: weights, outlier masks,
+    activations), per the input-generation rules of the benchmark configs."""
+    g = torch.Generator().manual_seed(0)
+    if kind == "cfg4":
+        w = torch.randn(N, K, generator=g) * 0.015
+        m = torch.rand(N, K, generator=g) < 0.005
+        w[m] = torch.randn(int(m.sum()), generator=g) * (8 * 0.015)
+        x = torch.randn(B, K, generator=g)
+    elif kind == "cfg2":
+        nu = 5
+        z = torch.randn(N, K, generator=g)
+        chi = sum(torch.randn(N, K, generator=g) ** 2 for _ in range(nu))
+        w = z / torch.sqrt(chi / nu) * (0.02 / np.sqrt(nu / (nu - 2)))
+        x = torch.randn(B, K, generator=g)
+        n_out = max(1, round(0.001 * K))
+        pos = torch.randperm(K, generator=g)[:n_out]
+        x[:, pos] *= 20.0
+    else:  # cfg1 / cfg3
+        w = torch.randn(N, K, generator=g) * 0.02
+        x = torch.randn(B, K, generator=g)
+    return w.contiguous(), x.to(xdtype)
+
+
+def time_gpu(pw: PackedWeight, x: torch.Tensor, y: torch.Tensor, steps: int, warmup: int):
+    """Back-to-back launches on the current stream, timed with HIP events on that stream
+    (the stream fb_gemv launches on).  Returns mean ms per call."""
+    L = C.lib()
+    shape = pw.shape(x.shape[0], x.dtype, y.dtype)
+    sref = ctypes.byref(shape)
+    wp, xp, yp = pw.wdev.data_ptr(), x.data_ptr(), y.data_ptr()
+    stream = torch.cuda.current_stream()
+    sp = stream.cuda_stream
+    for _ in range(warmup):
+        C.check(L.fb_gemv(wp, xp, yp, sref, None, 0, sp))
+    torch.cuda.synchronize()
+    t0 = torch.cuda.Event(enable_timing=True)
+    t1 = torch.cuda.Event(enable_timing=True)
+    t0.record(stream)
+    for _ in range(steps):
+        L.fb_gemv(wp, xp, yp, sref, None, 0, sp)
+    t1.record(stream)
+    torch.cuda.synchronize()
+    return t0.elapsed_time(t1) / steps
+
+
+def time_gpu_graph(pw, x, y, steps: int, reps: int = 5):
+    """Same calls captured in one HIP graph (launch overhead removed)."""
+    L = C.lib()
+    shape = pw.shape(x.shape[0], x.dtype, y.dtype)
+    sref = ctypes.byref(shape)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(s):
+        C.check(L.fb_gemv(pw.wdev.data_ptr(), x.data_ptr(), y.data_ptr(), sref, None, 0,
+                          s.cuda_stream))
+        torch.cuda.synchronize()
+        with torch.cuda.graph(graph, stream=s):
+            for _ in range(steps):
+                L.fb_gemv(pw.wdev.data_ptr(), x.data_ptr(), y.data_ptr(), sref, None, 0,
+                          torch.cuda.current_stream().cuda_stream)
+    graph.replay()
+    torch.cuda.synchronize()
+    best = float("inf")
+    for _ in range(reps):
+        t0 = torch.cuda.Event(enable_timing=True)
+        t1 = torch.cuda.Event(enable_timing=True)
+        t0.record()
+        graph.replay()
+        t1.record()
+        torch.cuda.synchronize()
+        best = min(best, t0.elapsed_time(t1) / steps)
+    return best
+
+
+def cpu_baseline(pw: PackedWeight, x: torch.Tensor, budget_s: float = 12.0):
+    """The reference's forward structure on the host CPU (layers.py:36-38): every call
+    dequantizes the packed weight to fp32 [N,K], then F.linear.  Run on a bounded row
+    sample; throughput is the sample's algorithmic bytes per second."""
+    from oracle import fourbit_oracle as O
+
+    threads = os.cpu_count() or 1
+    torch.set_num_threads(threads)
+    codes_all = pw.codes
+    meta_all = pw.meta
+    N = pw.N
+    rows = N
+
+    def one_call(r):
+        codes = O.unpack_nibbles(codes_all[:r].numpy())
+        if pw.fmt_name == "gf4":
+            W = O.dequant_f32("gf4", codes, meta_all[:r].numpy().view(np.uint16))
+        else:
+            W = O.dequant_f32("e2m1", codes, meta_all[:r].numpy())
+        return torch.nn.functional.linear(x.float(), W)
+
+    # size the sample so one call takes about a second
+    probe = min(N, 512)
+    t = time.perf_counter()
+    one_call(probe)
+    per_row = (time.perf_counter() - t) / probe
+    rows = int(max(64, min(N, 1.0 / max(per_row, 1e-9))))
+    one_call(rows)  # warm-up
+    times = []
+    t_start = time.perf_counter()
+    while len(times) < 10 or (time.perf_counter() - t_start) < budget_s * 0.5:
+        t = time.perf_counter()
+        one_call(rows)
+        times.append(time.perf_counter() - t)
+        if time.perf_counter() - t_start > budget_s:
+            break
+    med = float(np.median(times))
+    B = x.shape[0]
+    frac = rows / N
+    sample_bytes = pw.algorithmic_bytes(B) * frac
+    return {
+        "value": sample_bytes / med / 1e9,
+        "unit": "GB/s",
+        "cores": torch.get_num_threads(),
+        "kind": "port",
+        "sample": (f"{rows} of {N} rows per call (dequantize packed->fp32 then F.linear, "
+                   f"median of {len(times)} calls); CPU: {platform.processor() or platform.machine()}, "
+                   f"os.cpu_count()={threads}"),
+        "us_per_call_full_layer_est": med / frac * 1e6,
+    }
+
+
+def load_traffic(name: str):
+    p = ROOT / "profiles" / f"traffic_{name}.json"
+    if p.exists():
+        try:
+            return json.loads(p.read_text()).get("traffic_bytes")
+        except Exception:
+            return None
+    return None
+
+
+def run_workload(name: str, steps: int, warmup: int, want_cpu: bool, check: bool = True,
+                 graph: bool = True):
+    fmt, K, N, B, kind, fwht = WORKLOADS[name]
+    xdt = torch.float16 if fmt == "gf4" else torch.bfloat16
+    w, x = synth(kind, N, K, B, xdt)
+    fb = fwht_block_for(K) if fwht else 0
+    t = time.perf_counter()
+    pw = PackedWeight.quantize(w, fmt, fwht_block=fb, device="cuda:0")
+    pack_s = time.perf_counter() - t
+    del w
+    xd = x.to("cuda:0")
+    y = torch.empty(B, N, dtype=xdt, device="cuda:0")
+    ms = time_gpu(pw, xd, y, steps, warmup)
+    ms_graph = time_gpu_graph(pw, xd, y, min(steps, 200)) if graph else None
+    nbytes = pw.algorithmic_bytes(B)
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    rec = {
+        "workload": name, "fmt": fmt, "K": K, "N": N, "B": B, "fwht_block": fb,
+        "bytes_per_call": nbytes, "weight_stream_bytes": N * K // 2,
+        "us_per_call": ms * 1e3, "GBps": gbs, "frac_of_8TBps": gbs / PEAK_GBS,
+        "us_per_call_graph": None if ms_graph is None else ms_graph * 1e3,
+        "GBps_graph": None if ms_graph is None else nbytes / (ms_graph * 1e-3) / 1e9,
+        "tokens_per_s_equiv": B / (ms * 1e-3), "pack_s": pack_s,
+    }
+    if check:  # spot parity: sampled rows vs exact host decode + F.linear (fp32)
+        yk = torch.empty(B, N, dtype=torch.float32, device="cuda:0")
+        pw.gemv(xd, out=yk)
+        rows = torch.randint(0, N, (64,), generator=torch.Generator().manual_seed(1))
+        Wr = torch.from_numpy(np.stack([pw.dequant_host_row(int(r)) for r in rows]))
+        xin = x.float()
+        if fb:
+            from oracle import fourbit_oracle as O
+            xin = O.rotate_x(xin, fb)
+        yref = torch.nn.functional.linear(xin, Wr)
+        err = (yk.cpu()[:, rows] - yref).abs()
+        rec["parity_ok"] = bool((err <= 1e-2 + 1e-3 * yref.abs()).all())
+        rec["parity_max_abs_err"] = float(err.max())
+    if want_cpu:
+        rec["cpu_baseline"] = cpu_baseline(pw, x)
+    return rec, pw
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=500)
+    ap.add_argument("--warmup", type=int, default=50)
+    ap.add_argument("--workload", default=DEFAULT, choices=sorted(WORKLOADS))
+    ap.add_argument("--sweep", action="store_true", help="also time every config shape")
+    ap.add_argument("--sweep-out", default="gpurun_out/bench_sweep.jsonl")
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build runs on one GPU only (got --gpus {args.gpus}); the "
+              "multi-GPU sharding of the GEMV is a design note, not a measured path.",
+              file=sys.stderr)
+        sys.exit(2)
+    if not torch.cuda.is_available():
+        print("bench.py: no ROCm GPU visible", file=sys.stderr)
+        sys.exit(1)
+
+    if args.sweep:
+        Path(args.sweep_out).parent.mkdir(parents=True, exist_ok=True)
+        with open(args.sweep_out, "w") as f:
+            for name in WORKLOADS:
+                if name == args.workload:
+                    continue
+                rec, pw = run_workload(name, max(50, args.steps // 2), args.warmup, False)
+                del pw
+                torch.cuda.empty_cache()
+                f.write(json.dumps(rec) + "\n")
+                f.flush()
+                print(f"[sweep] {name}: {rec['us_per_call']:.2f} us, {rec['GBps']:.0f} GB/s, "
+                      f"parity {rec.get('parity_ok')}", file=sys.stderr, flush=True)
+
+    rec, pw = run_workload(args.workload, args.steps, args.warmup, not args.no_cpu)
+    fmt, K, N, B = rec["fmt"], rec["K"], rec["N"], rec["B"]
+    achieved = rec["GBps"]
+    out = {
+        "metric": METRIC,
+        "value": achieved,
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": rec["us_per_call"] / 1e3,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16" if fmt == "gf4" else "bf16",
+        "data": "synthetic (seeded; weights packed by the native Jenks/E2M1 packer)",
+        "config": {
+            "workload": args.workload, "format": fmt, "K": K, "N": N, "batch": B,
+            "fwht_block": rec["fwht_block"], "group": 128 if fmt == "gf4" else 32,
+            "accumulate": "fp32", "us_per_call": rec["us_per_call"],
+            "frac_of_peak": achieved / PEAK_GBS,
+            "tokens_per_s_equiv": rec["tokens_per_s_equiv"],
+            "bytes_per_call": rec["bytes_per_call"],
+            "weight_stream_bytes": rec["weight_stream_bytes"],
+            "us_per_call_hipgraph": rec["us_per_call_graph"],
+            "parity_ok": rec.get("parity_ok"),
+        },
+        "roofline": {
+            "bound": "hbm", "achieved": achieved, "peak": PEAK_GBS, "unit": "GB/s",
+            "frac": achieved / PEAK_GBS, "traffic": load_traffic(args.workload),
+        },
+        "cpu_baseline": rec.get("cpu_baseline"),
+    }
+    if out["cpu_baseline"] is not None:
+        out["cpu_baseline"] = {k: v for k, v in out["cpu_baseline"].items()
+                               if k in ("value", "unit", "cores", "kind", "sample")}
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,196 @@
+"""ctypes binding of libfourbit.so (the C ABI declared in ``include/fourbit.h``).
+
+The reference binds its native code with ``torch.utils.cpp_extension.load_inline`` and
+torch::Tensor signatures (``Python_Jenks_Test/Jenks_Tests/cuda_helpers.py:42-62``);
+here the boundary is a plain C ABI: tensors cross it as ``data_ptr()`` integers, the
+HIP stream as ``torch.cuda.current_stream().cuda_stream``, and every non-zero status
+becomes a ``RuntimeError`` carrying ``fb_strerror`` (the reference's ``TORCH_CHECK``
+failures surface the same way, ``cuda_helpers.py:72-78``).
+
+There is no fallback: if the library is missing, every call raises.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from pathlib import Path
+
+import torch
+
+LIB_PATH = Path(__file__).resolve().with_name("libfourbit.so")
+
+FMT_GF4, FMT_E2M1 = 0, 1
+DT_F16, DT_BF16, DT_F32 = 0, 1, 2
+FMT_BY_NAME = {"gf4": FMT_GF4, "e2m1": FMT_E2M1}
+GROUP_BY_FMT = {FMT_GF4: 128, FMT_E2M1: 32}
+DTYPE_CODE = {torch.float16: DT_F16, torch.bfloat16: DT_BF16, torch.float32: DT_F32}
+ABI_VERSION = 1
+
+# every symbol include/fourbit.h declares
+EXPORTED = (
+    "fb_abi_version", "fb_strerror", "fb_validate", "fb_device_bytes", "fb_workspace_bytes",
+    "fb_quantize_gf4", "fb_quantize_e2m1", "fb_fwht_rows_f32", "fb_to_device",
+    "fb_from_device", "fb_dequant_host", "fb_gemv", "fb_dequant",
+)
+
+
+class FbShape(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_int32) for n in
+                ("N", "K", "B", "group", "fmt", "fwht_block", "x_dtype", "y_dtype")]
+
+
+_lib = None
+
+
+def lib() -> ctypes.CDLL:
+    """Loads libfourbit.so once (raises if it has not been built)."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not LIB_PATH.exists():
+        raise RuntimeError(
+            f"{LIB_PATH} is missing: build it with `python -m if_i_could_turn_back_time_amd.build_lib`"
+        )
+    L = ctypes.CDLL(str(LIB_PATH))
+    vp, i32, sz = ctypes.c_void_p, ctypes.c_int32, ctypes.c_size_t
+    sp = ctypes.POINTER(FbShape)
+    sigs = {
+        "fb_abi_version": (i32, []),
+        "fb_strerror": (ctypes.c_char_p, [ctypes.c_int]),
+        "fb_validate": (ctypes.c_int, [sp]),
+        "fb_device_bytes": (sz, [sp]),
+        "fb_workspace_bytes": (sz, [sp]),
+        "fb_quantize_gf4": (ctypes.c_int, [vp, i32, i32, vp, vp, i32]),
+        "fb_quantize_e2m1": (ctypes.c_int, [vp, i32, i32, vp, vp, i32]),
+        "fb_fwht_rows_f32": (ctypes.c_int, [vp, i32, i32, i32, i32]),
+        "fb_to_device": (ctypes.c_int, [vp, vp, vp, sp]),
+        "fb_from_device": (ctypes.c_int, [vp, vp, vp, sp]),
+        "fb_dequant_host": (ctypes.c_int, [vp, vp, vp, sp]),
+        "fb_gemv": (ctypes.c_int, [vp, vp, vp, sp, vp, sz, vp]),
+        "fb_dequant": (ctypes.c_int, [vp, vp, i32, sp, vp]),
+    }
+    for name, (res, args) in sigs.items():
+        fn = getattr(L, name)
+        fn.restype, fn.argtypes = res, args
+    if L.fb_abi_version() != ABI_VERSION:
+        raise RuntimeError(f"libfourbit ABI {L.fb_abi_version()} != expected {ABI_VERSION}")
+    _lib = L
+    return L
+
+
+def strerror(code: int) -> str:
+    return lib().fb_strerror(code).decode()
+
+
+def check(code: int) -> None:
+    if code != 0:
+        raise RuntimeError(strerror(code))
+
+
+def nthreads_default() -> int:
+    return max(1, min(16, os.cpu_count() or 1))
+
+
+def make_shape(N, K, B=1, fmt=FMT_GF4, fwht_block=0, x_dtype=DT_F16, y_dtype=DT_F16) -> FbShape:
+    return FbShape(N, K, B, GROUP_BY_FMT[fmt], fmt, fwht_block, x_dtype, y_dtype)
+
+
+def _ptr(t: torch.Tensor) -> int:
+    return t.data_ptr()
+
+
+def _host_contig(t: torch.Tensor, dtype) -> torch.Tensor:
+    if t.device.type != "cpu":
+        raise ValueError("host packers take CPU tensors")
+    return t.detach().to(dtype).contiguous()
+
+
+# ------------------------------------------------------------------ host packers
+def quantize_gf4(w: torch.Tensor, nthreads: int | None = None):
+    """fp32 [N,K] -> (codes uint8 [N,K/2], codebook uint16-as-int16 [N,K/128,16])."""
+    w = _host_contig(w, torch.float32)
+    N, K = w.shape
+    codes = torch.empty(N, K // 2, dtype=torch.uint8)
+    book = torch.empty(N, max(K // 128, 1), 16, dtype=torch.int16)
+    check(lib().fb_quantize_gf4(_ptr(w), N, K, _ptr(codes), _ptr(book),
+                                nthreads or nthreads_default()))
+    return codes, book
+
+
+def quantize_e2m1(w: torch.Tensor, nthreads: int | None = None):
+    """fp32 [N,K] -> (codes uint8 [N,K/2], scales uint8 [N,K/32])."""
+    w = _host_contig(w, torch.float32)
+    N, K = w.shape
+    codes = torch.empty(N, K // 2, dtype=torch.uint8)
+    scales = torch.empty(N, max(K // 32, 1), dtype=torch.uint8)
+    check(lib().fb_quantize_e2m1(_ptr(w), N, K, _ptr(codes), _ptr(scales),
+                                 nthreads or nthreads_default()))
+    return codes, scales
+
+
+def fwht_rows(w: torch.Tensor, block: int, nthreads: int | None = None) -> torch.Tensor:
+    """Returns w with every K-block rotated: w H_b / sqrt(b) (fp64 math, fp32 result)."""
+    out = _host_contig(w, torch.float32).clone()
+    N, K = out.shape
+    check(lib().fb_fwht_rows_f32(_ptr(out), N, K, block, nthreads or nthreads_default()))
+    return out
+
+
+def device_bytes(shape: FbShape) -> int:
+    n = lib().fb_device_bytes(ctypes.byref(shape))
+    if n == 0:
+        check(lib().fb_validate(ctypes.byref(shape)))
+    return n
+
+
+def to_device_layout(codes: torch.Tensor, meta: torch.Tensor, shape: FbShape) -> torch.Tensor:
+    """Canonical host buffers -> device weight stream (uint8 CPU tensor)."""
+    codes = _host_contig(codes, torch.uint8)
+    meta = meta.detach().contiguous()
+    out = torch.empty(device_bytes(shape), dtype=torch.uint8)
+    check(lib().fb_to_device(_ptr(codes), _ptr(meta), _ptr(out), ctypes.byref(shape)))
+    return out
+
+
+def from_device_layout(wdev: torch.Tensor, shape: FbShape):
+    wdev = _host_contig(wdev, torch.uint8)
+    codes = torch.empty(shape.N, shape.K // 2, dtype=torch.uint8)
+    if shape.fmt == FMT_GF4:
+        meta = torch.empty(shape.N, shape.K // 128, 16, dtype=torch.int16)
+    else:
+        meta = torch.empty(shape.N, shape.K // 32, dtype=torch.uint8)
+    check(lib().fb_from_device(_ptr(wdev), _ptr(codes), _ptr(meta), ctypes.byref(shape)))
+    return codes, meta
+
+
+def dequant_host(codes: torch.Tensor, meta: torch.Tensor, shape: FbShape) -> torch.Tensor:
+    codes = _host_contig(codes, torch.uint8)
+    meta = meta.detach().contiguous()
+    out = torch.empty(shape.N, shape.K, dtype=torch.float32)
+    check(lib().fb_dequant_host(_ptr(codes), _ptr(meta), _ptr(out), ctypes.byref(shape)))
+    return out
+
+
+# ------------------------------------------------------------------ GPU entry points
+def _stream(dev: torch.device) -> int:
+    return torch.cuda.current_stream(dev).cuda_stream
+
+
+def gemv(wdev: torch.Tensor, x: torch.Tensor, y: torch.Tensor, shape: FbShape) -> torch.Tensor:
+    """y[B,N] = x'[B,K] . W^T on the GPU (asynchronous on the current stream)."""
+    if not (wdev.is_cuda and x.is_cuda and y.is_cuda):
+        raise RuntimeError("fb_gemv needs device tensors (ROCm GPU)")
+    if not (x.is_contiguous() and y.is_contiguous()):
+        raise ValueError("x and y must be contiguous")
+    check(lib().fb_gemv(_ptr(wdev), _ptr(x), _ptr(y), ctypes.byref(shape), None, 0,
+                        _stream(x.device)))
+    return y
+
+
+def dequant_device(wdev: torch.Tensor, shape: FbShape, out_dtype=torch.float32) -> torch.Tensor:
+    if not wdev.is_cuda:
+        raise RuntimeError("fb_dequant needs a device tensor (ROCm GPU)")
+    out = torch.empty(shape.N, shape.K, dtype=out_dtype, device=wdev.device)
+    check(lib().fb_dequant(_ptr(wdev), _ptr(out), DTYPE_CODE[out_dtype], ctypes.byref(shape),
+                           _stream(wdev.device)))
+    return out

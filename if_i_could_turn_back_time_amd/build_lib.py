@@ -1,0 +1,72 @@
+"""Builds libfourbit.so in-tree: hipcc for the gfx950 kernels, g++ for the host packers.
+
+Run as ``python -m if_i_could_turn_back_time_amd.build_lib`` (``__graft_entry__.build()``
+calls :func:`build`).  Always recompiles.  Objects go to ``_build/`` at the repo root;
+the shared library lands next to this file, where ``_capi`` loads it from.
+"""
+from __future__ import annotations
+
+import os
+import shutil
+import subprocess
+import sys
+from pathlib import Path
+
+PKG = Path(__file__).resolve().parent
+ROOT = PKG.parent
+CSRC = PKG / "csrc"
+INCLUDE = ROOT / "include"
+BUILD = ROOT / "_build"
+LIB = PKG / "libfourbit.so"
+ARCH = "gfx950"
+
+# packed fp32 VALU ops are disabled for every HIP translation unit
+HIP_FLAGS = [
+    f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-Wno-unused-command-line-argument",
+]
+HOST_FLAGS = ["-O3", "-std=c++17", "-fPIC", "-ffp-contract=off", "-Wall"]
+
+
+def _hipcc() -> str:
+    for cand in (shutil.which("hipcc"), "/opt/rocm/bin/hipcc"):
+        if cand and os.path.exists(cand):
+            return cand
+    raise RuntimeError("hipcc not found (ROCm is required to build libfourbit.so)")
+
+
+def _run(cmd: list[str]) -> None:
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        sys.stderr.write(r.stdout + r.stderr)
+        raise RuntimeError(f"build step failed ({r.returncode}): {' '.join(cmd)}")
+    # hipcc's host pass warns that it does not know the packed-fp32 feature: harmless
+    noise = "is not a recognized feature for this target"
+    err = "\n".join(l for l in r.stderr.splitlines() if noise not in l)
+    if err.strip():
+        sys.stderr.write(err + "\n")
+
+
+def build(verbose: bool = False) -> Path:
+    BUILD.mkdir(exist_ok=True)
+    inc = [f"-I{INCLUDE}", f"-I{CSRC}"]
+    host_o = BUILD / "fourbit_host.o"
+    gemv_o = BUILD / "fourbit_gemv.o"
+    steps = [
+        ["g++", *HOST_FLAGS, *inc, "-c", str(CSRC / "fourbit_host.cpp"), "-o", str(host_o)],
+        [_hipcc(), *HIP_FLAGS, *inc, "-c", str(CSRC / "fourbit_gemv.hip"), "-o", str(gemv_o)],
+    ]
+    tmp = LIB.with_suffix(".so.tmp")
+    steps.append([_hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", str(host_o), str(gemv_o),
+                  "-o", str(tmp), "-lpthread"])
+    for cmd in steps:
+        if verbose:
+            print(" ".join(cmd), flush=True)
+        _run(cmd)
+    os.replace(tmp, LIB)
+    return LIB
+
+
+if __name__ == "__main__":
+    print(build(verbose=True))

@@ -1,0 +1,382 @@
+// Host side of libfourbit.so: argument validation, deterministic packers (GF4 Jenks-16,
+// E2M1/E8M0), the offline FWHT weight rotation and the canonical <-> device weight
+// stream transform.  Built with -ffp-contract=off so every fp64 expression rounds
+// exactly as written (the packers must be bit-identical run to run and machine to
+// machine).
+#include "fourbit.h"
+#include "fourbit_layout.h"
+
+#include <algorithm>
+#include <atomic>
+#include <cmath>
+#include <cstring>
+#include <limits>
+#include <numeric>
+#include <thread>
+#include <vector>
+
+namespace {
+
+// ---------------------------------------------------------------------------------
+// fp32 -> fp16 (IEEE binary16) round-to-nearest-even, including subnormals.
+// ---------------------------------------------------------------------------------
+uint16_t f32_to_f16_rne(float f) {
+  uint32_t x;
+  std::memcpy(&x, &f, 4);
+  const uint32_t sign = (x >> 16) & 0x8000u;
+  const uint32_t ax = x & 0x7fffffffu;
+  if (ax >= 0x7f800000u) return (uint16_t)(sign | (ax > 0x7f800000u ? 0x7e00u : 0x7c00u));
+  if (ax >= 0x477ff000u) return (uint16_t)(sign | 0x7c00u);  // rounds to >= 65520 -> inf
+  if (ax < 0x38800000u) {                                    // |f| < 2^-14: subnormal half
+    // value = ax_float; half subnormal unit = 2^-24
+    const int e = (int)(ax >> 23);                           // biased fp32 exponent
+    if (e < 102) return (uint16_t)sign;                      // < 2^-25: rounds to 0
+    uint32_t mant = (ax & 0x7fffffu) | 0x800000u;            // 24-bit significand
+    const int shift = 126 - e;                               // to units of 2^-24
+    uint32_t q = mant >> shift;
+    const uint32_t rem = mant & ((1u << shift) - 1u);
+    const uint32_t half = 1u << (shift - 1);
+    if (rem > half || (rem == half && (q & 1u))) ++q;
+    return (uint16_t)(sign | q);
+  }
+  uint32_t h = ((ax >> 13) - (112u << 10));  // rebias 127 -> 15
+  const uint32_t rem = ax & 0x1fffu;
+  if (rem > 0x1000u || (rem == 0x1000u && (h & 1u))) ++h;
+  return (uint16_t)(sign | h);
+}
+
+float f16_bits_to_f32(uint16_t h) {
+  const uint32_t sign = (uint32_t)(h & 0x8000u) << 16;
+  const uint32_t e = (h >> 10) & 31u, m = h & 1023u;
+  float v;
+  if (e == 0) {
+    v = std::ldexp((float)m, -24);  // subnormal (or zero)
+  } else if (e == 31) {
+    v = m ? std::numeric_limits<float>::quiet_NaN() : std::numeric_limits<float>::infinity();
+  } else {
+    v = std::ldexp((float)(1024u + m), (int)e - 25);
+  }
+  uint32_t bits;
+  std::memcpy(&bits, &v, 4);
+  bits |= sign;
+  std::memcpy(&v, &bits, 4);
+  return v;
+}
+
+// Runs fn(begin, end) over [0, n) split across up to nthreads std::threads.
+template <class Fn>
+void parallel_for(int64_t n, int nthreads, Fn fn) {
+  if (n <= 0) return;
+  int nt = (int)std::min<int64_t>(std::max(1, nthreads), n);
+  if (nt == 1) {
+    fn((int64_t)0, n);
+    return;
+  }
+  std::vector<std::thread> th;
+  th.reserve(nt);
+  const int64_t chunk = (n + nt - 1) / nt;
+  for (int t = 0; t < nt; ++t) {
+    const int64_t b = t * chunk, e = std::min(n, b + chunk);
+    if (b >= e) break;
+    th.emplace_back([=] { fn(b, e); });
+  }
+  for (auto& x : th) x.join();
+}
+
+// ---------------------------------------------------------------------------------
+// GF4: Jenks natural breaks with 16 classes on one group of n values.
+// ---------------------------------------------------------------------------------
+struct JenksScratch {
+  std::vector<int> order;
+  std::vector<double> v, S1, S2, ssd, Dp, Dc;
+  std::vector<int> back;  // [k+1][n+1]
+  explicit JenksScratch(int n, int k)
+      : order(n), v(n), S1(n + 1), S2(n + 1), ssd((size_t)(n + 1) * (n + 1)), Dp(n + 1),
+        Dc(n + 1), back((size_t)(k + 1) * (n + 1)) {}
+};
+
+// Quantizes one group: vals[n] -> codes[n] (class index) and book[k] (fp16 bits).
+// Same arithmetic as the fp64 DP of the CPU oracle: sequential prefix sums,
+// SSD(i,j) = (S2[j]-S2[i]) - (S1[j]-S1[i])^2/(j-i), D[m][j] = min_i D[m-1][i] + SSD(i,j)
+// with the smallest i kept on ties (i ascends; only a strictly smaller candidate
+// replaces), centroid (S1[hi]-S1[lo])/(hi-lo) rounded fp64 -> fp32 -> fp16.
+void jenks_group(const float* vals, int n, int k, uint8_t* codes, uint16_t* book,
+                 JenksScratch& S) {
+  for (int t = 0; t < n; ++t) S.order[t] = t;
+  std::stable_sort(S.order.begin(), S.order.end(),
+                   [&](int a, int b) { return (double)vals[a] < (double)vals[b]; });
+  for (int t = 0; t < n; ++t) S.v[t] = (double)vals[S.order[t]];
+  S.S1[0] = 0.0;
+  S.S2[0] = 0.0;
+  for (int t = 0; t < n; ++t) {
+    S.S1[t + 1] = S.S1[t] + S.v[t];
+    S.S2[t + 1] = S.S2[t] + S.v[t] * S.v[t];
+  }
+  const int W = n + 1;
+  const double inf = std::numeric_limits<double>::infinity();
+  for (int i = 0; i <= n; ++i) {
+    double* row = &S.ssd[(size_t)i * W];
+    for (int j = 0; j <= i; ++j) row[j] = inf;
+    for (int j = i + 1; j <= n; ++j) {
+      const double s = S.S1[j] - S.S1[i];
+      const double q = S.S2[j] - S.S2[i];
+      row[j] = q - (s * s) / (double)(j - i);
+    }
+  }
+  // one class: [0, j)
+  for (int j = 0; j <= n; ++j) S.Dp[j] = S.ssd[j];
+  for (int m = 2; m <= k; ++m) {
+    int* bk = &S.back[(size_t)m * W];
+    for (int j = 0; j <= n; ++j) {
+      S.Dc[j] = inf;
+      bk[j] = 0;
+    }
+    for (int i = m - 1; i < n; ++i) {
+      const double d = S.Dp[i];
+      const double* row = &S.ssd[(size_t)i * W];
+      for (int j = i + 1; j <= n; ++j) {
+        const double c = d + row[j];
+        const bool better = c < S.Dc[j];
+        S.Dc[j] = better ? c : S.Dc[j];
+        bk[j] = better ? i : bk[j];
+      }
+    }
+    for (int j = 0; j < m; ++j) S.Dc[j] = inf;
+    std::swap(S.Dp, S.Dc);
+  }
+  int bounds[17];
+  bounds[0] = 0;
+  bounds[k] = n;
+  int j = n;
+  for (int m = k; m >= 2; --m) {
+    const int i = S.back[(size_t)m * W + j];
+    bounds[m - 1] = i;
+    j = i;
+  }
+  for (int c = 0; c < k; ++c) {
+    const int lo = bounds[c], hi = bounds[c + 1];
+    const double mean = (S.S1[hi] - S.S1[lo]) / (double)(hi - lo);
+    book[c] = f32_to_f16_rne((float)mean);
+    for (int p = lo; p < hi; ++p) codes[S.order[p]] = (uint8_t)c;
+  }
+}
+
+// ---------------------------------------------------------------------------------
+// E2M1 rounding: |q| onto {0,.5,1,1.5,2,3,4,6}, nearest, ties to even index, sat 6.
+// ---------------------------------------------------------------------------------
+uint8_t e2m1_index(double a) {
+  static const double mids[7] = {0.25, 0.75, 1.25, 1.75, 2.5, 3.5, 5.0};
+  int idx = 0;
+  bool tie = false;
+  for (int t = 0; t < 7; ++t) {
+    if (a > mids[t]) ++idx;
+    if (a == mids[t]) tie = true;
+  }
+  if (tie && (idx & 1)) ++idx;
+  return (uint8_t)std::min(idx, 7);
+}
+
+bool is_pow2(int v) { return v > 0 && (v & (v - 1)) == 0; }
+
+}  // namespace
+
+// ===================================================================================
+// C ABI
+// ===================================================================================
+extern "C" {
+
+int fb_abi_version(void) { return FB_ABI_VERSION; }
+
+const char* fb_strerror(int code) {
+  switch (code) {
+    case FB_OK: return "ok";
+    case FB_ERR_NULL: return "fourbit: required pointer is NULL";
+    case FB_ERR_SHAPE: return "fourbit: N, K or B out of range (need N>=1, K>=128, K%128==0, B>=1)";
+    case FB_ERR_GROUP: return "fourbit: group size must be 128 for GF4 and 32 for E2M1";
+    case FB_ERR_FORMAT: return "fourbit: unknown format";
+    case FB_ERR_DTYPE: return "fourbit: unsupported dtype (GF4 needs fp16 x; E2M1 fp16/bf16 x; y fp16/bf16/fp32)";
+    case FB_ERR_FWHT: return "fourbit: fwht_block must be 0 or a power of two >= 2 dividing K";
+    case FB_ERR_ALIGN: return "fourbit: device pointers must be 16-byte aligned";
+    case FB_ERR_WORKSPACE: return "fourbit: workspace smaller than fb_workspace_bytes()";
+    case FB_ERR_BATCH: return "fourbit: batch size not supported by this entry point";
+    case FB_ERR_VALUE: return "fourbit: non-finite weight";
+    case FB_ERR_HIP: return "fourbit: HIP runtime call failed";
+    case FB_ERR_THREADS: return "fourbit: nthreads must be >= 1";
+    case FB_ERR_LDS: return "fourbit: activation vector does not fit the kernel's LDS budget";
+    default: return "fourbit: unknown error";
+  }
+}
+
+int fb_validate(const fb_shape_t* s) {
+  if (!s) return FB_ERR_NULL;
+  if (s->fmt != FB_FMT_GF4 && s->fmt != FB_FMT_E2M1) return FB_ERR_FORMAT;
+  if (s->N < 1 || s->K < 128 || s->K % 128 != 0 || s->B < 1) return FB_ERR_SHAPE;
+  if (s->N > (1 << 26) || s->K > (1 << 24)) return FB_ERR_SHAPE;
+  if (s->fmt == FB_FMT_GF4 && s->group != 128) return FB_ERR_GROUP;
+  if (s->fmt == FB_FMT_E2M1 && s->group != 32) return FB_ERR_GROUP;
+  if (s->fwht_block != 0 && (!is_pow2(s->fwht_block) || s->fwht_block < 2 ||
+                             s->K % s->fwht_block != 0))
+    return FB_ERR_FWHT;
+  if (s->fmt == FB_FMT_GF4 && s->x_dtype != FB_DT_F16) return FB_ERR_DTYPE;
+  if (s->fmt == FB_FMT_E2M1 && s->x_dtype != FB_DT_F16 && s->x_dtype != FB_DT_BF16)
+    return FB_ERR_DTYPE;
+  if (s->y_dtype != FB_DT_F16 && s->y_dtype != FB_DT_BF16 && s->y_dtype != FB_DT_F32)
+    return FB_ERR_DTYPE;
+  return FB_OK;
+}
+
+size_t fb_device_bytes(const fb_shape_t* s) {
+  if (fb_validate(s) != FB_OK) return 0;
+  const int64_t items = (int64_t)s->N * (s->K / fb::kItemCodes);
+  const int64_t blocks = (items + fb::kBlockItems - 1) / fb::kBlockItems;
+  return (size_t)blocks * (size_t)fb::block_bytes(s->fmt);
+}
+
+int fb_quantize_gf4(const float* w, int32_t N, int32_t K, uint8_t* codes, uint16_t* codebook,
+                    int32_t nthreads) {
+  if (!w || !codes || !codebook) return FB_ERR_NULL;
+  if (N < 1 || K < 128 || K % 128) return FB_ERR_SHAPE;
+  if (nthreads < 1) return FB_ERR_THREADS;
+  const int64_t total = (int64_t)N * K;
+  for (int64_t t = 0; t < total; ++t)
+    if (!std::isfinite(w[t])) return FB_ERR_VALUE;
+  const int G = K / 128;
+  parallel_for((int64_t)N * G, nthreads, [&](int64_t b, int64_t e) {
+    JenksScratch S(128, 16);
+    uint8_t c[128];
+    for (int64_t it = b; it < e; ++it) {
+      const int64_t n = it / G, g = it % G;
+      jenks_group(w + n * K + g * 128, 128, 16, c, codebook + it * 16, S);
+      uint8_t* dst = codes + n * (K / 2) + g * 64;
+      for (int j = 0; j < 64; ++j) dst[j] = (uint8_t)(c[2 * j] | (c[2 * j + 1] << 4));
+    }
+  });
+  return FB_OK;
+}
+
+int fb_quantize_e2m1(const float* w, int32_t N, int32_t K, uint8_t* codes, uint8_t* scales,
+                     int32_t nthreads) {
+  if (!w || !codes || !scales) return FB_ERR_NULL;
+  if (N < 1 || K < 128 || K % 128) return FB_ERR_SHAPE;
+  if (nthreads < 1) return FB_ERR_THREADS;
+  const int64_t total = (int64_t)N * K;
+  for (int64_t t = 0; t < total; ++t)
+    if (!std::isfinite(w[t])) return FB_ERR_VALUE;
+  const int G = K / 32;
+  parallel_for((int64_t)N * G, nthreads, [&](int64_t b, int64_t e) {
+    for (int64_t it = b; it < e; ++it) {
+      const float* v = w + it * 32;  // rows are contiguous groups of 32
+      float amax = 0.0f;
+      for (int t = 0; t < 32; ++t) amax = std::max(amax, std::fabs(v[t]));
+      int ex = 0;
+      if (amax > 0.0f) {
+        int e2;
+        std::frexp((double)amax, &e2);  // amax = m * 2^e2, m in [0.5, 1)
+        ex = std::min(127, std::max(-127, e2 - 1 - 2));
+      }
+      scales[it] = (uint8_t)(ex + 127);
+      uint8_t c[32];
+      for (int t = 0; t < 32; ++t) {
+        const double q = std::ldexp((double)v[t], -ex);
+        const uint8_t idx = e2m1_index(std::fabs(q));
+        c[t] = (uint8_t)((std::signbit(v[t]) ? 8 : 0) | idx);
+      }
+      uint8_t* dst = codes + it * 16;
+      for (int j = 0; j < 16; ++j) dst[j] = (uint8_t)(c[2 * j] | (c[2 * j + 1] << 4));
+    }
+  });
+  return FB_OK;
+}
+
+int fb_fwht_rows_f32(float* w, int32_t N, int32_t K, int32_t block, int32_t nthreads) {
+  if (!w) return FB_ERR_NULL;
+  if (N < 1 || K < 1) return FB_ERR_SHAPE;
+  if (!is_pow2(block) || block < 2 || K % block) return FB_ERR_FWHT;
+  if (nthreads < 1) return FB_ERR_THREADS;
+  const double sc = 1.0 / std::sqrt((double)block);
+  parallel_for((int64_t)N, nthreads, [&](int64_t b, int64_t e) {
+    std::vector<double> t(block);
+    for (int64_t n = b; n < e; ++n) {
+      for (int k0 = 0; k0 < K; k0 += block) {
+        float* row = w + n * K + k0;
+        for (int u = 0; u < block; ++u) t[u] = (double)row[u];
+        for (int h = 1; h < block; h *= 2)
+          for (int p = 0; p < block; p += 2 * h)
+            for (int u = 0; u < h; ++u) {
+              const double x = t[p + u], y = t[p + h + u];
+              t[p + u] = x + y;
+              t[p + h + u] = x - y;
+            }
+        for (int u = 0; u < block; ++u) row[u] = (float)(t[u] * sc);
+      }
+    }
+  });
+  return FB_OK;
+}
+
+int fb_to_device(const uint8_t* codes, const void* meta, void* wdev, const fb_shape_t* s) {
+  if (!codes || !meta || !wdev) return FB_ERR_NULL;
+  const int st = fb_validate(s);
+  if (st != FB_OK) return st;
+  const int64_t ipr = s->K / fb::kItemCodes;
+  const int64_t items = (int64_t)s->N * ipr;
+  std::memset(wdev, 0, fb_device_bytes(s));
+  uint8_t* out = (uint8_t*)wdev;
+  for (int64_t i = 0; i < items; ++i) {
+    const int64_t n = i / ipr, g = i % ipr;
+    const uint8_t* crow = codes + n * (s->K / 2) + g * 64;  // 128 codes = 64 bytes
+    if (s->fmt == FB_FMT_GF4) {
+      const uint16_t* book = (const uint16_t*)meta + (n * ipr + g) * 16;
+      fb::gf4_encode_item(crow, book, out, i);
+    } else {
+      const uint8_t* sc = (const uint8_t*)meta + (n * ipr + g) * 4;
+      fb::e2m1_encode_item(crow, sc, out, i);
+    }
+  }
+  return FB_OK;
+}
+
+int fb_from_device(const void* wdev, uint8_t* codes, void* meta, const fb_shape_t* s) {
+  if (!codes || !meta || !wdev) return FB_ERR_NULL;
+  const int st = fb_validate(s);
+  if (st != FB_OK) return st;
+  const int64_t ipr = s->K / fb::kItemCodes;
+  const int64_t items = (int64_t)s->N * ipr;
+  const uint8_t* in = (const uint8_t*)wdev;
+  for (int64_t i = 0; i < items; ++i) {
+    const int64_t n = i / ipr, g = i % ipr;
+    uint8_t* crow = codes + n * (s->K / 2) + g * 64;
+    if (s->fmt == FB_FMT_GF4) {
+      uint16_t* book = (uint16_t*)meta + (n * ipr + g) * 16;
+      fb::gf4_decode_item(in, i, crow, book);
+    } else {
+      uint8_t* sc = (uint8_t*)meta + (n * ipr + g) * 4;
+      fb::e2m1_decode_item(in, i, crow, sc);
+    }
+  }
+  return FB_OK;
+}
+
+int fb_dequant_host(const uint8_t* codes, const void* meta, float* w_out, const fb_shape_t* s) {
+  if (!codes || !meta || !w_out) return FB_ERR_NULL;
+  const int st = fb_validate(s);
+  if (st != FB_OK) return st;
+  const int64_t N = s->N, K = s->K;
+  for (int64_t n = 0; n < N; ++n)
+    for (int64_t k = 0; k < K; ++k) {
+      const int c = (codes[n * (K / 2) + k / 2] >> ((k & 1) * 4)) & 15;
+      float v;
+      if (s->fmt == FB_FMT_GF4) {
+        const uint16_t h = ((const uint16_t*)meta)[(n * (K / 128) + k / 128) * 16 + c];
+        v = f16_bits_to_f32(h);
+      } else {
+        static const float grid[8] = {0.0f, 0.5f, 1.0f, 1.5f, 2.0f, 3.0f, 4.0f, 6.0f};
+        const int e = (int)((const uint8_t*)meta)[n * (K / 32) + k / 32] - 127;
+        v = std::ldexp((c & 8) ? -grid[c & 7] : grid[c & 7], e);
+      }
+      w_out[n * K + k] = v;
+    }
+  return FB_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,223 @@
+"""Drop-in quantized linear layer backed by the fused 4-bit dequant-GEMV.
+
+Mirrors the reference's ``QuantLinear`` (``Python_Jenks_Test/Jenks_Tests/
+Quantization_Experiments/layers.py:11-45``): same constructor
+``QuantLinear(linear_module, bitwidth=4, mask=None)``, ``forward(x)``, ``commit()`` and
+``hard_quant`` flag, and the ``quantize_module`` swap helper (``utils.py:1498-1524``).
+Where the reference keeps four dense fp32 ``[N,K]`` tensors (``s``, ``Q``, ``Theta``,
+``mask``) and dequantizes them on every call before ``F.linear`` (``layers.py:36-38``),
+this layer keeps the packed 4-bit weight (GF4 codebooks or E2M1 scales) and runs the
+HIP kernel, which decodes in registers.
+
+Extra keyword arguments: ``fmt`` ('gf4' | 'e2m1'), ``hadamard`` (False, True for the
+default block, or an explicit power-of-two block: the weight is rotated offline and x
+in-kernel) and ``nthreads`` for the host packer.
+"""
+from __future__ import annotations
+
+import copy
+
+import torch
+import torch.nn as nn
+
+from . import _capi as C
+
+LAYOUT_VERSION = 1
+MAX_GEMV_BATCH = 4
+
+
+def fwht_block_for(K: int) -> int:
+    """Default rotation block: 4096 when it divides K, else the largest power of two
+    dividing K (256 for K = 11008 = 43 * 256), capped at 4096."""
+    if K % 4096 == 0:
+        return 4096
+    b = K & -K
+    return min(b, 4096)
+
+
+class PackedWeight:
+    """Packed 4-bit weight: canonical host buffers + the device stream, and a GEMV."""
+
+    def __init__(self, fmt: str, N: int, K: int, codes: torch.Tensor, meta: torch.Tensor,
+                 fwht_block: int = 0, device=None):
+        self.fmt = C.FMT_BY_NAME[fmt]
+        self.fmt_name = fmt
+        self.N, self.K, self.fwht_block = N, K, fwht_block
+        self.codes, self.meta = codes, meta
+        shape = C.make_shape(N, K, 1, self.fmt, fwht_block)
+        self.wdev = C.to_device_layout(codes, meta, shape)
+        if device is not None:
+            self.wdev = self.wdev.to(device)
+
+    @classmethod
+    def quantize(cls, w: torch.Tensor, fmt: str = "gf4", fwht_block: int = 0, device=None,
+                 nthreads: int | None = None) -> "PackedWeight":
+        w = w.detach().float().cpu().contiguous()
+        N, K = w.shape
+        if fwht_block:
+            w = C.fwht_rows(w, fwht_block, nthreads)
+        if fmt == "gf4":
+            codes, meta = C.quantize_gf4(w, nthreads)
+        elif fmt == "e2m1":
+            codes, meta = C.quantize_e2m1(w, nthreads)
+        else:
+            raise ValueError(f"unknown fmt {fmt!r}")
+        return cls(fmt, N, K, codes, meta, fwht_block, device)
+
+    def shape(self, B: int, x_dtype: torch.dtype, y_dtype: torch.dtype) -> C.FbShape:
+        return C.make_shape(self.N, self.K, B, self.fmt, self.fwht_block,
+                            C.DTYPE_CODE[x_dtype], C.DTYPE_CODE[y_dtype])
+
+    def gemv(self, x: torch.Tensor, out: torch.Tensor | None = None,
+             out_dtype: torch.dtype | None = None) -> torch.Tensor:
+        """x [B,K] (B <= 4) on the GPU -> y [B,N]."""
+        B = x.shape[0]
+        ydt = out_dtype or x.dtype
+        if out is None:
+            out = torch.empty(B, self.N, dtype=ydt, device=x.device)
+        return C.gemv(self.wdev, x, out, self.shape(B, x.dtype, ydt))
+
+    def dequant_device(self, out_dtype=torch.float32) -> torch.Tensor:
+        return C.dequant_device(self.wdev, C.make_shape(self.N, self.K, 1, self.fmt), out_dtype)
+
+    def dequant_host(self) -> torch.Tensor:
+        return C.dequant_host(self.codes, self.meta, C.make_shape(self.N, self.K, 1, self.fmt))
+
+    def dequant_host_row(self, r: int):
+        """Exact fp32 decode of row r (numpy [K])."""
+        sh = C.make_shape(1, self.K, 1, self.fmt)
+        return C.dequant_host(self.codes[r:r + 1], self.meta[r:r + 1], sh)[0].numpy()
+
+    def algorithmic_bytes(self, B: int, xbytes: int = 2, ybytes: int = 2) -> int:
+        meta = self.N * (self.K // 128) * 32 if self.fmt == C.FMT_GF4 else self.N * (self.K // 32)
+        return self.N * self.K // 2 + meta + B * self.K * xbytes + B * self.N * ybytes
+
+
+class QuantLinear(nn.Linear):
+    """4-bit quantized ``nn.Linear`` (reference: ``layers.py:11-45``)."""
+
+    def __init__(self, linear_module: nn.Linear, bitwidth: int = 4, mask=None, *,
+                 fmt: str = "gf4", hadamard=False, nthreads: int | None = None):
+        super().__init__(linear_module.in_features, linear_module.out_features,
+                         bias=(linear_module.bias is not None))
+        if bitwidth != 4:
+            raise ValueError("QuantLinear packs 4-bit weights only (bitwidth=4)")
+        if fmt not in C.FMT_BY_NAME:
+            raise ValueError(f"fmt must be 'gf4' or 'e2m1', got {fmt!r}")
+        K = linear_module.in_features
+        if K % 128:
+            raise ValueError("in_features must be a multiple of 128")
+        self.weight.requires_grad = False
+        self.weight.data = linear_module.weight.data.clone()
+        if linear_module.bias is not None:
+            self.bias.data = linear_module.bias.data.clone()
+        self.fmt = fmt
+        self.fwht_block = (fwht_block_for(K) if hadamard is True else int(hadamard or 0))
+        self.nthreads = nthreads
+        self.register_buffer("mask", None if mask is None else torch.as_tensor(mask).float())
+        self.register_buffer("codes", torch.empty(0, dtype=torch.uint8))
+        self.register_buffer("meta", torch.empty(0, dtype=torch.uint8))
+        self.register_buffer("fb_header", torch.tensor(
+            [LAYOUT_VERSION, C.FMT_BY_NAME[fmt], C.GROUP_BY_FMT[C.FMT_BY_NAME[fmt]],
+             self.fwht_block], dtype=torch.int32))
+        self.register_buffer("wdev", torch.empty(0, dtype=torch.uint8), persistent=False)
+        self.hard_quant = False
+        self.register_load_state_dict_post_hook(QuantLinear._rebuild_after_load)
+        self.quantize()
+
+    # -- packing ------------------------------------------------------------------
+    def quantize(self) -> None:
+        """(Re)packs ``weight`` (times ``mask``) into 4-bit codes + codebooks/scales."""
+        w = self.weight.data.detach().float().cpu()
+        if self.mask is not None:
+            w = w * self.mask.float().cpu()
+        pw = PackedWeight.quantize(w, self.fmt, self.fwht_block, nthreads=self.nthreads)
+        dev = self.weight.device
+        self.codes = pw.codes.to(dev)
+        self.meta = pw.meta.to(dev)
+        self.wdev = pw.wdev.to(dev)
+
+    pack = quantize
+
+    def _shape(self, B=1, x_dtype=torch.float16, y_dtype=torch.float16) -> C.FbShape:
+        return C.make_shape(self.out_features, self.in_features, B, C.FMT_BY_NAME[self.fmt],
+                            self.fwht_block, C.DTYPE_CODE[x_dtype], C.DTYPE_CODE[y_dtype])
+
+    def _load_from_state_dict(self, state_dict, prefix, local_metadata, strict, missing_keys,
+                              unexpected_keys, error_msgs):
+        # packed buffers take the checkpoint's shape/dtype (format may differ from ctor)
+        for name in ("codes", "meta", "fb_header"):
+            key = prefix + name
+            if key in state_dict:
+                cur = getattr(self, name)
+                setattr(self, name, torch.empty_like(state_dict[key], device=cur.device))
+        super()._load_from_state_dict(state_dict, prefix, local_metadata, strict, missing_keys,
+                                      unexpected_keys, error_msgs)
+
+    def _rebuild_after_load(self, incompatible_keys) -> None:
+        hdr = self.fb_header.tolist()
+        if hdr[0] != LAYOUT_VERSION:
+            raise RuntimeError(f"packed layout version {hdr[0]} != {LAYOUT_VERSION}")
+        inv = {v: k for k, v in C.FMT_BY_NAME.items()}
+        self.fmt = inv[hdr[1]]
+        self.fwht_block = hdr[3]
+        shape = self._shape()
+        self.wdev = C.to_device_layout(self.codes.cpu(), self.meta.cpu(), shape).to(
+            self.codes.device)
+
+    # -- reference API ------------------------------------------------------------
+    def dequantized_weight(self) -> torch.Tensor:
+        """Exact fp32 decode of the packed weight (in the rotated basis when
+        ``fwht_block`` is set)."""
+        return C.dequant_host(self.codes.cpu(), self.meta.cpu(), self._shape())
+
+    def commit(self) -> None:
+        """Reference ``commit()`` (``layers.py:39-45``) stores the hard-rounded weight
+        in ``weight`` and sets ``hard_quant``; here the packed weight is already hard,
+        so ``weight`` receives its exact decode (rotated back when ``fwht_block``)."""
+        with torch.no_grad():
+            w = self.dequantized_weight()
+            if self.fwht_block:
+                w = C.fwht_rows(w, self.fwht_block)  # H is its own inverse
+            self.weight.data.copy_(w.to(self.weight.device))
+            self.hard_quant = True
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        if not x.is_cuda:
+            raise RuntimeError("QuantLinear.forward runs the HIP kernel: move the module and "
+                               "input to a ROCm GPU")
+        K, N = self.in_features, self.out_features
+        lead = x.shape[:-1]
+        x2 = x.reshape(-1, K)
+        if self.fmt == "gf4" or self.fwht_block:
+            xk = x2.to(torch.float16)
+        else:
+            xk = x2 if x2.dtype in (torch.float16, torch.bfloat16) else x2.to(torch.bfloat16)
+        xk = xk.contiguous()
+        ydt = x.dtype if x.dtype in C.DTYPE_CODE else torch.float32
+        y = torch.empty(x2.shape[0], N, dtype=ydt, device=x.device)
+        for b0 in range(0, x2.shape[0], MAX_GEMV_BATCH):
+            b1 = min(b0 + MAX_GEMV_BATCH, x2.shape[0])
+            C.gemv(self.wdev, xk[b0:b1], y[b0:b1], self._shape(b1 - b0, xk.dtype, ydt))
+        if self.bias is not None:
+            y = y + self.bias.to(ydt)
+        return y.reshape(*lead, N)
+
+    def extra_repr(self) -> str:
+        return (f"in_features={self.in_features}, out_features={self.out_features}, "
+                f"fmt={self.fmt}, fwht_block={self.fwht_block}, bias={self.bias is not None}")
+
+
+def quantize_module(module, bitwidth: int = 4, **kw):
+    """Recursively swaps every ``nn.Linear`` for a ``QuantLinear`` (reference:
+    ``Quantization_Experiments/utils.py:1498-1524``; masks come from existing zero
+    weights so pruning is preserved).  Other layers are left as they are."""
+    if isinstance(module, nn.Linear) and not isinstance(module, QuantLinear):
+        mask = (module.weight.data != 0).float()
+        return QuantLinear(module, bitwidth, mask=mask, **kw)
+    if isinstance(module, list):
+        return [quantize_module(m, bitwidth, **kw) for m in module]
+    module = copy.deepcopy(module)
+    for name, child in module.named_children():
+        setattr(module, name, quantize_module(child, bitwidth, **kw))
+    return module

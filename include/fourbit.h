@@ -1,0 +1,137 @@
+/*
+ * fourbit.h -- C ABI of libfourbit.so, the MI355X (gfx950) fused 4-bit dequant-GEMV.
+ *
+ * The reference (jvap2/If_I_could_turn_back_time) has no packed 4-bit path; its
+ * quantized linear layer dequantizes to fp32 and calls F.linear
+ * (Python_Jenks_Test/Jenks_Tests/Quantization_Experiments/layers.py:33-38), and its
+ * only native FFI is torch::Tensor-typed inline CUDA loaded with load_inline
+ * (Python_Jenks_Test/Jenks_Tests/cuda_helpers.py:42-62, 187-211, 293-299).  Each entry
+ * point below names the reference interface it replaces.
+ *
+ * Conventions
+ *  - Plain pointers and sizes only; no torch types.  The caller allocates every
+ *    buffer; the library never allocates device memory.
+ *  - Every function returns 0 (FB_OK) or a negative fb_status; fb_strerror() maps it
+ *    to text.  Argument validation runs on the host and needs no GPU.
+ *  - GPU entry points launch asynchronously on the given hipStream_t (passed as void*)
+ *    and never synchronise the device.
+ *  - Re-entrant: the only global state is a once-initialised device-property cache.
+ */
+#ifndef FOURBIT_H
+#define FOURBIT_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define FB_ABI_VERSION 1
+
+typedef enum {
+  FB_OK = 0,
+  FB_ERR_NULL = -1,          /* a required pointer is NULL                         */
+  FB_ERR_SHAPE = -2,         /* N, K or B out of range                             */
+  FB_ERR_GROUP = -3,         /* group size not supported for the format / K % group */
+  FB_ERR_FORMAT = -4,        /* unknown fmt                                        */
+  FB_ERR_DTYPE = -5,         /* unsupported x / y dtype for the format             */
+  FB_ERR_FWHT = -6,          /* fwht_block not a power of two dividing K           */
+  FB_ERR_ALIGN = -7,         /* pointer not 16-byte aligned                        */
+  FB_ERR_WORKSPACE = -8,     /* workspace too small                                */
+  FB_ERR_BATCH = -9,         /* batch size not supported by this entry point       */
+  FB_ERR_VALUE = -10,        /* non-finite input to a quantizer                    */
+  FB_ERR_HIP = -11,          /* a HIP runtime call failed                          */
+  FB_ERR_THREADS = -12,      /* nthreads < 1                                       */
+  FB_ERR_LDS = -13           /* activation does not fit the kernel's LDS budget    */
+} fb_status;
+
+typedef enum { FB_FMT_GF4 = 0, FB_FMT_E2M1 = 1 } fb_fmt;
+typedef enum { FB_DT_F16 = 0, FB_DT_BF16 = 1, FB_DT_F32 = 2 } fb_dtype;
+
+/* One quantized linear layer: y[B,N] = x[B,K] . W[N,K]^T. */
+typedef struct {
+  int32_t N;           /* out-features (rows of W)                                   */
+  int32_t K;           /* in-features (reduction dim); multiple of 128               */
+  int32_t B;           /* batch rows of x / y                                        */
+  int32_t group;       /* 128 for GF4, 32 for E2M1                                   */
+  int32_t fmt;         /* fb_fmt                                                     */
+  int32_t fwht_block;  /* 0 = no rotation, else power of two dividing K (x' = H x/sqrt(b)) */
+  int32_t x_dtype;     /* fb_dtype of x: GF4 needs F16; E2M1 takes F16 or BF16       */
+  int32_t y_dtype;     /* fb_dtype of y: F16, BF16 or F32                            */
+} fb_shape_t;
+
+int fb_abi_version(void);
+const char* fb_strerror(int code);
+
+/* Host-side checks of a shape (no GPU needed). */
+int fb_validate(const fb_shape_t* s);
+
+/* Bytes of the device weight stream (nibbles + codebooks/scales, padded to whole
+ * 64-item blocks) for fb_to_device / fb_gemv. */
+size_t fb_device_bytes(const fb_shape_t* s);
+
+/* Workspace bytes fb_gemv needs for this shape (0 when none). */
+size_t fb_workspace_bytes(const fb_shape_t* s);
+
+/* ---------------------------------------------------------------------------------
+ * Host packers.  They replace the reference's per-row fp32 quantizer state
+ * (layers.py:23-31, s/Q/Theta/mask as dense fp32 tensors) and its Jenks break search
+ * (cuda_helpers.py:151-211 + :378-395, k = 2, O(n^2) per array) with deterministic
+ * multithreaded packers.  Outputs are the canonical formats:
+ *   codes    uint8  [N, K/2]  element 2j in bits 3:0, element 2j+1 in bits 7:4
+ *   codebook uint16 [N, K/128, 16] fp16 bit patterns, non-decreasing   (GF4)
+ *   scales   uint8  [N, K/32]  E8M0, value 2^(s-127)                      (E2M1)
+ * ------------------------------------------------------------------------------- */
+
+/* GF4: per (row, 128-group) optimal 16-class 1-D partition (Fisher/Jenks DP over the
+ * stable-sorted group, fp64 prefix sums, ties to the smallest break), centroid =
+ * class mean rounded fp64->fp32->fp16.  Generalises Jenks_Optimization
+ * (cuda_helpers.py:151-184) from 2 to 16 classes. */
+int fb_quantize_gf4(const float* w, int32_t N, int32_t K, uint8_t* codes, uint16_t* codebook,
+                    int32_t nthreads);
+
+/* E2M1 + E8M0 per 32-group (OCP MX v1.0): e = floor(log2 amax) - 2, codes by RNE with
+ * saturation at +-6, amax = 0 -> scale byte 127.  Replaces the uniform grids of
+ * brecq.py:13-56 / utils.py:313-339 for this format. */
+int fb_quantize_e2m1(const float* w, int32_t N, int32_t K, uint8_t* codes, uint8_t* scales,
+                     int32_t nthreads);
+
+/* Offline weight rotation, in place: each K-block of each row becomes
+ * w H_b / sqrt(b) (fp64 butterflies, one rounding to fp32).  No reference counterpart. */
+int fb_fwht_rows_f32(float* w, int32_t N, int32_t K, int32_t block, int32_t nthreads);
+
+/* Canonical (codes + codebook|scales) -> device weight stream of fb_device_bytes(s)
+ * bytes (pure permutation / table transform, host memory), and its inverse. */
+int fb_to_device(const uint8_t* codes, const void* meta, void* wdev, const fb_shape_t* s);
+int fb_from_device(const void* wdev, uint8_t* codes, void* meta, const fb_shape_t* s);
+
+/* Host decode of canonical codes + codebook|scales to fp32 [N,K] (exact).  Produces
+ * the committed weight of QuantLinear.commit() (layers.py:39-45), which the reference
+ * stores as mask*s*round(Q+Theta) in fp32. */
+int fb_dequant_host(const uint8_t* codes, const void* meta, float* w_out, const fb_shape_t* s);
+
+/* ---------------------------------------------------------------------------------
+ * GPU entry points (hipStream_t passed as void*).
+ * ------------------------------------------------------------------------------- */
+
+/* Fused dequant-GEMV, batch 1..4: y = x' . W^T with x' = FWHT_b(x) when fwht_block.
+ * Replaces QuantLinear.forward's dequantize + F.linear pair (layers.py:33-38;
+ * brecq.py:323-329 new_forward) and the reference's native linear_kernel_batch
+ * (CUDA_C_Code/include/layers.h:9828-9839).  wdev is the fb_to_device stream in
+ * device memory; x is [B,K] of x_dtype, y is [B,N] of y_dtype.  ws may be NULL when
+ * fb_workspace_bytes(s) == 0. */
+int fb_gemv(const void* wdev, const void* x, void* y, const fb_shape_t* s, void* ws,
+            size_t ws_bytes, void* stream);
+
+/* Device decode of the whole weight: w_out [N,K] of out_dtype (F32 always exact; F16
+ * exact for GF4; BF16 exact for E2M1 within the bf16 normal range).  The same decode
+ * code as fb_gemv; used for bit-exact parity.  Replaces the dequantizer expression
+ * mask*s*(Q+Theta) (layers.py:36-37) / AdaRoundQuantizer.forward (brecq.py:81-92). */
+int fb_dequant(const void* wdev, void* w_out, int32_t out_dtype, const fb_shape_t* s,
+               void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* FOURBIT_H */

@@ -1,0 +1,310 @@
+"""CPU oracle for the fused 4-bit dequant-GEMV path.  TEST INFRASTRUCTURE ONLY.
+
+Only ``tests/``, ``__graft_entry__.smoke()`` and ``bench.py``'s ``cpu_baseline`` leg
+may import this module, and only as the checker (or, for the CPU baseline, as the
+thing timed on the host).  The product package never imports it: its packers are
+native C++ in ``libfourbit.so`` and its decode/GEMV runs in HIP kernels.
+
+This is a plain numpy / torch-CPU restatement of the path's arithmetic, written for
+clarity, not speed.  Every function states the reference code it follows or, where
+the reference has no counterpart (GF4, E2M1, FWHT and nibble packing do not exist in
+jvap2/If_I_could_turn_back_time), the published algorithm it restates.  How each
+function is pinned (closed forms, brute force, the reference's own known-answer
+test, scipy) is listed in its docstring and implemented in ``tests/test_oracle.py``.
+
+Canonical formats (build decisions, fixed by the golden fixtures under
+``tests/golden/``):
+
+* weights ``[N, K]`` (out x in), K contiguous;
+* canonical codes ``uint8 [N, K/2]``: byte ``j`` of a row holds element ``2j`` in
+  bits 3:0 and element ``2j+1`` in bits 7:4;
+* GF4 codebook ``uint16 [N, K/128, 16]`` (fp16 bit patterns, non-decreasing);
+* E2M1 scales ``uint8 [N, K/32]`` (E8M0: value ``2**(s-127)``).
+"""
+from __future__ import annotations
+
+import numpy as np
+import torch
+
+GF4_GROUP = 128
+E2M1_GROUP = 32
+GF4_LEVELS = 16
+
+# E2M1 magnitudes by 3-bit index (OCP Microscaling Formats v1.0, section 5.3.3).
+E2M1_GRID = np.array([0.0, 0.5, 1.0, 1.5, 2.0, 3.0, 4.0, 6.0], dtype=np.float64)
+
+
+# --------------------------------------------------------------------------------------
+# Jenks natural breaks with k classes (GF4 codebooks)
+# --------------------------------------------------------------------------------------
+def jenks_ssd_table(v_sorted: np.ndarray):
+    """Within-class sum of squared deviations for every class [i, j) of sorted rows.
+
+    ``v_sorted``: float64 ``[G, n]``.  Returns ``(ssd [G, n+1, n+1], S1 [G, n+1])``
+    with ``ssd[g, i, j] = (S2[j]-S2[i]) - (S1[j]-S1[i])**2 / (j-i)`` for ``i < j``
+    (+inf elsewhere), where S1/S2 are sequential fp64 prefix sums.
+
+    Follows the reference's Jenks cost (``cuda_helpers.py:151-184``: per split index,
+    left SSD + right SSD of a sorted array) generalised from 2 to k classes, written
+    with prefix sums (Fisher 1958).
+    """
+    G, n = v_sorted.shape
+    S1 = np.zeros((G, n + 1), np.float64)
+    S2 = np.zeros((G, n + 1), np.float64)
+    np.cumsum(v_sorted, axis=1, out=S1[:, 1:])  # sequential left-to-right accumulate
+    np.cumsum(v_sorted * v_sorted, axis=1, out=S2[:, 1:])
+    i = np.arange(n + 1)[:, None]
+    j = np.arange(n + 1)[None, :]
+    cnt = (j - i).astype(np.float64)
+    valid = j > i
+    cnt = np.where(valid, cnt, 1.0)
+    s = S1[:, None, :] - S1[:, :, None]          # [G, i, j] = S1[j] - S1[i]
+    q = S2[:, None, :] - S2[:, :, None]
+    ssd = q - (s * s) / cnt
+    ssd = np.where(valid[None], ssd, np.inf)
+    return ssd, S1
+
+
+def jenks_breaks(v_sorted: np.ndarray, k: int):
+    """Optimal k-class contiguous partition of each sorted row (Fisher/Jenks DP).
+
+    Returns ``(bounds [G, k+1] int64, cost [G] float64)``: class c covers sorted
+    positions ``[bounds[c], bounds[c+1])``; every class is non-empty.  Recurrence
+    ``D[m][j] = min_{m-1 <= i < j} D[m-1][i] + SSD(i, j)``; ties resolve to the
+    smallest break index ``i`` (``np.argmin`` returns the first minimum).  For
+    ``k = 2`` this is the reference's rule: argmin over split index of left-SSD +
+    right-SSD (``cuda_helpers.py:151-184`` kernel, argmin at ``:386-389``).
+    """
+    G, n = v_sorted.shape
+    if not 1 <= k <= n:
+        raise ValueError("need 1 <= k <= n")
+    ssd, _ = jenks_ssd_table(v_sorted)
+    D = ssd[:, 0, :].copy()                       # one class: [0, j)
+    back = np.zeros((k + 1, G, n + 1), np.int64)
+    for m in range(2, k + 1):
+        cand = D[:, :, None] + ssd                # [G, i, j]
+        idx = np.arange(n + 1)
+        cand[:, idx < m - 1, :] = np.inf          # first m-1 classes need >= m-1 points
+        arg = np.argmin(cand, axis=1)             # first minimum -> smallest i
+        Dn = np.take_along_axis(cand, arg[:, None, :], axis=1)[:, 0, :]
+        Dn[:, : m] = np.inf                       # m classes need j >= m
+        D = Dn
+        back[m] = arg
+    bounds = np.zeros((G, k + 1), np.int64)
+    bounds[:, k] = n
+    j = np.full(G, n, np.int64)
+    for m in range(k, 1, -1):
+        i = back[m, np.arange(G), j]
+        bounds[:, m - 1] = i
+        j = i
+    return bounds, D[:, n]
+
+
+def f64_to_f16_bits(x: np.ndarray) -> np.ndarray:
+    """fp64 -> fp32 -> fp16, each step round-to-nearest-even; returns uint16 bits."""
+    return np.asarray(x, np.float64).astype(np.float32).astype(np.float16).view(np.uint16)
+
+
+def gf4_quantize(w: np.ndarray, group: int = GF4_GROUP, k: int = GF4_LEVELS):
+    """GF4: per (row, group) Jenks-16 codebook + 4-bit codes.
+
+    ``w`` float32 ``[N, K]``.  Returns ``(codes uint8 [N, K] (unpacked), codebook
+    uint16 [N, K/group, 16])``.  Per group: stable sort (value, then index), the
+    k-class DP above, centroid = (S1[j]-S1[i])/(j-i) in fp64 rounded fp64->fp32->fp16,
+    code = class index in ascending order.
+    """
+    w = np.asarray(w, np.float32)
+    N, K = w.shape
+    if K % group:
+        raise ValueError("K must be a multiple of the group size")
+    G = K // group
+    vals = w.reshape(N * G, group).astype(np.float64)
+    if not np.isfinite(vals).all():
+        raise ValueError("weights must be finite")
+    order = np.argsort(vals, axis=1, kind="stable")
+    vs = np.take_along_axis(vals, order, axis=1)
+    codes = np.empty((N * G, group), np.uint8)
+    books = np.empty((N * G, k), np.uint16)
+    chunk = 512
+    for c0 in range(0, N * G, chunk):
+        sl = slice(c0, min(c0 + chunk, N * G))
+        bounds, _ = jenks_breaks(vs[sl], k)
+        S1 = np.zeros((vs[sl].shape[0], group + 1), np.float64)
+        np.cumsum(vs[sl], axis=1, out=S1[:, 1:])
+        lo, hi = bounds[:, :-1], bounds[:, 1:]
+        mean = (np.take_along_axis(S1, hi, 1) - np.take_along_axis(S1, lo, 1)) / (hi - lo)
+        books[sl] = f64_to_f16_bits(mean)
+        pos = np.arange(group)[None, :]
+        cls = (pos[:, :, None] >= bounds[:, None, 1:-1]).sum(-1)  # class of sorted position
+        cs = np.empty_like(cls)
+        np.put_along_axis(cs, order[sl], cls, axis=1)
+        codes[sl] = cs.astype(np.uint8)
+    return codes.reshape(N, K), books.reshape(N, G, k)
+
+
+def gf4_dequant(codes: np.ndarray, codebook: np.ndarray, group: int = GF4_GROUP) -> np.ndarray:
+    """w[n,k] = codebook[n, k/group, code[n,k]] as fp16 bits (uint16 [N, K])."""
+    N, K = codes.shape
+    g = np.arange(K) // group
+    return codebook[np.arange(N)[:, None], g[None, :], codes.astype(np.int64)]
+
+
+# --------------------------------------------------------------------------------------
+# E2M1 with E8M0 group scales (MXFP4-style)
+# --------------------------------------------------------------------------------------
+def e2m1_round_index(q: np.ndarray) -> np.ndarray:
+    """Round |q| (float64) onto E2M1_GRID: nearest, ties to the even index, saturating
+    at 6.  Returns the 3-bit magnitude index."""
+    a = np.abs(np.asarray(q, np.float64))
+    # midpoints between consecutive grid values
+    mids = (E2M1_GRID[:-1] + E2M1_GRID[1:]) / 2.0
+    idx = np.searchsorted(mids, a, side="left")        # a <= mid -> lower index
+    tie = np.isin(a, mids)
+    # at a tie searchsorted(left) gives the lower index; move to the even one
+    up = tie & (idx % 2 == 1)
+    idx = idx + up
+    return np.minimum(idx, 7).astype(np.uint8)
+
+
+def e8m0_exponent(amax: np.ndarray) -> np.ndarray:
+    """Shared exponent e = floor(log2 amax) - 2 (OCP MX v1.0 section 6.3), clamped to the
+    E8M0 range [-127, 127]; amax == 0 gives e = 0 (scale byte 127)."""
+    amax = np.asarray(amax, np.float64)
+    m, ex = np.frexp(amax)                  # amax = m * 2**ex, m in [0.5, 1)
+    e = ex.astype(np.int64) - 1 - 2
+    e = np.where(amax == 0, 0, e)
+    return np.clip(e, -127, 127)
+
+
+def e2m1_quantize(w: np.ndarray, group: int = E2M1_GROUP):
+    """Returns ``(codes uint8 [N, K] unpacked, scales uint8 [N, K/group])``.
+
+    code = sign<<3 | index(RNE(|w| / 2**e)), sign = signbit(w) (so -0.0 -> code 8).
+    """
+    w = np.asarray(w, np.float32)
+    N, K = w.shape
+    if K % group:
+        raise ValueError("K must be a multiple of the group size")
+    if not np.isfinite(w).all():
+        raise ValueError("weights must be finite")
+    G = K // group
+    wg = w.reshape(N, G, group).astype(np.float64)
+    e = e8m0_exponent(np.abs(wg).max(-1))
+    q = wg / np.exp2(e)[..., None]
+    idx = e2m1_round_index(q)
+    sign = np.signbit(wg).astype(np.uint8)
+    codes = (sign << 3) | idx
+    return codes.reshape(N, K).astype(np.uint8), (e + 127).astype(np.uint8)
+
+
+def e2m1_decode_code(codes: np.ndarray) -> np.ndarray:
+    """E2M1 code -> float32 value (code 8 is -0.0)."""
+    c = np.asarray(codes, np.int64)
+    mag = E2M1_GRID[c & 7]
+    return np.where(c & 8, -mag, mag).astype(np.float32)
+
+
+def e2m1_dequant(codes: np.ndarray, scales: np.ndarray, group: int = E2M1_GROUP) -> np.ndarray:
+    """w = E2M1(code) * 2**(scale-127), exact in float32 (float32 [N, K])."""
+    N, K = codes.shape
+    g = np.arange(K) // group
+    e = scales.astype(np.int64)[:, g] - 127
+    return np.ldexp(e2m1_decode_code(codes).astype(np.float64), e).astype(np.float32)
+
+
+# --------------------------------------------------------------------------------------
+# Nibble packing
+# --------------------------------------------------------------------------------------
+def pack_nibbles(codes: np.ndarray) -> np.ndarray:
+    """uint8 [N, K] codes (0..15) -> uint8 [N, K/2]; element 2j low nibble, 2j+1 high."""
+    c = np.asarray(codes, np.uint8)
+    if (c > 15).any():
+        raise ValueError("codes must be 4-bit")
+    return (c[:, 0::2] | (c[:, 1::2] << 4)).astype(np.uint8)
+
+
+def unpack_nibbles(packed: np.ndarray) -> np.ndarray:
+    p = np.asarray(packed, np.uint8)
+    out = np.empty((p.shape[0], p.shape[1] * 2), np.uint8)
+    out[:, 0::2] = p & 15
+    out[:, 1::2] = p >> 4
+    return out
+
+
+# --------------------------------------------------------------------------------------
+# Walsh-Hadamard transform (Sylvester order, normalised by 1/sqrt(b)), blockwise on rows
+# --------------------------------------------------------------------------------------
+def fwht_rows(a: np.ndarray, block: int) -> np.ndarray:
+    """Normalised blockwise FWHT along the last axis, computed in float64.
+
+    Iterative butterflies with stride h = 1, 2, 4, ..., block/2 (pair (u, u+h) ->
+    (u+h', ...) = (a+b, a-b)), then a multiply by 1/sqrt(block).  For a row-vector
+    block w this is ``w @ H_b / sqrt(b)`` (H symmetric), and for a column x it is
+    ``H_b x / sqrt(b)``.
+    """
+    a = np.asarray(a, np.float64)
+    K = a.shape[-1]
+    if block & (block - 1) or K % block:
+        raise ValueError("block must be a power of two dividing K")
+    lead = a.shape[:-1]
+    t = a.reshape(-1, K // block, block).copy()
+    h = 1
+    while h < block:
+        t = t.reshape(t.shape[0], t.shape[1], block // (2 * h), 2, h)
+        x, y = t[:, :, :, 0, :], t[:, :, :, 1, :]
+        t = np.stack([x + y, x - y], axis=3).reshape(t.shape[0], t.shape[1], block)
+        h *= 2
+    t = t * (1.0 / np.sqrt(block))
+    return t.reshape(*lead, K)
+
+
+def rotate_weights(w: np.ndarray, block: int) -> np.ndarray:
+    """Offline rotation W' = W @ H_b/sqrt(b) per K-block, fp64 then one RNE to fp32."""
+    return fwht_rows(np.asarray(w, np.float32), block).astype(np.float32)
+
+
+# --------------------------------------------------------------------------------------
+# Dequantize-then-matmul (the reference's forward structure)
+# --------------------------------------------------------------------------------------
+def dequant_f32(fmt: str, codes, meta) -> torch.Tensor:
+    """Dense fp32 [N, K] weight from unpacked codes + codebook/scales."""
+    if fmt == "gf4":
+        bits = gf4_dequant(codes, meta)
+        return torch.from_numpy(bits.view(np.float16).astype(np.float32))
+    if fmt == "e2m1":
+        return torch.from_numpy(e2m1_dequant(codes, meta))
+    raise ValueError(fmt)
+
+
+def rotate_x(x: torch.Tensor, block: int) -> torch.Tensor:
+    """x' = H x / sqrt(b) per block in fp64, returned as fp32."""
+    return torch.from_numpy(fwht_rows(x.double().numpy(), block).astype(np.float32))
+
+
+def y_ref(fmt: str, codes, meta, x: torch.Tensor, fwht_block: int = 0) -> torch.Tensor:
+    """``F.linear(x.float(), dequant(W))`` on the CPU in fp32 -- the structure of
+    ``Quantization_Experiments/layers.py:36-38`` (dequantize, then ``F.linear``) and
+    ``brecq.py:323-329``.  With ``fwht_block`` the activation is rotated first."""
+    W = dequant_f32(fmt, codes, meta)
+    xf = x.float()
+    if fwht_block:
+        xf = rotate_x(xf, fwht_block)
+    return torch.nn.functional.linear(xf, W)
+
+
+# --------------------------------------------------------------------------------------
+# The reference's own 4-bit format (QuantLinear.commit) as a GF4 codebook
+# --------------------------------------------------------------------------------------
+def quantlinear_commit_weight(w, theta, mask=None, bitwidth=4):
+    """Restates ``Quantization_Experiments/layers.py:23-26`` (per-row scale and floor)
+    and ``:39-45`` (commit): ``mask * s * round(Q + [sigmoid(Theta)*1.2-0.1 > 0.5])``
+    with ``s = amax_k|w| / (2**(b-1)-1) + 1e-12`` and ``Q = floor(w / s)``; fp32 torch
+    arithmetic as in the reference.  Returns (W_q, s, level) with level = Q_round."""
+    w = torch.as_tensor(w, dtype=torch.float32)
+    qmax = 2 ** (bitwidth - 1) - 1
+    s = w.abs().amax(dim=1, keepdim=True) / qmax + 1e-12
+    Q = torch.floor(w / s)
+    th = (torch.sigmoid(torch.as_tensor(theta, dtype=torch.float32)) * 1.2 - 0.1 > 0.5).float()
+    Qr = torch.round(Q + th)
+    m = torch.ones_like(w) if mask is None else torch.as_tensor(mask, dtype=torch.float32)
+    return m * s * Qr, s, Qr * (m != 0)

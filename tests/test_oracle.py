@@ -1,0 +1,260 @@
+"""Pins the CPU oracle (oracle/fourbit_oracle.py) without trusting its own formulas.
+
+Each test checks the oracle against something independent of it: brute force, the
+reference's own known-answer test (jenks_test.py), a direct restatement of the
+reference's k = 2 Jenks kernel, the OCP E2M1 code table, scipy's Hadamard matrix, or
+a mathematical invariant chosen so that a dropped term / wrong index fails it.
+"""
+import itertools
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import fourbit_oracle as O
+
+RNG = np.random.default_rng(1234)
+
+
+# ----------------------------------------------------------------------------- Jenks
+def _brute_partition(v, k):
+    n = len(v)
+    best = None
+    for br in itertools.combinations(range(1, n), k - 1):
+        b = (0,) + br + (n,)
+        c = sum(((v[b[t]:b[t + 1]] - v[b[t]:b[t + 1]].mean()) ** 2).sum() for t in range(k))
+        if best is None or c < best[0] - 1e-12:
+            best = (c, b)
+    return best
+
+
+@pytest.mark.parametrize("seed", range(6))
+def test_jenks_matches_brute_force(seed):
+    rng = np.random.default_rng(seed)
+    for _ in range(40):
+        n = int(rng.integers(2, 11))
+        k = int(rng.integers(1, min(n, 4) + 1))
+        v = np.sort(rng.normal(size=n) * rng.choice([1e-3, 1.0, 50.0]))
+        cost, b = _brute_partition(v, k)
+        bounds, c = O.jenks_breaks(v[None], k)
+        assert tuple(bounds[0]) == b
+        assert abs(c[0] - cost) <= 1e-9 * max(1.0, abs(cost))
+
+
+def _reference_k2_split(v):
+    """Direct restatement of the reference's Jenks_Optimization kernel rule
+    (cuda_helpers.py:151-184): for every split idx, mean/SSD of [0,idx) and [idx,n)
+    by explicit loops; Linear_Mask takes the first argmin (cuda_helpers.py:386-389)."""
+    n = len(v)
+    var = np.empty(n)
+    for idx in range(n):
+        m1 = v[:idx].sum() / idx if idx else 0.0
+        m2 = v[idx:].sum() / (n - idx)
+        var[idx] = ((v[:idx] - m1) ** 2).sum() + ((v[idx:] - m2) ** 2).sum()
+    return int(np.argmin(var)), var
+
+
+def test_jenks_k2_reduces_to_reference_rule():
+    for _ in range(30):
+        n = int(RNG.integers(3, 200))
+        v = np.sort(RNG.standard_t(3, size=n))
+        ref_split, var = _reference_k2_split(v)
+        bounds, cost = O.jenks_breaks(v[None], 2)
+        srt = np.sort(var)
+        if srt[1] - srt[0] < 1e-9 * srt[0]:
+            continue  # numerical near-tie between two splits: either answer is optimal
+        assert bounds[0, 1] == ref_split
+        assert np.isclose(cost[0], var.min(), rtol=1e-12)
+
+
+def test_jenks_test_known_answer():
+    """The reference's only known-answer test (jenks_test.py:4-60): 2-class Jenks labels
+    of |arr * arr_1| drive one masked momentum update compared with `goal` (atol 1e-4).
+
+    Finding: `goal` is not reachable by ANY threshold labelling of the score (the
+    elements that must have received the gradient are not the top or bottom of the
+    score order), so no 2-class natural-breaks split can satisfy it; the reference
+    test prints False.  What the file does pin is the 2-class split of its score
+    array, checked here against the reference kernel's own rule."""
+    arr = np.array([[0.4175, 0.2946, -0.2116, -0.2154], [0.3566, 0.4245, 0.2321, -0.4188],
+                    [-0.4813, 0.3807, -0.4328, -0.3908], [-0.0824, -0.0291, 0.1397, 0.0277],
+                    [-0.1358, -0.4866, 0.1868, -0.4537], [-0.0392, -0.2796, 0.2498, 0.3536],
+                    [-0.4195, -0.3004, 0.1421, 0.1625], [0.0492, -0.3681, -0.3715, -0.0706]])
+    arr_1 = np.repeat(np.array([-0.0615, 0.0, 0.0, 0.0277, 0.0, -0.0377, -0.0516, 0.0])[:, None],
+                      4, axis=1)
+    goal = np.array([[0.4137, 0.2919, -0.2091, -0.2129], [0.3534, 0.4207, 0.2301, -0.4151],
+                     [-0.4770, 0.3773, -0.4289, -0.3873], [-0.0819, -0.0291, 0.1382, 0.0271],
+                     [-0.1346, -0.4822, 0.1851, -0.4496], [-0.0385, -0.2767, 0.2475, 0.3504],
+                     [-0.4152, -0.2972, 0.1408, 0.1610], [0.0487, -0.3648, -0.3682, -0.0700]])
+    score = np.abs(arr * arr_1).reshape(-1)
+    order = np.argsort(score, kind="stable")
+    bounds, _ = O.jenks_breaks(score[order][None], 2)
+    ref_split, _ = _reference_k2_split(score[order])
+    assert bounds[0, 1] == ref_split == 22
+
+    def update(grad_mask):  # jenks_test.py:36-46 (velocity starts at zero)
+        p, g = arr.reshape(-1), arr_1.reshape(-1)
+        return (p - 0.01 * (0.9 * p + np.where(grad_mask, g, 0.0))).reshape(arr.shape)
+
+    reachable = [np.allclose(update(m), goal, atol=1e-4)
+                 for t in np.unique(score) for m in (score > t, score <= t)]
+    assert not any(reachable)
+    # the per-element best choice does fit, so the update formula itself is right
+    both = np.stack([update(np.zeros(32, bool)), update(np.ones(32, bool))])
+    assert np.abs(both - goal).min(0).max() < 1e-4
+
+
+def test_gf4_invariants():
+    w = (RNG.normal(size=(4, 512)) * 0.02).astype(np.float32)
+    w[0, :128] = 0.0                                  # all-zero group
+    w[1, :128] = RNG.choice([-0.5, 0.25, 1.0], 128)   # 3 distinct values
+    w[2, 128:256] = np.float32(0.125)                 # constant group
+    codes, book = O.gf4_quantize(w)
+    books = book.view(np.float16).astype(np.float64)
+    assert (np.diff(books, axis=-1) >= 0).all(), "codebook must be non-decreasing"
+    assert (codes < 16).all()
+    assert (book[0, 0] == 0).all()                    # zeros decode to exactly +0
+    deq = O.gf4_dequant(codes, book).view(np.float16).astype(np.float32)
+    assert np.array_equal(deq[1, :128], w[1, :128])   # few distinct values: lossless
+    assert np.array_equal(deq[2, 128:256], w[2, 128:256])
+    # optimality: each value is nearest (fp64) to the mean of its own class
+    for g in range(4):
+        v = w[3, g * 128:(g + 1) * 128].astype(np.float64)
+        c = codes[3, g * 128:(g + 1) * 128]
+        means = np.array([v[c == j].mean() for j in range(16)])
+        d = np.abs(v[:, None] - means[None, :])
+        assert (d[np.arange(128), c] <= d.min(1) + 1e-12).all()
+        # moving any break by one position does not lower the SSD
+        vs = np.sort(v)
+        bounds, cost = O.jenks_breaks(vs[None], 16)
+        for t in range(1, 16):
+            for dlt in (-1, 1):
+                b = bounds[0].copy()
+                b[t] += dlt
+                if b[t] <= b[t - 1] or b[t] >= b[t + 1]:
+                    continue
+                alt = sum(((vs[b[u]:b[u + 1]] - vs[b[u]:b[u + 1]].mean()) ** 2).sum()
+                          for u in range(16))
+                assert alt >= cost[0] - 1e-15
+
+
+def test_centroid_rounding_is_fp64_fp32_fp16():
+    # 1 + 2^-11 + 2^-40: fp64 -> fp16 directly rounds up, via fp32 it is a tie -> even
+    x = 1.0 + 2.0 ** -11 + 2.0 ** -40
+    assert O.f64_to_f16_bits(np.array([x]))[0] == np.float16(1.0).view(np.uint16)
+    assert np.array([x]).astype(np.float16).view(np.uint16)[0] != np.float16(1.0).view(np.uint16)
+
+
+# ----------------------------------------------------------------------------- E2M1
+def test_e2m1_code_table():
+    vals = O.e2m1_decode_code(np.arange(16))
+    exp = np.array([0, .5, 1, 1.5, 2, 3, 4, 6], np.float32)
+    assert np.array_equal(vals[:8], exp)
+    assert np.array_equal(vals[8:], -exp)
+    assert np.signbit(vals[8])
+
+
+def test_e2m1_rne_tie_table():
+    ties = {0.25: 0.0, 0.75: 1.0, 1.25: 1.0, 1.75: 2.0, 2.5: 2.0, 3.5: 4.0, 5.0: 4.0}
+    for a, want in ties.items():
+        idx = O.e2m1_round_index(np.array([a, -a]))
+        assert (O.E2M1_GRID[idx] == want).all(), a
+
+
+def test_e2m1_rounding_brute_force():
+    a = np.concatenate([np.linspace(0, 9, 200001), O.E2M1_GRID,
+                        (O.E2M1_GRID[:-1] + O.E2M1_GRID[1:]) / 2])
+    idx = O.e2m1_round_index(a)
+    # independent: nearest grid value, ties to the even index, saturating at 6
+    d = np.abs(a[:, None] - O.E2M1_GRID[None, :])
+    dmin = d.min(1, keepdims=True)
+    cand = np.where(d == dmin, np.arange(8)[None, :], 99)
+    even = np.where(cand % 2 == 0, cand, 99).min(1)
+    want = np.where((cand < 99).sum(1) > 1, even, cand.min(1))
+    assert np.array_equal(idx, want)
+
+
+def test_e2m1_scale_rule():
+    # amax exactly a power of two and just below: floor(log2) - 2
+    for amax, e in ((1.0, -2), (np.nextafter(np.float32(1), np.float32(0)), -3), (6.0, 0),
+                    (8.0, 1), (2.0 ** -130, -127), (0.0, 0)):
+        assert O.e8m0_exponent(np.array([amax]))[0] == e
+    w = np.zeros((1, 64), np.float32)
+    w[0, :32] = RNG.normal(size=32) * 0.02
+    codes, sc = O.e2m1_quantize(w)
+    assert sc[0, 1] == 127 and (codes[0, 32:] == 0).all()
+    # values on the grid times 2^e are reproduced exactly
+    g = np.concatenate([O.E2M1_GRID, -O.E2M1_GRID[1:]]).astype(np.float32)
+    w2 = np.resize(g, (2, 32)) * np.float32(2.0 ** -5)
+    c2, s2 = O.e2m1_quantize(w2)
+    assert np.array_equal(O.e2m1_dequant(c2, s2), w2)
+    # saturation: (6, 8) x 2^e clips to 6 x 2^e
+    w3 = np.full((1, 32), 7.5, np.float32)
+    w3[0, 0] = 7.9
+    c3, s3 = O.e2m1_quantize(w3)
+    assert s3[0, 0] == 127 and (O.e2m1_dequant(c3, s3) == 6.0).all()
+
+
+# ----------------------------------------------------------------------------- FWHT
+@pytest.mark.parametrize("b", [2, 16, 256, 4096])
+def test_fwht_matches_scipy(b):
+    from scipy.linalg import hadamard
+    H = hadamard(b).astype(np.float64) / np.sqrt(b)
+    x = RNG.normal(size=(3, 2 * b))
+    got = O.fwht_rows(x, b)
+    want = np.concatenate([x[:, :b] @ H, x[:, b:] @ H], axis=1)
+    assert np.allclose(got, want, atol=1e-12, rtol=1e-12)
+
+
+def test_fwht_invariants():
+    x = RNG.normal(size=(2, 11008))
+    y = O.fwht_rows(x, 256)
+    assert np.allclose(O.fwht_rows(y, 256), x, atol=1e-12)          # H.H = I
+    assert np.allclose((y ** 2).sum(1), (x ** 2).sum(1), rtol=1e-12)  # norm
+    w = RNG.normal(size=(5, 11008))
+    assert np.allclose(O.fwht_rows(w, 256) @ y[0], w @ x[0], rtol=1e-10)  # (WH)(Hx) = Wx
+    # blocks are independent: perturb one block only
+    x2 = x.copy()
+    x2[0, 256:512] += 1.0
+    d = O.fwht_rows(x2, 256) - y
+    assert np.abs(d[0, :256]).max() == 0 and np.abs(d[0, 512:]).max() == 0
+
+
+# ----------------------------------------------------------------------------- packing
+def test_nibble_pack_roundtrip_and_order():
+    c = RNG.integers(0, 16, size=(7, 256)).astype(np.uint8)
+    p = O.pack_nibbles(c)
+    assert np.array_equal(O.unpack_nibbles(p), c)
+    assert p[0, 0] == (c[0, 0] | (c[0, 1] << 4))
+    with pytest.raises(ValueError):
+        O.pack_nibbles(np.array([[16, 0]], np.uint8))
+
+
+# ----------------------------------------------------------------------------- y_ref
+def test_yref_special_cases():
+    w = (RNG.normal(size=(16, 256)) * 0.02).astype(np.float32)
+    codes, book = O.gf4_quantize(w)
+    W = O.dequant_f32("gf4", codes, book)
+    x = torch.zeros(1, 256)
+    x[0, 37] = 1.0
+    assert torch.equal(O.y_ref("gf4", codes, book, x)[0], W[:, 37])     # one-hot -> column
+    assert torch.equal(O.y_ref("gf4", codes, book, torch.zeros(2, 256)), torch.zeros(2, 16))
+    const = np.full_like(book, np.float16(0.5).view(np.uint16))
+    xr = torch.randn(1, 256)
+    assert torch.allclose(O.y_ref("gf4", codes, const, xr)[0], 0.5 * xr.sum().repeat(16), rtol=1e-5)
+    # the rotation path: rotating W offline and x online preserves W x
+    xr64 = torch.randn(1, 256, dtype=torch.float64)
+    wr = O.rotate_weights(w, 256)
+    assert np.allclose(wr.astype(np.float64) @ O.fwht_rows(xr64.numpy(), 256)[0],
+                       w.astype(np.float64) @ xr64.numpy()[0], rtol=1e-5, atol=1e-6)
+
+
+def test_quantlinear_commit_restatement():
+    """layers.py:23-26, 39-45: levels are in [-7, 8] and W_q = mask * s * level."""
+    w = torch.randn(8, 64) * 0.02
+    theta = torch.randn(8, 64)
+    mask = (torch.rand(8, 64) > 0.3).float()
+    Wq, s, lvl = O.quantlinear_commit_weight(w, theta, mask)
+    assert lvl.min() >= -7 and lvl.max() <= 8
+    assert torch.equal(Wq, mask * s * torch.round(torch.floor(w / s) +
+                                                  (torch.sigmoid(theta) * 1.2 - 0.1 > 0.5).float()))
