@@ -176,13 +176,28 @@ def _stream(dev: torch.device) -> int:
     return torch.cuda.current_stream(dev).cuda_stream
 
 
-def gemv(wdev: torch.Tensor, x: torch.Tensor, y: torch.Tensor, shape: FbShape) -> torch.Tensor:
+def workspace_bytes(shape: FbShape) -> int:
+    return lib().fb_workspace_bytes(ctypes.byref(shape))
+
+
+def new_workspace(shape: FbShape, device) -> torch.Tensor | None:
+    """Zero-filled device workspace for fb_gemv, or None when the shape needs none."""
+    need = workspace_bytes(shape)
+    return torch.zeros(need, dtype=torch.uint8, device=device) if need else None
+
+
+def gemv(wdev: torch.Tensor, x: torch.Tensor, y: torch.Tensor, shape: FbShape,
+         workspace: torch.Tensor | None = None) -> torch.Tensor:
     """y[B,N] = x'[B,K] . W^T on the GPU (asynchronous on the current stream)."""
     if not (wdev.is_cuda and x.is_cuda and y.is_cuda):
         raise RuntimeError("fb_gemv needs device tensors (ROCm GPU)")
     if not (x.is_contiguous() and y.is_contiguous()):
         raise ValueError("x and y must be contiguous")
-    check(lib().fb_gemv(_ptr(wdev), _ptr(x), _ptr(y), ctypes.byref(shape), None, 0,
+    need = workspace_bytes(shape)
+    if need and (workspace is None or workspace.numel() < need):
+        workspace = new_workspace(shape, x.device)
+    wp = _ptr(workspace) if need else None
+    check(lib().fb_gemv(_ptr(wdev), _ptr(x), _ptr(y), ctypes.byref(shape), wp, need,
                         _stream(x.device)))
     return y
 

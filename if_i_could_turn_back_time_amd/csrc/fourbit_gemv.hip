@@ -1,17 +1,25 @@
-// Fused 4-bit dequant-GEMV for gfx950 (MI355X), batch 1..4, and the device decoder.
+// Fused 4-bit dequant-GEMV for gfx950 (MI355X), batch 1..16, and the device decoder.
 //
-// One workgroup = 8 wave64s.  Each workgroup stages the activation x[B,K] in LDS
-// (optionally rotating it with a blockwise FWHT first), then every wave streams a
-// contiguous range of whole rows of the weight.  The weight is cut into items of 128
-// K-elements of one row (see fourbit_layout.h); lane l of a wave takes item
-// i0 + l + 64*s at step s, so each global_load_dwordx4 of the wave reads 1 KiB of
-// consecutive bytes.  A lane decodes its item in registers (GF4: two v_perm_b32
-// lookups per byte plane merged by XOR; E2M1: v_cvt_scalef32_pk_{bf16,f16}_fp4),
-// multiplies with v_dot2_f32_{f16,bf16} into fp32 partials, and the wave folds the
-// partials of each row with a DPP reduction.  Rows never straddle waves, so every
-// output is written once and results do not depend on scheduling.
+// Work unit = one (16-row tile, 512-element span) block of the device stream
+// (fourbit_layout.h).  Lane L of a wave loads the 96-byte (GF4) / 68-byte (E2M1) record
+// of row 16t + L%16, item 4sp + L/16, decodes it in registers -- GF4: two v_perm_b32
+// lookups per byte plane merged by XOR; E2M1: v_cvt_scalef32_pk_{bf16,f16}_fp4 -- into
+// exactly the A operand of v_mfma_f32_16x16x32_{f16,bf16}, and the matrix core does the
+// multiply-accumulate against x (B operand, one batch row per MFMA column, staged in
+// LDS).  The VALU only decodes; the cross-lane reduction is the MFMA itself; batch 1..16
+// costs the same VALU work.
+//
+// Partition: workgroup g (16 waves) owns the contiguous 16-row tiles [t0, t1); its waves
+// are split into TB = 16/WPT tile slots of WPT waves, and the WPT waves of a slot take
+// every WPT-th span of their tile.  When x does not fit LDS the K range is cut into S
+// slices that the workgroup stages one after the other.  Each wave keeps one tile's
+// partial MFMA accumulator in registers and parks it in LDS when done; after the last
+// slice the workgroup adds the WPT partials of each output in a fixed order.  No
+// workgroup talks to another, so there are no atomics or device-scope fences, and
+// results do not depend on scheduling.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <atomic>
 
 #include "fourbit.h"
@@ -19,46 +27,22 @@
 
 namespace {
 
-typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
-typedef __bf16 bf162_t __attribute__((ext_vector_type(2)));
+typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
+typedef __bf16 bf168_t __attribute__((ext_vector_type(8)));
 typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
 
-constexpr int kWaves = 8;
+constexpr int kWaves = 16;
 constexpr int kThreads = kWaves * 64;
 constexpr int kLdsLimit = 160 * 1024;
+constexpr int kSliceBytes = 272;  // 128 x 16-bit values + 16-byte pad (bank spread)
+constexpr int kDepth = 2;         // record buffers per wave (loads in flight + the one decoding)
 
 // ---------------------------------------------------------------------------------
 // small device helpers
 // ---------------------------------------------------------------------------------
 __device__ __forceinline__ unsigned perm(unsigned s0, unsigned s1, unsigned sel) {
   return __builtin_amdgcn_perm(s0, s1, sel);
-}
-
-__device__ __forceinline__ float dot2_f16(unsigned w, unsigned x, float acc) {
-  return __builtin_amdgcn_fdot2(__builtin_bit_cast(half2_t, w), __builtin_bit_cast(half2_t, x),
-                                acc, false);
-}
-
-__device__ __forceinline__ float dot2_bf16(unsigned w, unsigned x, float acc) {
-  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf162_t, w),
-                                         __builtin_bit_cast(bf162_t, x), acc, false);
-}
-
-template <int CTRL, int ROWMASK>
-__device__ __forceinline__ float dpp_f(float v) {
-  return __builtin_bit_cast(
-      float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, ROWMASK, 0xF, false));
-}
-
-// Sum over the 64 lanes; the result is returned uniformly.
-__device__ __forceinline__ float wave_sum(float v) {
-  v += dpp_f<0xB1, 0xF>(v);   // quad_perm [1,0,3,2]
-  v += dpp_f<0x4E, 0xF>(v);   // quad_perm [2,3,0,1]
-  v += dpp_f<0x141, 0xF>(v);  // row_half_mirror
-  v += dpp_f<0x140, 0xF>(v);  // row_mirror
-  v += dpp_f<0x142, 0xA>(v);  // row_bcast:15 into rows 1, 3
-  v += dpp_f<0x143, 0xC>(v);  // row_bcast:31 into rows 2, 3
-  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
 }
 
 __device__ __forceinline__ u32x4 ldg16(const uint8_t* p) {
@@ -75,13 +59,10 @@ __device__ __forceinline__ void store_y(void* y, int64_t idx, float v, int ydt) 
   }
 }
 
-// ---------------------------------------------------------------------------------
-// GF4 decode of one 32-bit word (8 codes, layout order) into 4 fp16 pairs in
-// element order (e0,e1) (e2,e3) (e4,e5) (e6,e7).
-// tl/th: lo/hi byte-plane tables {A'[0..3], A'[4..7], B'[0..3], B'[4..7]}.
-// ---------------------------------------------------------------------------------
-__device__ __forceinline__ void gf4_decode8(unsigned q, const u32x4& tl, const u32x4& th,
-                                            unsigned w[4]) {
+// GF4 decode of one 32-bit word (8 codes, layout order) into 4 fp16 pairs in element
+// order (e0,e1) (e2,e3) (e4,e5) (e6,e7).  tl/th: lo/hi byte-plane tables
+// {A'[0..3], A'[4..7], B'[0..3], B'[4..7]}.
+__device__ __forceinline__ u32x4 gf4_decode8(unsigned q, const u32x4& tl, const u32x4& th) {
   const unsigned sa = q & 0x0F0F0F0Fu;
   const unsigned sb = (q >> 4) & 0x0F0F0F0Fu;
   const unsigned sa8 = sa ^ 0x08080808u;
@@ -90,128 +71,145 @@ __device__ __forceinline__ void gf4_decode8(unsigned q, const u32x4& tl, const u
   const unsigned hiA = perm(th.y, th.x, sa) ^ perm(th.w, th.z, sa8);
   const unsigned loB = perm(tl.y, tl.x, sb) ^ perm(tl.w, tl.z, sb8);
   const unsigned hiB = perm(th.y, th.x, sb) ^ perm(th.w, th.z, sb8);
-  w[0] = perm(hiA, loA, 0x05010400u);
-  w[1] = perm(hiA, loA, 0x07030602u);
-  w[2] = perm(hiB, loB, 0x05010400u);
-  w[3] = perm(hiB, loB, 0x07030602u);
+  u32x4 w;
+  w.x = perm(hiA, loA, 0x05010400u);
+  w.y = perm(hiA, loA, 0x07030602u);
+  w.z = perm(hiB, loB, 0x05010400u);
+  w.w = perm(hiB, loB, 0x07030602u);
+  return w;
 }
 
-// E2M1 decode of byte j of q (elements 2j, 2j+1) into a 16-bit pair, unscaled.
-template <int XDT, int J>
-__device__ __forceinline__ unsigned e2m1_decode2(unsigned q) {
+
+// Two independent 8-code decodes written stage by stage, so the scheduler sees twice the
+// instruction-level parallelism of one decode chain.
+__device__ __forceinline__ void gf4_decode16(unsigned q0, unsigned q1, const u32x4& tl,
+                                             const u32x4& th, u32x4& w0, u32x4& w1) {
+  const unsigned sa0 = q0 & 0x0F0F0F0Fu, sa1 = q1 & 0x0F0F0F0Fu;
+  const unsigned t0 = q0 >> 4, t1 = q1 >> 4;
+  const unsigned sa80 = sa0 ^ 0x08080808u, sa81 = sa1 ^ 0x08080808u;
+  const unsigned sb0 = t0 & 0x0F0F0F0Fu, sb1 = t1 & 0x0F0F0F0Fu;
+  const unsigned sb80 = sb0 ^ 0x08080808u, sb81 = sb1 ^ 0x08080808u;
+  const unsigned la0 = perm(tl.y, tl.x, sa0), la1 = perm(tl.y, tl.x, sa1);
+  const unsigned lb0 = perm(tl.w, tl.z, sa80), lb1 = perm(tl.w, tl.z, sa81);
+  const unsigned ha0 = perm(th.y, th.x, sa0), ha1 = perm(th.y, th.x, sa1);
+  const unsigned hb0 = perm(th.w, th.z, sa80), hb1 = perm(th.w, th.z, sa81);
+  const unsigned loA0 = la0 ^ lb0, loA1 = la1 ^ lb1, hiA0 = ha0 ^ hb0, hiA1 = ha1 ^ hb1;
+  const unsigned lc0 = perm(tl.y, tl.x, sb0), lc1 = perm(tl.y, tl.x, sb1);
+  const unsigned ld0 = perm(tl.w, tl.z, sb80), ld1 = perm(tl.w, tl.z, sb81);
+  const unsigned hc0 = perm(th.y, th.x, sb0), hc1 = perm(th.y, th.x, sb1);
+  const unsigned hd0 = perm(th.w, th.z, sb80), hd1 = perm(th.w, th.z, sb81);
+  w0.x = perm(hiA0, loA0, 0x05010400u); w1.x = perm(hiA1, loA1, 0x05010400u);
+  w0.y = perm(hiA0, loA0, 0x07030602u); w1.y = perm(hiA1, loA1, 0x07030602u);
+  const unsigned loB0 = lc0 ^ ld0, loB1 = lc1 ^ ld1, hiB0 = hc0 ^ hd0, hiB1 = hc1 ^ hd1;
+  w0.z = perm(hiB0, loB0, 0x05010400u); w1.z = perm(hiB1, loB1, 0x05010400u);
+  w0.w = perm(hiB0, loB0, 0x07030602u); w1.w = perm(hiB1, loB1, 0x07030602u);
+}
+// E2M1 decode of one 32-bit word (8 codes, canonical order) times `scale`.
+template <int XDT>
+__device__ __forceinline__ u32x4 e2m1_decode8(unsigned q, float scale) {
+  u32x4 w;
   if constexpr (XDT == FB_DT_BF16) {
-    return __builtin_bit_cast(unsigned, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(q, 1.0f, J));
+    w.x = __builtin_bit_cast(unsigned, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(q, scale, 0));
+    w.y = __builtin_bit_cast(unsigned, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(q, scale, 1));
+    w.z = __builtin_bit_cast(unsigned, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(q, scale, 2));
+    w.w = __builtin_bit_cast(unsigned, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(q, scale, 3));
   } else {
-    return __builtin_bit_cast(unsigned, __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(q, 1.0f, J));
+    w.x = __builtin_bit_cast(unsigned, __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(q, scale, 0));
+    w.y = __builtin_bit_cast(unsigned, __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(q, scale, 1));
+    w.z = __builtin_bit_cast(unsigned, __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(q, scale, 2));
+    w.w = __builtin_bit_cast(unsigned, __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(q, scale, 3));
+  }
+  return w;
+}
+
+template <int XDT>
+__device__ __forceinline__ f32x4 mfma(const u32x4& a, const u32x4& b, const f32x4& c) {
+  if constexpr (XDT == FB_DT_BF16) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf168_t, a),
+                                                   __builtin_bit_cast(bf168_t, b), c, 0, 0, 0);
+  } else {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8_t, a),
+                                                  __builtin_bit_cast(half8_t, b), c, 0, 0, 0);
   }
 }
 
-// ---------------------------------------------------------------------------------
-// Per-item records
-// ---------------------------------------------------------------------------------
+// One lane's record of a work unit.
 template <int FMT>
 struct Rec {
   u32x4 nib[4];
   u32x4 t0, t1;  // GF4: lo / hi tables.  E2M1: t0.x holds the 4 scale bytes.
 };
 
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+constexpr int kRsrcWord3 = 0x00020000;  // raw (untyped) buffer, gfx9 family
+constexpr int kNT = 2;                  // streaming (non-temporal) cache policy
+
+// Loads one lane's record of the block at byte offset `boff` of the weight stream.
+// With a zero-sized resource the loads are out of range: they return zeros and move no
+// data, which is how the pipeline issues its loads unconditionally past the last unit.
 template <int FMT>
-__device__ __forceinline__ void load_rec(const uint8_t* __restrict__ w, int item, Rec<FMT>& r) {
-  constexpr int BB = FMT == FB_FMT_GF4 ? fb::kGf4BlockBytes : fb::kE2m1BlockBytes;
-  const uint8_t* base = w + (int64_t)(item >> 6) * BB + (item & 63) * 16;
+__device__ __forceinline__ void load_rec(rsrc_t rs, unsigned boff, int lane, Rec<FMT>& r) {
+  const int vo = lane * 16;
+#pragma unroll
+  for (int c = 0; c < 4; ++c)
+    r.nib[c] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                             rs, vo + c * 1024, (int)boff, kNT));
+  if constexpr (FMT == FB_FMT_GF4) {
+    r.t0 = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, vo, (int)boff + 4096, kNT));
+    r.t1 = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, vo, (int)boff + 5120, kNT));
+  } else {
+    r.t0.x = __builtin_amdgcn_raw_buffer_load_b32(rs, lane * 4, (int)boff + 4096, kNT);
+  }
+}
+
+// Record read for the device decoder (plain global loads).
+template <int FMT>
+__device__ __forceinline__ void load_rec_global(const uint8_t* __restrict__ blk, int lane,
+                                                Rec<FMT>& r) {
+  const uint8_t* base = blk + lane * 16;
 #pragma unroll
   for (int c = 0; c < 4; ++c) r.nib[c] = ldg16(base + c * 1024);
   if constexpr (FMT == FB_FMT_GF4) {
     r.t0 = ldg16(base + 4096);
     r.t1 = ldg16(base + 5120);
   } else {
-    const uint8_t* sp = w + (int64_t)(item >> 6) * BB + 4096 + (item & 63) * 4;
-    r.t0.x = __builtin_nontemporal_load(reinterpret_cast<const unsigned*>(sp));
-  }
-}
-
-// Partial dot products of one item with the staged activation slice.
-// xs: LDS slice base (batch b at xs + b*256 bytes, 128 x 16-bit values each).
-template <int FMT, int B, int XDT>
-__device__ __forceinline__ void item_dot(const Rec<FMT>& r, const uint8_t* xs, float acc[B]) {
-  if constexpr (FMT == FB_FMT_GF4) {
-#pragma unroll
-    for (int c = 0; c < 4; ++c) {
-#pragma unroll
-      for (int d = 0; d < 4; ++d) {
-        unsigned w[4];
-        gf4_decode8(r.nib[c][d], r.t0, r.t1, w);
-#pragma unroll
-        for (int b = 0; b < B; ++b) {
-          const u32x4 xv = *reinterpret_cast<const u32x4*>(xs + b * 256 + (c * 32 + d * 8) * 2);
-          acc[b] = dot2_f16(w[0], xv.x, acc[b]);
-          acc[b] = dot2_f16(w[1], xv.y, acc[b]);
-          acc[b] = dot2_f16(w[2], xv.z, acc[b]);
-          acc[b] = dot2_f16(w[3], xv.w, acc[b]);
-        }
-      }
-    }
-  } else {
-#pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      float part[B];
-#pragma unroll
-      for (int b = 0; b < B; ++b) part[b] = 0.0f;
-#pragma unroll
-      for (int d = 0; d < 4; ++d) {
-        const unsigned q = r.nib[c][d];
-        const unsigned w0 = e2m1_decode2<XDT, 0>(q);
-        const unsigned w1 = e2m1_decode2<XDT, 1>(q);
-        const unsigned w2 = e2m1_decode2<XDT, 2>(q);
-        const unsigned w3 = e2m1_decode2<XDT, 3>(q);
-#pragma unroll
-        for (int b = 0; b < B; ++b) {
-          const u32x4 xv = *reinterpret_cast<const u32x4*>(xs + b * 256 + (c * 32 + d * 8) * 2);
-          if constexpr (XDT == FB_DT_BF16) {
-            part[b] = dot2_bf16(w0, xv.x, part[b]);
-            part[b] = dot2_bf16(w1, xv.y, part[b]);
-            part[b] = dot2_bf16(w2, xv.z, part[b]);
-            part[b] = dot2_bf16(w3, xv.w, part[b]);
-          } else {
-            part[b] = dot2_f16(w0, xv.x, part[b]);
-            part[b] = dot2_f16(w1, xv.y, part[b]);
-            part[b] = dot2_f16(w2, xv.z, part[b]);
-            part[b] = dot2_f16(w3, xv.w, part[b]);
-          }
-        }
-      }
-      const int e = (int)((r.t0.x >> (8 * c)) & 0xFFu) - 127;
-#pragma unroll
-      for (int b = 0; b < B; ++b) acc[b] += __builtin_ldexpf(part[b], e);
-    }
+    r.t0.x = __builtin_nontemporal_load(reinterpret_cast<const unsigned*>(blk + 4096 + lane * 4));
   }
 }
 
 // ---------------------------------------------------------------------------------
-// Activation staging.  Slice g (128 values) of batch row b lives at
-// g*(B*256+16) + b*256 bytes: the 16-byte pad per slice spreads lanes that read
-// neighbouring slices over all LDS banks.
+// Activation staging.  The slice [k0, k0 + 512*SPL) of each batch row b is stored as
+// 128-value groups of kSliceBytes: byte offset b*RS + (k/128)*272 + (k%128)*2.  Values
+// at k >= K are zero (the device stream is zero there too).
 // ---------------------------------------------------------------------------------
-template <int B>
-__device__ __forceinline__ void stage_plain(uint8_t* lds, const uint16_t* __restrict__ x, int K) {
-  const int ss = B * 256 + 16;
-  const int per_row = K >> 3;  // 16-byte chunks per batch row
+__host__ __device__ inline int x_row_stride(int nsl) {
+  int rs = nsl * kSliceBytes;
+  if (((rs >> 4) & 1) == 0) rs += 16;  // odd number of 16-byte units: batch rows spread
+  return rs;
+}
+
+__device__ void stage_plain(uint8_t* lds, const uint16_t* __restrict__ x, int K, int B, int k0,
+                            int nsl, int RS) {
+  const int per_row = nsl * 16;  // 16-byte chunks per batch row
   for (int t = threadIdx.x; t < B * per_row; t += kThreads) {
     const int b = t / per_row;
-    const int k8 = (t - b * per_row) << 3;
-    const u32x4 v = *reinterpret_cast<const u32x4*>(x + (int64_t)b * K + k8);
-    *reinterpret_cast<u32x4*>(lds + (k8 >> 7) * ss + b * 256 + (k8 & 127) * 2) = v;
+    const int c8 = t - b * per_row;
+    const int k = k0 + c8 * 8;
+    u32x4 v = {0u, 0u, 0u, 0u};
+    if (k < K) v = *reinterpret_cast<const u32x4*>(x + (int64_t)b * K + k);
+    *reinterpret_cast<u32x4*>(lds + b * RS + (c8 >> 4) * kSliceBytes + (c8 & 15) * 16) = v;
   }
 }
 
-// Blockwise normalised FWHT of x (fp16) in fp32, result rounded to fp16 into the
-// slices.  F (B*K floats) is LDS scratch.  Stages are done 4 at a time: a thread owns
-// 16 values spaced h0 apart and applies strides h0, 2h0, 4h0, 8h0 in registers.
-template <int B>
-__device__ __forceinline__ void stage_fwht(uint8_t* lds, float* F, const _Float16* __restrict__ x,
-                                           int K, int fb) {
-  const int ss = B * 256 + 16;
-  for (int t = threadIdx.x; t < B * K; t += kThreads) F[t] = (float)x[t];
+// Blockwise normalised FWHT (fp32 butterflies) of x[b, k0 : k0+kw] into the staged
+// layout (rounded to fp16).  F: LDS scratch of B*kw floats; kw is a whole number of
+// blocks.  Stages go 4 at a time: a thread owns 16 values spaced h0 apart.
+__device__ void stage_fwht(uint8_t* lds, float* F, const _Float16* __restrict__ x, int K, int B,
+                           int k0, int kw, int nsl, int RS, int fb) {
+  for (int t = threadIdx.x; t < B * kw; t += kThreads) {
+    const int b = t / kw;
+    F[t] = (float)x[(int64_t)b * K + k0 + (t - b * kw)];
+  }
   __syncthreads();
   const int lg_fb = 31 - __builtin_clz(fb);
   for (int lg_h0 = 0; lg_h0 < lg_fb; lg_h0 += 4) {
@@ -219,7 +217,7 @@ __device__ __forceinline__ void stage_fwht(uint8_t* lds, float* F, const _Float1
     const int span = 1 << lg_span;
     const int h0 = 1 << lg_h0;
     const int lg_nhi = lg_fb - lg_h0 - lg_span;
-    const int ngroups = (B * K) >> lg_span;
+    const int ngroups = (B * kw) >> lg_span;
     for (int t = threadIdx.x; t < ngroups; t += kThreads) {
       const int lo = t & (h0 - 1);
       const int rest = t >> lg_h0;
@@ -249,154 +247,192 @@ __device__ __forceinline__ void stage_fwht(uint8_t* lds, float* F, const _Float1
     __syncthreads();
   }
   const float sc = 1.0f / __builtin_sqrtf((float)fb);
-  for (int t = threadIdx.x; t < B * K; t += kThreads) {
-    const int b = t / K;
-    const int k = t - b * K;
-    *reinterpret_cast<_Float16*>(lds + (k >> 7) * ss + b * 256 + (k & 127) * 2) =
-        (_Float16)(F[t] * sc);
+  const int width = nsl * 128;
+  for (int t = threadIdx.x; t < B * width; t += kThreads) {
+    const int b = t / width;
+    const int k = t - b * width;
+    const float v = k < kw ? F[b * kw + k] * sc : 0.0f;
+    *reinterpret_cast<_Float16*>(lds + b * RS + (k >> 7) * kSliceBytes + (k & 127) * 2) =
+        (_Float16)v;
   }
+}
+
+__host__ __device__ inline int x_lds_bytes(int B, int K, int SPL, int fwht_block) {
+  int b = B * x_row_stride(SPL * 4);
+  if (fwht_block) b += B * min(K, SPL * 512) * 4;
+  return (b + 15) & ~15;
 }
 
 // ---------------------------------------------------------------------------------
 // The GEMV kernel
 // ---------------------------------------------------------------------------------
-template <int FMT, int B, int XDT>
+template <int FMT, int XDT>
 __global__ __launch_bounds__(kThreads) void gemv_kernel(const uint8_t* __restrict__ w,
                                                         const void* __restrict__ x,
-                                                        void* __restrict__ y, int N, int K,
-                                                        int fwht_block, int rows_per_wave,
+                                                        void* __restrict__ y, int N, int K, int B,
+                                                        int S, int SPL, int WPT, int fwht_block,
                                                         int ydt) {
   extern __shared__ __align__(16) uint8_t lds[];
-  const int ipr = K >> 7;
-  const int ss = B * 256 + 16;
-  if (fwht_block) {
-    stage_fwht<B>(lds, reinterpret_cast<float*>(lds + ipr * ss),
-                  static_cast<const _Float16*>(x), K, fwht_block);
-  } else {
-    stage_plain<B>(lds, static_cast<const uint16_t*>(x), K);
-  }
-  __syncthreads();
+  constexpr int BB = FMT == FB_FMT_GF4 ? fb::kGf4BlockBytes : fb::kE2m1BlockBytes;
+  const int GS = ((K >> 7) + 3) >> 2;  // spans per row
+  const int T = (N + 15) >> 4;          // row tiles
+  const int t0 = (int)((int64_t)blockIdx.x * T / gridDim.x);
+  const int t1 = (int)((int64_t)(blockIdx.x + 1) * T / gridDim.x);
+  const int TB = kWaves / WPT;
+  const int nsl = SPL * 4;
+  const int RS = x_row_stride(nsl);
+  f32x4* slots = reinterpret_cast<f32x4*>(lds + x_lds_bytes(B, K, SPL, fwht_block));
 
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform: SGPR math
   const int lane = threadIdx.x & 63;
-  const int wave = blockIdx.x * kWaves + (threadIdx.x >> 6);
-  const int r0 = wave * rows_per_wave;
-  const int r1 = min(N, r0 + rows_per_wave);
-  if (r0 >= r1) return;
-  const int i_begin = r0 * ipr;
-  const int i_end = r1 * ipr;
+  const int ts = wave / WPT;            // tile slot
+  const int ph = wave - ts * WPT;       // span phase
+  const int col = lane & 15;            // batch column / row within tile
+  const int q = lane >> 4;              // K-quarter of the span / output row group
+  const int xb = col < B ? col : 0;     // columns >= B duplicate column 0 (unused)
+  const int nj = (SPL - ph + WPT - 1) / WPT;  // spans of a tile this wave takes (WPT <= SPL)
+  const int tw0 = t0 + ts;
+  const int nbw = tw0 < t1 ? (t1 - 1 - tw0) / TB + 1 : 0;  // batches with a tile for us
+  const int nunits = nbw * nj;
 
-  // lane position (row, slice) of item i_begin + lane, advanced by 64 per step
-  int row = r0 + lane / ipr;
-  int slice = lane - (lane / ipr) * ipr;
-  // wave position of the step's first item
-  int rlo = r0;
-  int sb_slice = 0;
+  // byte offset of the block of unit v (slice s) in the weight stream
+  auto unit_off = [&](int s, int v) -> unsigned {
+    const int bt = v / nj;
+    const int j = ph + (v - bt * nj) * WPT;
+    return (unsigned)(((int64_t)(tw0 + bt * TB) * GS + s * SPL + j) * BB);
+  };
 
-  float carry[B];
+  f32x4 acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
+  const uint8_t* xl = lds + xb * RS + q * kSliceBytes;
+
+  // Decode + MFMA of unit v (slice s) from record r; parks the tile partial in LDS when
+  // this wave is done with the tile.
+  auto process = [&](const Rec<FMT>& r, int s, int v) {
+    const int bt = v / nj;
+    const int jj = v - bt * nj;
+    const uint8_t* xs = xl + (ph + jj * WPT) * 4 * kSliceBytes;
 #pragma unroll
-  for (int b = 0; b < B; ++b) carry[b] = 0.0f;
-
-  Rec<FMT> cur, nxt;
-  int item = i_begin + lane;
-  if (item < i_end) load_rec<FMT>(w, item, cur);
-
-  for (int sb = i_begin; sb < i_end; sb += 64) {
-    const int inext = item + 64;
-    if (inext < i_end) load_rec<FMT>(w, inext, nxt);
-
-    float p[B];
+    for (int c = 0; c < 4; ++c) {
+      float scale = 1.0f;
+      if constexpr (FMT == FB_FMT_E2M1)
+        scale = __builtin_bit_cast(float, ((r.t0.x >> (8 * c)) & 0xFFu) << 23);
 #pragma unroll
-    for (int b = 0; b < B; ++b) p[b] = 0.0f;
-    const bool valid = item < i_end;
-    if (valid) item_dot<FMT, B, XDT>(cur, lds + slice * ss, p);
-
-    // rows touched by this step: rlo .. rhi
-    const int slast = min(sb + 63, i_end - 1);
-    int rhi = rlo;
-    int t = sb_slice + (slast - sb);
-    while (t >= ipr) {
-      t -= ipr;
-      ++rhi;
-    }
-    for (int r = rlo; r <= rhi; ++r) {
-      const bool mine = valid && row == r;
-      const bool done = (r + 1) * ipr - 1 <= slast;
-#pragma unroll
-      for (int b = 0; b < B; ++b) {
-        float tot = wave_sum(mine ? p[b] : 0.0f);
-        if (r == rlo) {
-          tot += carry[b];
-          carry[b] = 0.0f;
-        }
-        if (done) {
-          if (lane == 0) store_y(y, (int64_t)b * N + r, tot, ydt);
+      for (int d = 0; d < 4; d += 2) {
+        u32x4 a0, a1;
+        if constexpr (FMT == FB_FMT_GF4) {
+          gf4_decode16(r.nib[c][d], r.nib[c][d + 1], r.t0, r.t1, a0, a1);
         } else {
-          carry[b] = tot;
+          a0 = e2m1_decode8<XDT>(r.nib[c][d], scale);
+          a1 = e2m1_decode8<XDT>(r.nib[c][d + 1], scale);
         }
+        const u32x4 xv0 = *reinterpret_cast<const u32x4*>(xs + (c * 32 + d * 8) * 2);
+        const u32x4 xv1 = *reinterpret_cast<const u32x4*>(xs + (c * 32 + d * 8 + 8) * 2);
+        acc0 = mfma<XDT>(a0, xv0, acc0);
+        acc1 = mfma<XDT>(a1, xv1, acc1);
       }
     }
+    if (jj == nj - 1) {  // this wave's share of tile tw0 + bt*TB is done
+      if (col < B) {
+        f32x4* sl = slots + ((bt * kWaves + wave) * 4 + q) * B + col;
+        if (s == 0)
+          *sl = acc0 + acc1;
+        else
+          *sl += acc0 + acc1;
+      }
+      acc0 = f32x4{0.f, 0.f, 0.f, 0.f};
+      acc1 = acc0;
+    }
+  };
 
-    // advance
-    item = inext;
-    slice += 64;
-    while (slice >= ipr) {
-      slice -= ipr;
-      ++row;
+  // Ring of kDepth record buffers: loads run kDepth-1 units ahead of the decode.  All
+  // loads are unconditional (past the last unit they use the empty resource), so the
+  // wait before each unit covers exactly that unit's loads.
+  Rec<FMT> ring[kDepth];
+  auto issue = [&](int s, int v, Rec<FMT>& r) {
+    const bool real = v < nunits;  // wave-uniform: no branch, only the range changes
+    const rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(w), (short)0,
+                                                        real ? 0x7fffffff : 0, kRsrcWord3);
+    load_rec<FMT>(rs, real ? unit_off(s, v) : 0u, lane, r);
+  };
+  for (int s = 0; s < S; ++s) {
+#pragma unroll
+    for (int i = 0; i < kDepth - 1; ++i) issue(s, i, ring[i]);
+    const int k0 = s * SPL * 512;
+    if (fwht_block) {
+      const int kw = min(K - k0, nsl * 128);
+      stage_fwht(lds, reinterpret_cast<float*>(lds + B * RS), static_cast<const _Float16*>(x), K,
+                 B, k0, kw, nsl, RS, fwht_block);
+    } else {
+      stage_plain(lds, static_cast<const uint16_t*>(x), K, B, k0, nsl, RS);
     }
-    sb_slice += 64;
-    while (sb_slice >= ipr) {
-      sb_slice -= ipr;
-      ++rlo;
+    __syncthreads();
+    for (int v = 0; v < nunits; v += kDepth) {
+#pragma unroll
+      for (int i = 0; i < kDepth; ++i) {
+        issue(s, v + i + kDepth - 1, ring[(i + kDepth - 1) % kDepth]);
+        __builtin_amdgcn_sched_barrier(0);  // keep the prefetch ahead of the compute
+        if (v + i < nunits) process(ring[i], s, v + i);
+      }
     }
-    cur = nxt;
+    __syncthreads();  // slice done: x may be restaged, slots are complete
+  }
+
+  // y[col][row] = sum over the WPT waves of the tile slot, in phase order
+  const int nt = t1 - t0;
+  for (int e = threadIdx.x; e < nt * 16 * B; e += kThreads) {
+    const int c = e % B;
+    const int r = (e / B) & 15;
+    const int tl = e / (16 * B);
+    const int bt = tl / TB;
+    const int tsl = tl - bt * TB;
+    const int row = (t0 + tl) * 16 + r;
+    float sum = 0.0f;
+    for (int p2 = 0; p2 < WPT; ++p2) {
+      const f32x4 v = slots[((bt * kWaves + tsl * WPT + p2) * 4 + (r >> 2)) * B + c];
+      sum += v[r & 3];
+    }
+    if (row < N) store_y(y, (int64_t)c * N + row, sum, ydt);
   }
 }
 
 // ---------------------------------------------------------------------------------
-// Device decode: one thread per item writes 128 values.
+// Device decode: one thread per item writes 128 values of row n.
 // ---------------------------------------------------------------------------------
 template <int FMT>
 __global__ __launch_bounds__(256) void dequant_kernel(const uint8_t* __restrict__ w,
                                                       void* __restrict__ out, int N, int K,
                                                       int odt) {
-  const int ipr = K >> 7;
+  constexpr int BB = FMT == FB_FMT_GF4 ? fb::kGf4BlockBytes : fb::kE2m1BlockBytes;
+  const int G = K >> 7;
+  const int GS = (G + 3) >> 2;
   const int item = blockIdx.x * 256 + threadIdx.x;
-  if (item >= N * ipr) return;
-  const int n = item / ipr;
-  const int g = item - n * ipr;
+  if (item >= N * G) return;
+  const int n = item / G;
+  const int g = item - n * G;
   Rec<FMT> r;
-  load_rec<FMT>(w, item, r);
+  load_rec_global<FMT>(w + ((int64_t)(n >> 4) * GS + (g >> 2)) * BB, (n & 15) + 16 * (g & 3), r);
   const int64_t o0 = (int64_t)n * K + g * 128;
 #pragma unroll
   for (int c = 0; c < 4; ++c) {
+    const int e = FMT == FB_FMT_GF4 ? 0 : (int)((r.t0.x >> (8 * c)) & 0xFFu) - 127;
 #pragma unroll
     for (int d = 0; d < 4; ++d) {
-      unsigned pr[4];
-      float scale_e = 0;
-      int e = 0;
-      if constexpr (FMT == FB_FMT_GF4) {
-        gf4_decode8(r.nib[c][d], r.t0, r.t1, pr);
-      } else {
-        const unsigned q = r.nib[c][d];
-        pr[0] = e2m1_decode2<FB_DT_BF16, 0>(q);
-        pr[1] = e2m1_decode2<FB_DT_BF16, 1>(q);
-        pr[2] = e2m1_decode2<FB_DT_BF16, 2>(q);
-        pr[3] = e2m1_decode2<FB_DT_BF16, 3>(q);
-        e = (int)((r.t0.x >> (8 * c)) & 0xFFu) - 127;
-      }
-      (void)scale_e;
+      u32x4 pr;
+      if constexpr (FMT == FB_FMT_GF4)
+        pr = gf4_decode8(r.nib[c][d], r.t0, r.t1);
+      else
+        pr = e2m1_decode8<FB_DT_BF16>(r.nib[c][d], 1.0f);
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
+      for (int jj = 0; jj < 4; ++jj) {
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
-          const unsigned bits = (pr[j] >> (16 * h)) & 0xFFFFu;
+          const unsigned bits = (pr[jj] >> (16 * h)) & 0xFFFFu;
           float v;
-          if constexpr (FMT == FB_FMT_GF4) {
+          if constexpr (FMT == FB_FMT_GF4)
             v = (float)__builtin_bit_cast(_Float16, (unsigned short)bits);
-          } else {
+          else
             v = __builtin_ldexpf(__builtin_bit_cast(float, bits << 16), e);
-          }
-          const int64_t o = o0 + c * 32 + d * 8 + j * 2 + h;
+          const int64_t o = o0 + c * 32 + d * 8 + jj * 2 + h;
           if (odt == FB_DT_F32) {
             static_cast<float*>(out)[o] = v;
           } else if (odt == FB_DT_F16) {
@@ -414,7 +450,7 @@ __global__ __launch_bounds__(256) void dequant_kernel(const uint8_t* __restrict_
 }
 
 // ---------------------------------------------------------------------------------
-// host helpers
+// host side
 // ---------------------------------------------------------------------------------
 constexpr int kMaxDevices = 64;
 std::atomic<int> g_cu_count[kMaxDevices];
@@ -433,18 +469,59 @@ int cu_count(int dev) {
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
-size_t gemv_lds_bytes(const fb_shape_t* s) {
-  const size_t ipr = (size_t)s->K / 128;
-  size_t b = ipr * (size_t)(s->B * 256 + 16);
-  if (s->fwht_block) b += (size_t)s->B * s->K * 4;
-  return b;
+struct Plan {
+  int S = 0;     // K-slices staged one after the other
+  int SPL = 0;   // spans per slice
+  int WPT = 0;   // waves per tile
+  int grid = 0;  // workgroups
+  size_t lds = 0;
+};
+
+// Picks (WPT, S, grid) minimising the most units any wave streams, subject to the LDS
+// limit; ties prefer fewer slices.
+bool make_plan(const fb_shape_t* s, int cus, Plan& pl) {
+  const int GS = (s->K / 128 + 3) / 4;
+  const int T = (s->N + 15) / 16;
+  const int grid = std::max(1, std::min(T, cus));
+  const int tpw = (T + grid - 1) / grid;  // most tiles a workgroup owns
+  int64_t best = -1;
+  for (int WPT = 16; WPT >= 1; WPT /= 2) {
+    if (WPT > GS && WPT > 1) continue;
+    const int TB = kWaves / WPT;
+    const int nb = (tpw + TB - 1) / TB;
+    for (int S = 1; S <= GS; ++S) {
+      if (GS % S) continue;
+      const int SPL = GS / S;
+      if (WPT > SPL) continue;
+      if (s->fwht_block && S > 1 && (SPL * 512) % s->fwht_block) continue;
+      const size_t lds = (size_t)x_lds_bytes(s->B, s->K, SPL, s->fwht_block) +
+                         (size_t)nb * kWaves * 4 * s->B * 16;
+      if (lds > (size_t)kLdsLimit) continue;
+      const int64_t cost = (int64_t)nb * ((SPL + WPT - 1) / WPT) * S;
+      if (best < 0 || cost < best) {
+        best = cost;
+        pl.S = S;
+        pl.SPL = SPL;
+        pl.WPT = WPT;
+        pl.grid = grid;
+        pl.lds = lds;
+      }
+      break;  // more slices only add staging work at the same cost
+    }
+  }
+  return best >= 0;
 }
 
-template <int FMT, int B, int XDT>
-int launch_gemv(const void* wdev, const void* x, void* y, const fb_shape_t* s,
+int device_cus() {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return 256;
+  return cu_count(dev);
+}
+
+template <int FMT, int XDT>
+int launch_gemv(const void* wdev, const void* x, void* y, const fb_shape_t* s, const Plan& pl,
                 hipStream_t stream) {
-  auto kern = gemv_kernel<FMT, B, XDT>;
-  const size_t lds = gemv_lds_bytes(s);
+  auto kern = gemv_kernel<FMT, XDT>;
   static std::atomic<bool> attr_set{false};
   if (!attr_set.load(std::memory_order_acquire)) {
     if (hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
@@ -452,33 +529,10 @@ int launch_gemv(const void* wdev, const void* x, void* y, const fb_shape_t* s,
       return FB_ERR_HIP;
     attr_set.store(true, std::memory_order_release);
   }
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess) return FB_ERR_HIP;
-  const int cus = cu_count(dev);
-  const int wg_per_cu = lds <= (size_t)kLdsLimit / 2 ? 2 : 1;
-  const int ipr = s->K / 128;
-  const int total_waves = cus * wg_per_cu * kWaves;
-  int rpw = (s->N + total_waves - 1) / total_waves;
-  const int min_rows = (64 + ipr - 1) / ipr;
-  if (rpw < min_rows) rpw = min_rows;
-  const int waves = (s->N + rpw - 1) / rpw;
-  const int grid = (waves + kWaves - 1) / kWaves;
-  hipLaunchKernelGGL(kern, dim3(grid), dim3(kThreads), lds, stream,
-                     static_cast<const uint8_t*>(wdev), x, y, s->N, s->K, s->fwht_block, rpw,
-                     s->y_dtype);
+  hipLaunchKernelGGL(kern, dim3(pl.grid), dim3(kThreads), pl.lds, stream,
+                     static_cast<const uint8_t*>(wdev), x, y, s->N, s->K, s->B, pl.S, pl.SPL,
+                     pl.WPT, s->fwht_block, s->y_dtype);
   return hipGetLastError() == hipSuccess ? FB_OK : FB_ERR_HIP;
-}
-
-template <int FMT, int XDT>
-int dispatch_batch(const void* wdev, const void* x, void* y, const fb_shape_t* s,
-                   hipStream_t st) {
-  switch (s->B) {
-    case 1: return launch_gemv<FMT, 1, XDT>(wdev, x, y, s, st);
-    case 2: return launch_gemv<FMT, 2, XDT>(wdev, x, y, s, st);
-    case 3: return launch_gemv<FMT, 3, XDT>(wdev, x, y, s, st);
-    case 4: return launch_gemv<FMT, 4, XDT>(wdev, x, y, s, st);
-    default: return FB_ERR_BATCH;
-  }
 }
 
 }  // namespace
@@ -487,7 +541,7 @@ extern "C" {
 
 size_t fb_workspace_bytes(const fb_shape_t* s) {
   (void)s;
-  return 0;
+  return 0;  // the GEMV needs no device workspace
 }
 
 int fb_gemv(const void* wdev, const void* x, void* y, const fb_shape_t* s, void* ws,
@@ -497,15 +551,17 @@ int fb_gemv(const void* wdev, const void* x, void* y, const fb_shape_t* s, void*
   if (!s || !wdev || !x || !y) return FB_ERR_NULL;
   int st = fb_validate(s);
   if (st != FB_OK) return st;
-  if (s->B < 1 || s->B > 4) return FB_ERR_BATCH;
+  if (s->B > 16) return FB_ERR_BATCH;
   if (!aligned16(wdev) || !aligned16(x) || (reinterpret_cast<uintptr_t>(y) & 3u))
     return FB_ERR_ALIGN;
   if (s->fwht_block && s->x_dtype != FB_DT_F16) return FB_ERR_DTYPE;
-  if (gemv_lds_bytes(s) > (size_t)kLdsLimit) return FB_ERR_LDS;
+  Plan pl;
+  if (!make_plan(s, device_cus(), pl)) return FB_ERR_LDS;
   hipStream_t hs = static_cast<hipStream_t>(stream);
-  if (s->fmt == FB_FMT_GF4) return dispatch_batch<FB_FMT_GF4, FB_DT_F16>(wdev, x, y, s, hs);
-  if (s->x_dtype == FB_DT_BF16) return dispatch_batch<FB_FMT_E2M1, FB_DT_BF16>(wdev, x, y, s, hs);
-  return dispatch_batch<FB_FMT_E2M1, FB_DT_F16>(wdev, x, y, s, hs);
+  if (s->fmt == FB_FMT_GF4) return launch_gemv<FB_FMT_GF4, FB_DT_F16>(wdev, x, y, s, pl, hs);
+  if (s->x_dtype == FB_DT_BF16)
+    return launch_gemv<FB_FMT_E2M1, FB_DT_BF16>(wdev, x, y, s, pl, hs);
+  return launch_gemv<FB_FMT_E2M1, FB_DT_F16>(wdev, x, y, s, pl, hs);
 }
 
 int fb_dequant(const void* wdev, void* w_out, int32_t out_dtype, const fb_shape_t* s,

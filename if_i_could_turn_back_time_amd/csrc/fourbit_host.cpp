@@ -227,9 +227,7 @@ int fb_validate(const fb_shape_t* s) {
 
 size_t fb_device_bytes(const fb_shape_t* s) {
   if (fb_validate(s) != FB_OK) return 0;
-  const int64_t items = (int64_t)s->N * (s->K / fb::kItemCodes);
-  const int64_t blocks = (items + fb::kBlockItems - 1) / fb::kBlockItems;
-  return (size_t)blocks * (size_t)fb::block_bytes(s->fmt);
+  return (size_t)fb::device_bytes(s->N, s->K, s->fmt);
 }
 
 int fb_quantize_gf4(const float* w, int32_t N, int32_t K, uint8_t* codes, uint16_t* codebook,
@@ -327,10 +325,10 @@ int fb_to_device(const uint8_t* codes, const void* meta, void* wdev, const fb_sh
     const uint8_t* crow = codes + n * (s->K / 2) + g * 64;  // 128 codes = 64 bytes
     if (s->fmt == FB_FMT_GF4) {
       const uint16_t* book = (const uint16_t*)meta + (n * ipr + g) * 16;
-      fb::gf4_encode_item(crow, book, out, i);
+      fb::gf4_encode_item(crow, book, out, n, g, s->K);
     } else {
       const uint8_t* sc = (const uint8_t*)meta + (n * ipr + g) * 4;
-      fb::e2m1_encode_item(crow, sc, out, i);
+      fb::e2m1_encode_item(crow, sc, out, n, g, s->K);
     }
   }
   return FB_OK;
@@ -348,10 +346,10 @@ int fb_from_device(const void* wdev, uint8_t* codes, void* meta, const fb_shape_
     uint8_t* crow = codes + n * (s->K / 2) + g * 64;
     if (s->fmt == FB_FMT_GF4) {
       uint16_t* book = (uint16_t*)meta + (n * ipr + g) * 16;
-      fb::gf4_decode_item(in, i, crow, book);
+      fb::gf4_decode_item(in, n, g, s->K, crow, book);
     } else {
       uint8_t* sc = (uint8_t*)meta + (n * ipr + g) * 4;
-      fb::e2m1_decode_item(in, i, crow, sc);
+      fb::e2m1_decode_item(in, n, g, s->K, crow, sc);
     }
   }
   return FB_OK;

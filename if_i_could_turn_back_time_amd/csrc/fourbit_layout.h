@@ -1,9 +1,14 @@
 // Device weight-stream layout shared by the host packer and the HIP kernels.
 //
 // The weight of a layer is cut into items of 128 consecutive K-elements of one row:
-// item i = n * (K/128) + g.  Items are stored in blocks of 64 (one per lane of a
-// wave64); inside a block every 16-byte chunk kind is contiguous over the 64 items, so
-// one global_load_dwordx4 of a wave reads 1 KiB of consecutive bytes.
+// item (n, g) covers row n, elements [128g, 128g+128).  Items are stored in blocks of 64,
+// one per lane of a wave64: block (t, sp) holds rows 16t..16t+15 times the four items
+// 4sp..4sp+3 of each row ("span" sp = 512 K-elements), lane L = (n % 16) + 16 * (g % 4),
+// which is the lane that feeds that row / K-quarter into a 16x16x32 MFMA.  Blocks are
+// ordered t-major: block index = t * GS + sp with GS = ceil(K/512) spans per row; rows
+// are padded to a multiple of 16 and the last span with zero bytes.  Inside a block
+// every 16-byte chunk kind is contiguous over the 64 lanes, so one global_load_dwordx4
+// of a wave reads 1 KiB of consecutive bytes.
 //
 //  GF4 block (6144 B):  chunk c = 0..3 at c*1024 + lane*16  -> 32 codes each
 //                       chunk 4 at 4096 + lane*16           -> lo-byte tables A'|B'
@@ -72,14 +77,22 @@ inline uint8_t gf4_lookup_plane(const uint8_t A[8], const uint8_t B[8], int c) {
   return (uint8_t)(perm8(A, (uint8_t)c) ^ perm8(B, (uint8_t)(c ^ 8)));
 }
 
-inline uint8_t* item_base(uint8_t* dev, int64_t i, int fmt) {
-  return dev + (i / kBlockItems) * (int64_t)block_bytes(fmt);
+inline int64_t spans_per_row(int64_t K) { return (K / kItemCodes + 3) / 4; }
+inline int64_t row_tiles(int64_t N) { return (N + 15) / 16; }
+inline int64_t device_bytes(int64_t N, int64_t K, int fmt) {
+  return row_tiles(N) * spans_per_row(K) * block_bytes(fmt);
 }
+// block offset and lane of item (n, g)
+inline int64_t item_block(int64_t n, int64_t g, int64_t K) {
+  return (n / 16) * spans_per_row(K) + g / 4;
+}
+inline int item_lane(int64_t n, int64_t g) { return (int)(n % 16 + 16 * (g % 4)); }
 
 // Host: canonical 64 code bytes (128 codes) + 16 fp16 -> device item i.
-inline void gf4_encode_item(const uint8_t* canon, const uint16_t* book, uint8_t* dev, int64_t i) {
-  uint8_t* base = item_base(dev, i, 0);
-  const int lane = (int)(i % kBlockItems);
+inline void gf4_encode_item(const uint8_t* canon, const uint16_t* book, uint8_t* dev, int64_t n,
+                            int64_t g, int64_t K) {
+  uint8_t* base = dev + item_block(n, g, K) * kGf4BlockBytes;
+  const int lane = item_lane(n, g);
   auto code = [&](int e) { return (uint8_t)((canon[e >> 1] >> ((e & 1) * 4)) & 15); };
   for (int c = 0; c < 4; ++c) {
     uint8_t* dst = base + c * 1024 + lane * 16;
@@ -101,9 +114,10 @@ inline void gf4_encode_item(const uint8_t* canon, const uint16_t* book, uint8_t*
 }
 
 // Host inverse of gf4_encode_item (decodes the tables through the perm8 model).
-inline void gf4_decode_item(const uint8_t* dev, int64_t i, uint8_t* canon, uint16_t* book) {
-  const uint8_t* base = dev + (i / kBlockItems) * (int64_t)kGf4BlockBytes;
-  const int lane = (int)(i % kBlockItems);
+inline void gf4_decode_item(const uint8_t* dev, int64_t n, int64_t g, int64_t K, uint8_t* canon,
+                            uint16_t* book) {
+  const uint8_t* base = dev + item_block(n, g, K) * kGf4BlockBytes;
+  const int lane = item_lane(n, g);
   memset(canon, 0, 64);
   for (int c = 0; c < 4; ++c) {
     const uint8_t* src = base + c * 1024 + lane * 16;
@@ -121,16 +135,18 @@ inline void gf4_decode_item(const uint8_t* dev, int64_t i, uint8_t* canon, uint1
     book[t] = (uint16_t)(gf4_lookup_plane(tl, tl + 8, t) | (gf4_lookup_plane(th, th + 8, t) << 8));
 }
 
-inline void e2m1_encode_item(const uint8_t* canon, const uint8_t* sc4, uint8_t* dev, int64_t i) {
-  uint8_t* base = item_base(dev, i, 1);
-  const int lane = (int)(i % kBlockItems);
+inline void e2m1_encode_item(const uint8_t* canon, const uint8_t* sc4, uint8_t* dev, int64_t n,
+                             int64_t g, int64_t K) {
+  uint8_t* base = dev + item_block(n, g, K) * kE2m1BlockBytes;
+  const int lane = item_lane(n, g);
   for (int c = 0; c < 4; ++c) memcpy(base + c * 1024 + lane * 16, canon + c * 16, 16);
   memcpy(base + 4096 + lane * 4, sc4, 4);
 }
 
-inline void e2m1_decode_item(const uint8_t* dev, int64_t i, uint8_t* canon, uint8_t* sc4) {
-  const uint8_t* base = dev + (i / kBlockItems) * (int64_t)kE2m1BlockBytes;
-  const int lane = (int)(i % kBlockItems);
+inline void e2m1_decode_item(const uint8_t* dev, int64_t n, int64_t g, int64_t K, uint8_t* canon,
+                             uint8_t* sc4) {
+  const uint8_t* base = dev + item_block(n, g, K) * kE2m1BlockBytes;
+  const int lane = item_lane(n, g);
   for (int c = 0; c < 4; ++c) memcpy(canon + c * 16, base + c * 1024 + lane * 16, 16);
   memcpy(sc4, base + 4096 + lane * 4, 4);
 }

@@ -23,7 +23,7 @@ import torch.nn as nn
 from . import _capi as C
 
 LAYOUT_VERSION = 1
-MAX_GEMV_BATCH = 4
+MAX_GEMV_BATCH = 16
 
 
 def fwht_block_for(K: int) -> int:
@@ -44,6 +44,7 @@ class PackedWeight:
         self.fmt_name = fmt
         self.N, self.K, self.fwht_block = N, K, fwht_block
         self.codes, self.meta = codes, meta
+        self._ws = {}
         shape = C.make_shape(N, K, 1, self.fmt, fwht_block)
         self.wdev = C.to_device_layout(codes, meta, shape)
         if device is not None:
@@ -68,14 +69,27 @@ class PackedWeight:
         return C.make_shape(self.N, self.K, B, self.fmt, self.fwht_block,
                             C.DTYPE_CODE[x_dtype], C.DTYPE_CODE[y_dtype])
 
+    def workspace(self, shape: C.FbShape, device):
+        """Cached zero-initialised fb_gemv workspace for this device and shape (None when
+        the shape needs none)."""
+        need = C.workspace_bytes(shape)
+        if not need:
+            return None
+        key = (str(device), need)
+        ws = self._ws.get(key)
+        if ws is None:
+            ws = self._ws[key] = C.new_workspace(shape, device)
+        return ws
+
     def gemv(self, x: torch.Tensor, out: torch.Tensor | None = None,
              out_dtype: torch.dtype | None = None) -> torch.Tensor:
-        """x [B,K] (B <= 4) on the GPU -> y [B,N]."""
+        """x [B,K] (B <= 16) on the GPU -> y [B,N]."""
         B = x.shape[0]
-        ydt = out_dtype or x.dtype
+        ydt = out.dtype if out is not None else (out_dtype or x.dtype)
         if out is None:
             out = torch.empty(B, self.N, dtype=ydt, device=x.device)
-        return C.gemv(self.wdev, x, out, self.shape(B, x.dtype, ydt))
+        shape = self.shape(B, x.dtype, ydt)
+        return C.gemv(self.wdev, x, out, shape, self.workspace(shape, x.device))
 
     def dequant_device(self, out_dtype=torch.float32) -> torch.Tensor:
         return C.dequant_device(self.wdev, C.make_shape(self.N, self.K, 1, self.fmt), out_dtype)
@@ -154,6 +168,15 @@ class QuantLinear(nn.Linear):
         super()._load_from_state_dict(state_dict, prefix, local_metadata, strict, missing_keys,
                                       unexpected_keys, error_msgs)
 
+    def _workspace(self, shape: C.FbShape):
+        need = C.workspace_bytes(shape)
+        if not need:
+            return None
+        ws = getattr(self, "_ws_cache", None)
+        if ws is None or ws.numel() < need or ws.device != self.wdev.device:
+            ws = self._ws_cache = C.new_workspace(shape, self.wdev.device)
+        return ws
+
     def _rebuild_after_load(self, incompatible_keys) -> None:
         hdr = self.fb_header.tolist()
         if hdr[0] != LAYOUT_VERSION:
@@ -198,7 +221,8 @@ class QuantLinear(nn.Linear):
         y = torch.empty(x2.shape[0], N, dtype=ydt, device=x.device)
         for b0 in range(0, x2.shape[0], MAX_GEMV_BATCH):
             b1 = min(b0 + MAX_GEMV_BATCH, x2.shape[0])
-            C.gemv(self.wdev, xk[b0:b1], y[b0:b1], self._shape(b1 - b0, xk.dtype, ydt))
+            shape = self._shape(b1 - b0, xk.dtype, ydt)
+            C.gemv(self.wdev, xk[b0:b1], y[b0:b1], shape, self._workspace(shape))
         if self.bias is not None:
             y = y + self.bias.to(ydt)
         return y.reshape(*lead, N)

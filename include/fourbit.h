@@ -67,11 +67,12 @@ const char* fb_strerror(int code);
 /* Host-side checks of a shape (no GPU needed). */
 int fb_validate(const fb_shape_t* s);
 
-/* Bytes of the device weight stream (nibbles + codebooks/scales, padded to whole
- * 64-item blocks) for fb_to_device / fb_gemv. */
+/* Bytes of the device weight stream (nibbles + codebooks/scales; rows padded to a
+ * multiple of 16 and K to a multiple of 512 with zero bytes) for fb_to_device /
+ * fb_gemv. */
 size_t fb_device_bytes(const fb_shape_t* s);
 
-/* Workspace bytes fb_gemv needs for this shape (0 when none). */
+/* Workspace bytes fb_gemv needs for this shape on the current device (0 = invalid). */
 size_t fb_workspace_bytes(const fb_shape_t* s);
 
 /* ---------------------------------------------------------------------------------
@@ -115,12 +116,15 @@ int fb_dequant_host(const uint8_t* codes, const void* meta, float* w_out, const 
  * GPU entry points (hipStream_t passed as void*).
  * ------------------------------------------------------------------------------- */
 
-/* Fused dequant-GEMV, batch 1..4: y = x' . W^T with x' = FWHT_b(x) when fwht_block.
+/* Fused dequant-GEMV, batch 1..16: y = x' . W^T with x' = FWHT_b(x) when fwht_block.
  * Replaces QuantLinear.forward's dequantize + F.linear pair (layers.py:33-38;
  * brecq.py:323-329 new_forward) and the reference's native linear_kernel_batch
  * (CUDA_C_Code/include/layers.h:9828-9839).  wdev is the fb_to_device stream in
- * device memory; x is [B,K] of x_dtype, y is [B,N] of y_dtype.  ws may be NULL when
- * fb_workspace_bytes(s) == 0. */
+ * device memory; x is [B,K] of x_dtype, y is [B,N] of y_dtype.
+ * ws: device workspace of at least fb_workspace_bytes(s) bytes, 16-byte aligned, whose
+ * bytes must be zero before its first use; every call leaves it reusable (the tile
+ * counters it holds are reset by the call).  Calls that overlap in time must not share
+ * a workspace. */
 int fb_gemv(const void* wdev, const void* x, void* y, const fb_shape_t* s, void* ws,
             size_t ws_bytes, void* stream);
 

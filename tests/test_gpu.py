@@ -86,7 +86,7 @@ def test_decode_bit_exact_shapes(fmt, N, K):
 
 @pytest.mark.parametrize("fmt,xdt", [("gf4", torch.float16), ("e2m1", torch.bfloat16),
                                      ("e2m1", torch.float16)])
-@pytest.mark.parametrize("B", [1, 2, 3, 4])
+@pytest.mark.parametrize("B", [1, 2, 3, 4, 8, 16])
 @pytest.mark.parametrize("N,K", [(1, 128), (7, 256), (64, 1024), (130, 4096), (48, 11008),
                                  (40, 28672)])
 def test_gemv_vs_oracle(fmt, xdt, B, N, K):
@@ -120,9 +120,11 @@ def test_gemv_fwht_vs_oracle(B, N, K, block):
     torch.cuda.synchronize()
     ok, emax, _ = within_tol(y, yref)
     assert ok, f"max abs err {emax}"
-    # rotation invariance: the rotated layer approximates the unrotated product
+    # rotation invariance: the rotated 4-bit layer approximates the unrotated product
+    # (quantization error of 16 Jenks levels is ~7% rms of the weight)
     ydense = x.float() @ w.t()
-    assert (y.cpu() - ydense).abs().max() < 0.2
+    rel = ((y.cpu() - ydense).pow(2).mean() / ydense.pow(2).mean()).sqrt()
+    assert rel < 0.15
 
 
 @pytest.mark.parametrize("fmt", ["gf4", "e2m1"])
@@ -166,9 +168,11 @@ def test_full_size_vs_torch_reference(fmt, N, K):
     rows = torch.randint(0, N, (16,), generator=gen)
     host = pw.dequant_host()
     assert torch.equal(W[rows].cpu(), host[rows])
-    for B in (1, 2, 4):
+    for B in (1, 2, 4, 8, 16):
         x = torch.randn(B, K, generator=gen).to(xdt)
         y = pw.gemv(x.to(DEV), out_dtype=torch.float32)
+        y2 = pw.gemv(x.to(DEV), out_dtype=torch.float32)  # workspace reuse, same bits
+        assert torch.equal(y, y2)
         yref = (x.to(DEV).float() @ W.t())
         torch.cuda.synchronize()
         ok, emax, _ = within_tol(y, yref)

@@ -43,9 +43,9 @@ def test_validate_errors(kw, err):
 
 
 def test_gemv_validation_needs_no_gpu():
-    sh = C.make_shape(64, 1024, 5)
+    sh = C.make_shape(64, 1024, 17)
     buf = ctypes.c_char_p(b"x" * 64)
-    assert C.lib().fb_gemv(buf, buf, buf, ctypes.byref(sh), None, 0, None) == -9  # batch 5
+    assert C.lib().fb_gemv(buf, buf, buf, ctypes.byref(sh), None, 0, None) == -9  # batch 17
     sh = C.make_shape(64, 1024, 1)
     assert C.lib().fb_gemv(None, buf, buf, ctypes.byref(sh), None, 0, None) == -1
     sh.group = 32
@@ -115,8 +115,8 @@ def test_device_layout_roundtrip(fmt, N, K):
         meta = torch.from_numpy(RNG.integers(0, 255, size=(N, K // 32), dtype=np.uint8))
     sh = C.make_shape(N, K, 1, fmt)
     dev = C.to_device_layout(codes, meta, sh)
-    items = N * K // 128
-    assert dev.numel() == -(-items // 64) * (6144 if fmt == C.FMT_GF4 else 4352)
+    tiles, spans = -(-N // 16), -(-(K // 128) // 4)
+    assert dev.numel() == tiles * spans * (6144 if fmt == C.FMT_GF4 else 4352)
     c2, m2 = C.from_device_layout(dev, sh)
     assert torch.equal(c2, codes) and torch.equal(m2, meta)
 
@@ -209,3 +209,13 @@ def test_quantize_module_swaps_linears_and_keeps_masks():
     assert isinstance(net[0], torch.nn.Linear) and not isinstance(net[0], QuantLinear)
     assert torch.equal(q[0].mask[:, :64], torch.zeros(64, 64))
     assert (q[0].dequantized_weight()[:, :64] == 0).all()
+
+
+def test_workspace_contract():
+    """The GEMV needs no device workspace (workgroups never exchange partial sums), so
+    fb_gemv accepts NULL; the argument stays in the ABI for callers that pass one."""
+    for B in (1, 4, 16):
+        assert C.workspace_bytes(C.make_shape(8192, 28672, B)) == 0
+    buf = ctypes.c_char_p(b"x" * 64)
+    big = C.make_shape(8192, 28672, 17)
+    assert C.lib().fb_gemv(buf, buf, buf, ctypes.byref(big), None, 0, None) == -9
