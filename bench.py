@@ -212,7 +212,7 @@ def load_traffic(name: str):
 
 
 def run_workload(name: str, steps: int, warmup: int, want_cpu: bool, check: bool = True,
-                 graph: bool = True):
+                 warm: bool = False):
     fmt, K, N, B, kind, fwht = WORKLOADS[name]
     xdt = torch.float16 if fmt == "gf4" else torch.bfloat16
     w, x = synth(kind, N, K, B, xdt)
@@ -224,8 +224,8 @@ def run_workload(name: str, steps: int, warmup: int, want_cpu: bool, check: bool
     xd = x.to("cuda:0")
     y = torch.empty(B, N, dtype=xdt, device="cuda:0")
     ms, ncp = time_gpu(pw, xd, y, steps, warmup, cold=True)
-    ms_warm, _ = time_gpu(pw, xd, y, steps, warmup, cold=False)
-    ms_graph = time_gpu_graph(pw, xd, y, min(steps, 200)) if graph else None
+    ms_warm = time_gpu(pw, xd, y, steps, warmup, cold=False)[0] if warm else None
+    ms_graph = time_gpu_graph(pw, xd, y, min(steps, 200)) if warm else None
     nbytes = pw.algorithmic_bytes(B)
     gbs = nbytes / (ms * 1e-3) / 1e9
     rec = {
@@ -233,8 +233,8 @@ def run_workload(name: str, steps: int, warmup: int, want_cpu: bool, check: bool
         "bytes_per_call": nbytes, "weight_stream_bytes": N * K // 2,
         "us_per_call": ms * 1e3, "GBps": gbs, "frac_of_8TBps": gbs / PEAK_GBS,
         "weight_copies_cycled": ncp,
-        "us_per_call_warm": ms_warm * 1e3,
-        "GBps_warm": nbytes / (ms_warm * 1e-3) / 1e9,
+        "us_per_call_warm": None if ms_warm is None else ms_warm * 1e3,
+        "GBps_warm": None if ms_warm is None else nbytes / (ms_warm * 1e-3) / 1e9,
         "us_per_call_graph": None if ms_graph is None else ms_graph * 1e3,
         "GBps_graph": None if ms_graph is None else nbytes / (ms_graph * 1e-3) / 1e9,
         "tokens_per_s_equiv": B / (ms * 1e-3), "pack_s": pack_s,
@@ -266,7 +266,21 @@ def main():
     ap.add_argument("--sweep", action="store_true", help="also time every config shape")
     ap.add_argument("--sweep-out", default="gpurun_out/bench_sweep.jsonl")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--warm", action="store_true",
+                    help="also time one weight copy (Infinity-Cache warm) and a HIP graph")
+    ap.add_argument("--calib-copy", type=int, default=0, metavar="BYTES",
+                    help="only run device-to-device copies of BYTES bytes (PMC calibration)")
     args = ap.parse_args()
+    if args.calib_copy:
+        # a plain copy kernel of known size: FETCH_SIZE / WRITE_SIZE per dispatch of it
+        # give the scale between those counters and bytes moved
+        src = torch.randint(0, 255, (args.calib_copy,), dtype=torch.uint8, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(args.steps):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"calib_copy_bytes": args.calib_copy, "copies": args.steps}))
+        return
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (got --gpus {args.gpus}); the "
               "multi-GPU sharding of the GEMV is a design note, not a measured path.",
@@ -282,7 +296,8 @@ def main():
             for name in WORKLOADS:
                 if name == args.workload:
                     continue
-                rec, pw = run_workload(name, max(50, args.steps // 2), args.warmup, False)
+                rec, pw = run_workload(name, max(50, args.steps // 2), args.warmup, False,
+                                       warm=args.warm)
                 del pw
                 torch.cuda.empty_cache()
                 f.write(json.dumps(rec) + "\n")
@@ -290,7 +305,8 @@ def main():
                 print(f"[sweep] {name}: {rec['us_per_call']:.2f} us, {rec['GBps']:.0f} GB/s, "
                       f"parity {rec.get('parity_ok')}", file=sys.stderr, flush=True)
 
-    rec, pw = run_workload(args.workload, args.steps, args.warmup, not args.no_cpu)
+    rec, pw = run_workload(args.workload, args.steps, args.warmup, not args.no_cpu,
+                           warm=args.warm)
     fmt, K, N, B = rec["fmt"], rec["K"], rec["N"], rec["B"]
     achieved = rec["GBps"]
     out = {

@@ -72,7 +72,7 @@ int fb_validate(const fb_shape_t* s);
  * fb_gemv. */
 size_t fb_device_bytes(const fb_shape_t* s);
 
-/* Workspace bytes fb_gemv needs for this shape on the current device (0 = invalid). */
+/* Workspace bytes fb_gemv needs for this shape (currently 0 for every shape). */
 size_t fb_workspace_bytes(const fb_shape_t* s);
 
 /* ---------------------------------------------------------------------------------
@@ -121,10 +121,10 @@ int fb_dequant_host(const uint8_t* codes, const void* meta, float* w_out, const 
  * brecq.py:323-329 new_forward) and the reference's native linear_kernel_batch
  * (CUDA_C_Code/include/layers.h:9828-9839).  wdev is the fb_to_device stream in
  * device memory; x is [B,K] of x_dtype, y is [B,N] of y_dtype.
- * ws: device workspace of at least fb_workspace_bytes(s) bytes, 16-byte aligned, whose
- * bytes must be zero before its first use; every call leaves it reusable (the tile
- * counters it holds are reset by the call).  Calls that overlap in time must not share
- * a workspace. */
+ * ws: device workspace of at least fb_workspace_bytes(s) bytes (16-byte aligned).  The
+ * current kernels exchange nothing between workgroups through memory, so
+ * fb_workspace_bytes is 0 for every valid shape and ws may be NULL; the argument is
+ * kept so that a future split-K variant does not change the ABI. */
 int fb_gemv(const void* wdev, const void* x, void* y, const fb_shape_t* s, void* ws,
             size_t ws_bytes, void* stream);
 

@@ -31,3 +31,14 @@ def pytest_collection_modifyitems(config, items):
     for it in items:
         if "gpu" in it.keywords:
             it.add_marker(skip)
+
+
+@pytest.fixture(autouse=True)
+def _seed_everything():
+    """Every test starts from the same torch / numpy global RNG state, so failures
+    reproduce by test id alone."""
+    import numpy as np
+    import torch
+    torch.manual_seed(1234)
+    np.random.seed(1234)
+    yield

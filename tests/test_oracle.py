@@ -250,11 +250,27 @@ def test_yref_special_cases():
 
 
 def test_quantlinear_commit_restatement():
-    """layers.py:23-26, 39-45: levels are in [-7, 8] and W_q = mask * s * level."""
-    w = torch.randn(8, 64) * 0.02
-    theta = torch.randn(8, 64)
-    mask = (torch.rand(8, 64) > 0.3).float()
-    Wq, s, lvl = O.quantlinear_commit_weight(w, theta, mask)
-    assert lvl.min() >= -7 and lvl.max() <= 8
-    assert torch.equal(Wq, mask * s * torch.round(torch.floor(w / s) +
-                                                  (torch.sigmoid(theta) * 1.2 - 0.1 > 0.5).float()))
+    """layers.py:23-26, 39-45 (scale = amax/7, floor, +1 where the gate is open).
+
+    Known answer on exactly representable values (s = 0.4375/7 = 2^-4 exactly; the
+    1e-12 is below the fp32 ulp), then floor/ceil bounds on random rows.  Levels can
+    reach -8: fp32 rounding of amax/7 can put -amax/s just below -7."""
+    w = torch.tensor([[7.0, -3.5, 1.0, 0.0, -7.0, 2.5]]) / 16
+    closed = torch.full_like(w, -20.0)          # sigmoid*1.2-0.1 < 0.5 -> +0
+    opened = torch.full_like(w, 20.0)           # -> +1
+    Wq, s, lvl = O.quantlinear_commit_weight(w, closed)
+    assert float(s) == 1 / 16
+    assert lvl.tolist() == [[7, -4, 1, 0, -7, 2]]
+    assert torch.equal(Wq, lvl / 16)
+    Wq, _, lvl = O.quantlinear_commit_weight(w, opened, mask=torch.tensor([[1, 1, 1, 1, 1, 0.]]))
+    assert lvl.tolist() == [[8, -3, 2, 1, -6, 0]]
+    assert Wq[0, 5] == 0                        # masked weight vanishes
+    g = torch.Generator().manual_seed(7)
+    w = torch.randn(8, 64, generator=g) * 0.02
+    for theta, lo, hi in ((closed[:, :1].expand(8, 64), 0.0, 1.0),
+                          (opened[:, :1].expand(8, 64), -1.0, 0.0)):
+        Wq, s, lvl = O.quantlinear_commit_weight(w, theta)
+        assert lvl.min() >= -8 and lvl.max() <= 8
+        assert torch.equal(lvl, torch.round(lvl))
+        r = (w - Wq) / s                        # floor: r in [0, 1); floor+1: r in [-1, 0)
+        assert r.min() >= lo - 1e-5 and r.max() < hi + 1e-5
