@@ -264,7 +264,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=50)
     ap.add_argument("--workload", default=DEFAULT, choices=sorted(WORKLOADS))
     ap.add_argument("--sweep", action="store_true", help="also time every config shape")
-    ap.add_argument("--sweep-out", default="gpurun_out/bench_sweep.jsonl")
+    ap.add_argument("--sweep-out", default="bench_sweep.jsonl")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--warm", action="store_true",
                     help="also time one weight copy (Infinity-Cache warm) and a HIP graph")

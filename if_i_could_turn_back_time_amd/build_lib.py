@@ -20,10 +20,16 @@ BUILD = ROOT / "_build"
 LIB = PKG / "libfourbit.so"
 ARCH = "gfx950"
 
-# packed fp32 VALU ops are disabled for every HIP translation unit
+# packed fp32 VALU ops are disabled for every HIP translation unit: a correctness
+# precaution for gfx950, where some of their forms have been seen to give wrong results
 HIP_FLAGS = [
     f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # the GEMV's work counter is a one-lane LDS atomic whose result is used a step later;
+    # the wave-aggregating atomic rewrite would wait for it on the spot
+    "-mllvm", "-amdgpu-atomic-optimizer-strategy=None",
+    # kernel arguments arrive in SGPRs with the wave instead of through a scalar load
+    "-mllvm", "-amdgpu-kernarg-preload-count=16",
     "-Wno-unused-command-line-argument",
 ]
 HOST_FLAGS = ["-O3", "-std=c++17", "-fPIC", "-ffp-contract=off", "-Wall"]

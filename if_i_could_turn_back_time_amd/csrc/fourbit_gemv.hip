@@ -9,14 +9,14 @@
 // LDS).  The VALU only decodes; the cross-lane reduction is the MFMA itself; batch 1..16
 // costs the same VALU work.
 //
-// Partition: workgroup g (16 waves) owns the contiguous 16-row tiles [t0, t1); its waves
-// are split into TB = 16/WPT tile slots of WPT waves, and the WPT waves of a slot take
-// every WPT-th span of their tile.  When x does not fit LDS the K range is cut into S
-// slices that the workgroup stages one after the other.  Each wave keeps one tile's
-// partial MFMA accumulator in registers and parks it in LDS when done; after the last
-// slice the workgroup adds the WPT partials of each output in a fixed order.  No
-// workgroup talks to another, so there are no atomics or device-scope fences, and
-// results do not depend on scheduling.
+// Partition: workgroup g (16 waves, one per CU) owns the contiguous 16-row tiles [t0, t1).
+// Its (tile, span) units are handed to its waves through an LDS counter: the SIMDs issue
+// the oldest wave first, so with a fixed split the youngest wave of each SIMD would finish
+// long after the others; taking units on demand keeps all waves busy to the end.  Each
+// unit's partial sums go to a slot of their own, and after the last unit the workgroup
+// adds each output's slots in span order, so results do not depend on which wave did what.
+// When x does not fit LDS the K range is cut into S slices staged one after the other.
+// No workgroup talks to another: no global atomics or device-scope fences.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -36,7 +36,6 @@ constexpr int kWaves = 16;
 constexpr int kThreads = kWaves * 64;
 constexpr int kLdsLimit = 160 * 1024;
 constexpr int kSliceBytes = 272;  // 128 x 16-bit values + 16-byte pad (bank spread)
-constexpr int kDepth = 2;         // record buffers per wave (loads in flight + the one decoding)
 
 // ---------------------------------------------------------------------------------
 // small device helpers
@@ -147,19 +146,21 @@ constexpr int kNT = 2;                  // streaming (non-temporal) cache policy
 // Loads one lane's record of the block at byte offset `boff` of the weight stream.
 // With a zero-sized resource the loads are out of range: they return zeros and move no
 // data, which is how the pipeline issues its loads unconditionally past the last unit.
+// The tables / scales are issued first: chunk 0 can then be decoded as soon as they and
+// nibble chunk 0 have arrived, while chunks 1..3 are still in flight.
 template <int FMT>
 __device__ __forceinline__ void load_rec(rsrc_t rs, unsigned boff, int lane, Rec<FMT>& r) {
   const int vo = lane * 16;
-#pragma unroll
-  for (int c = 0; c < 4; ++c)
-    r.nib[c] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                                             rs, vo + c * 1024, (int)boff, kNT));
   if constexpr (FMT == FB_FMT_GF4) {
     r.t0 = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, vo, (int)boff + 4096, kNT));
     r.t1 = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, vo, (int)boff + 5120, kNT));
   } else {
     r.t0.x = __builtin_amdgcn_raw_buffer_load_b32(rs, lane * 4, (int)boff + 4096, kNT);
   }
+#pragma unroll
+  for (int c = 0; c < 4; ++c)
+    r.nib[c] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                             rs, vo + c * 1024, (int)boff, kNT));
 }
 
 // Record read for the device decoder (plain global loads).
@@ -188,27 +189,76 @@ __host__ __device__ inline int x_row_stride(int nsl) {
   return rs;
 }
 
-__device__ void stage_plain(uint8_t* lds, const uint16_t* __restrict__ x, int K, int B, int k0,
-                            int nsl, int RS) {
-  const int per_row = nsl * 16;  // 16-byte chunks per batch row
-  for (int t = threadIdx.x; t < B * per_row; t += kThreads) {
+// x is read in chunks of 8 consecutive values (16 bytes), kXPre per thread ahead of the
+// slice's first weight loads, so that their wait does not queue behind the weight stream.
+constexpr int kXPre = 4;
+struct XPre {
+  u32x4 v[kXPre];
+};
+
+__device__ __forceinline__ u32x4 x_load8(const uint16_t* __restrict__ x, int K, int b, int k) {
+  u32x4 v = {0u, 0u, 0u, 0u};
+  if (k < K) v = *reinterpret_cast<const u32x4*>(x + (int64_t)b * K + k);
+  return v;
+}
+
+// Chunk t of a slice is batch row t / per_row, values k0 + 8 * (t % per_row) ...; thread
+// j * kThreads + threadIdx.x of the workgroup takes chunk t in step j.
+__device__ __forceinline__ void x_preload(XPre& xp, const uint16_t* __restrict__ x, int K, int k0,
+                                          int per_row, int nchunks) {
+#pragma unroll
+  for (int j = 0; j < kXPre; ++j) {
+    const int t = threadIdx.x + j * kThreads;
+    if (t < nchunks) {
+      const int b = t / per_row;
+      xp.v[j] = x_load8(x, K, b, k0 + (t - b * per_row) * 8);
+    }
+  }
+}
+
+// Plain staging: chunk t lands in its 128-value group of the slice layout.
+__device__ void stage_plain(uint8_t* lds, const XPre& xp, const uint16_t* __restrict__ x, int K,
+                            int B, int k0, int nsl, int RS) {
+  const int per_row = nsl * 16;
+  const int n = B * per_row;
+  auto put = [&](int t, const u32x4& v) {
     const int b = t / per_row;
     const int c8 = t - b * per_row;
-    const int k = k0 + c8 * 8;
-    u32x4 v = {0u, 0u, 0u, 0u};
-    if (k < K) v = *reinterpret_cast<const u32x4*>(x + (int64_t)b * K + k);
     *reinterpret_cast<u32x4*>(lds + b * RS + (c8 >> 4) * kSliceBytes + (c8 & 15) * 16) = v;
+  };
+#pragma unroll
+  for (int j = 0; j < kXPre; ++j) {
+    const int t = threadIdx.x + j * kThreads;
+    if (t < n) put(t, xp.v[j]);
+  }
+  for (int t = threadIdx.x + kXPre * kThreads; t < n; t += kThreads) {
+    const int b = t / per_row;
+    put(t, x_load8(x, K, b, k0 + (t - b * per_row) * 8));
   }
 }
 
 // Blockwise normalised FWHT (fp32 butterflies) of x[b, k0 : k0+kw] into the staged
 // layout (rounded to fp16).  F: LDS scratch of B*kw floats; kw is a whole number of
 // blocks.  Stages go 4 at a time: a thread owns 16 values spaced h0 apart.
-__device__ void stage_fwht(uint8_t* lds, float* F, const _Float16* __restrict__ x, int K, int B,
-                           int k0, int kw, int nsl, int RS, int fb) {
-  for (int t = threadIdx.x; t < B * kw; t += kThreads) {
-    const int b = t / kw;
-    F[t] = (float)x[(int64_t)b * K + k0 + (t - b * kw)];
+__device__ void stage_fwht(uint8_t* lds, float* F, const XPre& xp, const uint16_t* __restrict__ x,
+                           int K, int B, int k0, int kw, int nsl, int RS, int fb) {
+  const int per_row = kw / 8;
+  const int n = B * per_row;
+  auto put = [&](int t, const u32x4& v) {
+    const int b = t / per_row;
+    float* f = F + b * kw + (t - b * per_row) * 8;
+    const half8_t h = __builtin_bit_cast(half8_t, v);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) f[e] = (float)h[e];
+  };
+#pragma unroll
+  for (int j = 0; j < kXPre; ++j) {
+    const int t = threadIdx.x + j * kThreads;
+    if (t < n) put(t, xp.v[j]);
+  }
+  for (int t = threadIdx.x + kXPre * kThreads; t < n; t += kThreads) {
+    const int b = t / per_row;
+    put(t, x_load8(x, K, b, k0 + (t - b * per_row) * 8));
   }
   __syncthreads();
   const int lg_fb = 31 - __builtin_clz(fb);
@@ -263,6 +313,45 @@ __host__ __device__ inline int x_lds_bytes(int B, int K, int SPL, int fwht_block
   return (b + 15) & ~15;
 }
 
+// Decode + MFMA of one unit held in registers: the lane's f32x4 of partial sums (rows
+// 4q..4q+3 of the tile, batch column L % 16).  xs: the unit's x in the staged layout.
+template <int FMT, int XDT>
+__device__ __forceinline__ f32x4 unit_partial(const Rec<FMT>& r, const uint8_t* xs) {
+  f32x4 acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    // The SIMD issues the oldest ready wave first; raising the priority as a unit
+    // progresses lets the waves that are furthest into their unit finish it first, so
+    // the units of young waves do not trail behind at the end.
+    if (c == 0)
+      __builtin_amdgcn_s_setprio(0);
+    else if (c == 1)
+      __builtin_amdgcn_s_setprio(1);
+    else if (c == 2)
+      __builtin_amdgcn_s_setprio(2);
+    else
+      __builtin_amdgcn_s_setprio(3);
+    float scale = 1.0f;
+    if constexpr (FMT == FB_FMT_E2M1)
+      scale = __builtin_bit_cast(float, ((r.t0.x >> (8 * c)) & 0xFFu) << 23);
+#pragma unroll
+    for (int d = 0; d < 4; d += 2) {
+      u32x4 a0, a1;
+      if constexpr (FMT == FB_FMT_GF4) {
+        gf4_decode16(r.nib[c][d], r.nib[c][d + 1], r.t0, r.t1, a0, a1);
+      } else {
+        a0 = e2m1_decode8<XDT>(r.nib[c][d], scale);
+        a1 = e2m1_decode8<XDT>(r.nib[c][d + 1], scale);
+      }
+      const u32x4 xv0 = *reinterpret_cast<const u32x4*>(xs + (c * 32 + d * 8) * 2);
+      const u32x4 xv1 = *reinterpret_cast<const u32x4*>(xs + (c * 32 + d * 8 + 8) * 2);
+      acc0 = mfma<XDT>(a0, xv0, acc0);
+      acc1 = mfma<XDT>(a1, xv1, acc1);
+    }
+  }
+  return acc0 + acc1;
+}
+
 // ---------------------------------------------------------------------------------
 // The GEMV kernel
 // ---------------------------------------------------------------------------------
@@ -270,127 +359,121 @@ template <int FMT, int XDT>
 __global__ __launch_bounds__(kThreads) void gemv_kernel(const uint8_t* __restrict__ w,
                                                         const void* __restrict__ x,
                                                         void* __restrict__ y, int N, int K, int B,
-                                                        int S, int SPL, int WPT, int fwht_block,
-                                                        int ydt) {
+                                                        int S, int SPL, int fwht_block, int ydt) {
   extern __shared__ __align__(16) uint8_t lds[];
   constexpr int BB = FMT == FB_FMT_GF4 ? fb::kGf4BlockBytes : fb::kE2m1BlockBytes;
   const int GS = ((K >> 7) + 3) >> 2;  // spans per row
   const int T = (N + 15) >> 4;          // row tiles
   const int t0 = (int)((int64_t)blockIdx.x * T / gridDim.x);
   const int t1 = (int)((int64_t)(blockIdx.x + 1) * T / gridDim.x);
-  const int TB = kWaves / WPT;
   const int nsl = SPL * 4;
   const int RS = x_row_stride(nsl);
+  const int nu = (t1 - t0) * SPL;  // units of this workgroup in one slice
   f32x4* slots = reinterpret_cast<f32x4*>(lds + x_lds_bytes(B, K, SPL, fwht_block));
+  int* counter = reinterpret_cast<int*>(slots + (size_t)nu * 4 * B);
+
+  uint8_t* zeros = reinterpret_cast<uint8_t*>(counter) + 16;  // 256 zero bytes
 
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform: SGPR math
   const int lane = threadIdx.x & 63;
-  const int ts = wave / WPT;            // tile slot
-  const int ph = wave - ts * WPT;       // span phase
-  const int col = lane & 15;            // batch column / row within tile
-  const int q = lane >> 4;              // K-quarter of the span / output row group
-  const int xb = col < B ? col : 0;     // columns >= B duplicate column 0 (unused)
-  const int nj = (SPL - ph + WPT - 1) / WPT;  // spans of a tile this wave takes (WPT <= SPL)
-  const int tw0 = t0 + ts;
-  const int nbw = tw0 < t1 ? (t1 - 1 - tw0) / TB + 1 : 0;  // batches with a tile for us
-  const int nunits = nbw * nj;
+  const int col = lane & 15;  // batch column / row within tile
+  const int q = lane >> 4;    // K-quarter of the span / output row group
+  // MFMA columns >= B multiply zeros (read from one 256-byte block whatever the span):
+  // their results are not used, and zeros keep the matrix core from switching.
+  const uint8_t* xl = col < B ? lds + col * RS + q * kSliceBytes : zeros;
+  const int xspan = col < B ? 4 * kSliceBytes : 0;  // x bytes per span for this lane
 
-  // byte offset of the block of unit v (slice s) in the weight stream
-  auto unit_off = [&](int s, int v) -> unsigned {
-    const int bt = v / nj;
-    const int j = ph + (v - bt * nj) * WPT;
-    return (unsigned)(((int64_t)(tw0 + bt * TB) * GS + s * SPL + j) * BB);
+  // Unit u of a slice is span u % SPL of tile t0 + u / SPL.  After two fixed units per
+  // wave, the waves take units from the workgroup's LDS counter, so a wave that the SIMD's
+  // issue order favours does more of them and all waves finish together.
+  // lane 0 holds the fetched index; it is made uniform when it is used, a step later, so
+  // the atomic's latency is hidden.
+  auto grab = [&]() -> int {
+    int u = 0;
+    if (lane == 0)
+      u = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    return u;
+  };
+  auto unit_off = [&](int s, int u) -> unsigned {
+    const int lt = u / SPL;
+    return (unsigned)(((int64_t)(t0 + lt) * GS + s * SPL + (u - lt * SPL)) * BB);
   };
 
-  f32x4 acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
-  const uint8_t* xl = lds + xb * RS + q * kSliceBytes;
-
-  // Decode + MFMA of unit v (slice s) from record r; parks the tile partial in LDS when
-  // this wave is done with the tile.
-  auto process = [&](const Rec<FMT>& r, int s, int v) {
-    const int bt = v / nj;
-    const int jj = v - bt * nj;
-    const uint8_t* xs = xl + (ph + jj * WPT) * 4 * kSliceBytes;
-#pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      float scale = 1.0f;
-      if constexpr (FMT == FB_FMT_E2M1)
-        scale = __builtin_bit_cast(float, ((r.t0.x >> (8 * c)) & 0xFFu) << 23);
-#pragma unroll
-      for (int d = 0; d < 4; d += 2) {
-        u32x4 a0, a1;
-        if constexpr (FMT == FB_FMT_GF4) {
-          gf4_decode16(r.nib[c][d], r.nib[c][d + 1], r.t0, r.t1, a0, a1);
-        } else {
-          a0 = e2m1_decode8<XDT>(r.nib[c][d], scale);
-          a1 = e2m1_decode8<XDT>(r.nib[c][d + 1], scale);
-        }
-        const u32x4 xv0 = *reinterpret_cast<const u32x4*>(xs + (c * 32 + d * 8) * 2);
-        const u32x4 xv1 = *reinterpret_cast<const u32x4*>(xs + (c * 32 + d * 8 + 8) * 2);
-        acc0 = mfma<XDT>(a0, xv0, acc0);
-        acc1 = mfma<XDT>(a1, xv1, acc1);
-      }
-    }
-    if (jj == nj - 1) {  // this wave's share of tile tw0 + bt*TB is done
-      if (col < B) {
-        f32x4* sl = slots + ((bt * kWaves + wave) * 4 + q) * B + col;
-        if (s == 0)
-          *sl = acc0 + acc1;
-        else
-          *sl += acc0 + acc1;
-      }
-      acc0 = f32x4{0.f, 0.f, 0.f, 0.f};
-      acc1 = acc0;
+  // Decode + MFMA of unit u (slice s) from record r; the unit's partial sums go to its own
+  // LDS slot (added to the earlier slices' value), so the final sum has a fixed order
+  // whichever wave did the unit.
+  auto process = [&](const Rec<FMT>& r, int s, int u) {
+    const f32x4 acc = unit_partial<FMT, XDT>(r, xl + (u % SPL) * xspan);
+    if (col < B) {
+      f32x4* sl = slots + ((size_t)u * 4 + q) * B + col;
+      if (s == 0)
+        *sl = acc;
+      else
+        *sl += acc;
     }
   };
 
-  // Ring of kDepth record buffers: loads run kDepth-1 units ahead of the decode.  All
-  // loads are unconditional (past the last unit they use the empty resource), so the
-  // wait before each unit covers exactly that unit's loads.
-  Rec<FMT> ring[kDepth];
-  auto issue = [&](int s, int v, Rec<FMT>& r) {
-    const bool real = v < nunits;  // wave-uniform: no branch, only the range changes
+  // Two record buffers: the loads of the next unit are in flight while one is decoded.
+  // Loads past the last unit use the empty resource (no branch, no traffic).  Unit
+  // indices only grow, so the first index past the end stops the wave.
+  Rec<FMT> ring[2];
+  auto issue = [&](int s, int u, Rec<FMT>& r) {
+    const bool real = u < nu;  // wave-uniform: only the range changes
     const rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(w), (short)0,
                                                         real ? 0x7fffffff : 0, kRsrcWord3);
-    load_rec<FMT>(rs, real ? unit_off(s, v) : 0u, lane, r);
+    load_rec<FMT>(rs, real ? unit_off(s, u) : 0u, lane, r);
   };
+  const uint16_t* xg = static_cast<const uint16_t*>(x);
+  // Each wave's first two units are static (wave, wave + kWaves); the counter hands out
+  // the rest.
+  if (threadIdx.x == 0) *counter = 2 * kWaves;
+  if (threadIdx.x < 16) reinterpret_cast<u32x4*>(zeros)[threadIdx.x] = u32x4{0u, 0u, 0u, 0u};
   for (int s = 0; s < S; ++s) {
-#pragma unroll
-    for (int i = 0; i < kDepth - 1; ++i) issue(s, i, ring[i]);
     const int k0 = s * SPL * 512;
-    if (fwht_block) {
-      const int kw = min(K - k0, nsl * 128);
-      stage_fwht(lds, reinterpret_cast<float*>(lds + B * RS), static_cast<const _Float16*>(x), K,
-                 B, k0, kw, nsl, RS, fwht_block);
-    } else {
-      stage_plain(lds, static_cast<const uint16_t*>(x), K, B, k0, nsl, RS);
-    }
-    __syncthreads();
-    for (int v = 0; v < nunits; v += kDepth) {
-#pragma unroll
-      for (int i = 0; i < kDepth; ++i) {
-        issue(s, v + i + kDepth - 1, ring[(i + kDepth - 1) % kDepth]);
-        __builtin_amdgcn_sched_barrier(0);  // keep the prefetch ahead of the compute
-        if (v + i < nunits) process(ring[i], s, v + i);
-      }
+    const int kw = min(K - k0, nsl * 128);  // rotated width of the slice
+    const int per_row = fwht_block ? kw / 8 : nsl * 16;  // x chunks per batch row
+    XPre xp;
+    x_preload(xp, xg, K, k0, per_row, B * per_row);
+    int u0 = wave, u1 = wave + kWaves;
+    issue(s, u0, ring[0]);
+    if (fwht_block)
+      stage_fwht(lds, reinterpret_cast<float*>(lds + B * RS), xp, xg, K, B, k0, kw, nsl, RS,
+                 fwht_block);
+    else
+      stage_plain(lds, xp, xg, K, B, k0, nsl, RS);
+    __syncthreads();  // x staged, counter set
+    issue(s, u1, ring[1]);
+    __builtin_amdgcn_sched_barrier(0);  // keep the prefetch ahead of the compute
+    if (u0 < nu) process(ring[0], s, u0);
+    int un = grab();
+    for (;;) {
+      u0 = __builtin_amdgcn_readfirstlane(un);
+      un = grab();
+      issue(s, u0, ring[0]);
+      __builtin_amdgcn_sched_barrier(0);
+      if (u1 >= nu) break;
+      process(ring[1], s, u1);
+      u1 = __builtin_amdgcn_readfirstlane(un);
+      un = grab();
+      issue(s, u1, ring[1]);
+      __builtin_amdgcn_sched_barrier(0);
+      if (u0 >= nu) break;
+      process(ring[0], s, u0);
     }
     __syncthreads();  // slice done: x may be restaged, slots are complete
+    if (threadIdx.x == 0) *counter = 2 * kWaves;
   }
 
-  // y[col][row] = sum over the WPT waves of the tile slot, in phase order
+  // y[col][row] = sum over the spans of the tile, in span order
   const int nt = t1 - t0;
   for (int e = threadIdx.x; e < nt * 16 * B; e += kThreads) {
     const int c = e % B;
     const int r = (e / B) & 15;
-    const int tl = e / (16 * B);
-    const int bt = tl / TB;
-    const int tsl = tl - bt * TB;
-    const int row = (t0 + tl) * 16 + r;
+    const int lt = e / (16 * B);
+    const int row = (t0 + lt) * 16 + r;
+    const f32x4* sl = slots + ((size_t)lt * SPL * 4 + (r >> 2)) * B + c;
     float sum = 0.0f;
-    for (int p2 = 0; p2 < WPT; ++p2) {
-      const f32x4 v = slots[((bt * kWaves + tsl * WPT + p2) * 4 + (r >> 2)) * B + c];
-      sum += v[r & 3];
-    }
+    for (int j = 0; j < SPL; ++j) sum += sl[(size_t)j * 4 * B][r & 3];
     if (row < N) store_y(y, (int64_t)c * N + row, sum, ydt);
   }
 }
@@ -472,44 +555,36 @@ bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) ==
 struct Plan {
   int S = 0;     // K-slices staged one after the other
   int SPL = 0;   // spans per slice
-  int WPT = 0;   // waves per tile
   int grid = 0;  // workgroups
   size_t lds = 0;
 };
 
-// Picks (WPT, S, grid) minimising the most units any wave streams, subject to the LDS
-// limit; ties prefer fewer slices.
+// LDS of one workgroup: staged x, one partial-sum slot per unit, the unit counter, and
+// the zero block that MFMA columns past the batch read.
+size_t plan_lds(const fb_shape_t* s, int tpw, int SPL) {
+  return (size_t)x_lds_bytes(s->B, s->K, SPL, s->fwht_block) + (size_t)tpw * SPL * 64 * s->B +
+         16 + 256;
+}
+
+// One workgroup per CU (up to the number of row tiles); the fewest K-slices whose LDS fits.
 bool make_plan(const fb_shape_t* s, int cus, Plan& pl) {
   const int GS = (s->K / 128 + 3) / 4;
   const int T = (s->N + 15) / 16;
   const int grid = std::max(1, std::min(T, cus));
   const int tpw = (T + grid - 1) / grid;  // most tiles a workgroup owns
-  int64_t best = -1;
-  for (int WPT = 16; WPT >= 1; WPT /= 2) {
-    if (WPT > GS && WPT > 1) continue;
-    const int TB = kWaves / WPT;
-    const int nb = (tpw + TB - 1) / TB;
-    for (int S = 1; S <= GS; ++S) {
-      if (GS % S) continue;
-      const int SPL = GS / S;
-      if (WPT > SPL) continue;
-      if (s->fwht_block && S > 1 && (SPL * 512) % s->fwht_block) continue;
-      const size_t lds = (size_t)x_lds_bytes(s->B, s->K, SPL, s->fwht_block) +
-                         (size_t)nb * kWaves * 4 * s->B * 16;
-      if (lds > (size_t)kLdsLimit) continue;
-      const int64_t cost = (int64_t)nb * ((SPL + WPT - 1) / WPT) * S;
-      if (best < 0 || cost < best) {
-        best = cost;
-        pl.S = S;
-        pl.SPL = SPL;
-        pl.WPT = WPT;
-        pl.grid = grid;
-        pl.lds = lds;
-      }
-      break;  // more slices only add staging work at the same cost
-    }
+  for (int S = 1; S <= GS; ++S) {
+    if (GS % S) continue;
+    const int SPL = GS / S;
+    if (s->fwht_block && S > 1 && (SPL * 512) % s->fwht_block) continue;
+    const size_t lds = plan_lds(s, tpw, SPL);
+    if (lds > (size_t)kLdsLimit) continue;
+    pl.S = S;
+    pl.SPL = SPL;
+    pl.grid = grid;
+    pl.lds = lds;
+    return true;
   }
-  return best >= 0;
+  return false;
 }
 
 int device_cus() {
@@ -531,7 +606,7 @@ int launch_gemv(const void* wdev, const void* x, void* y, const fb_shape_t* s, c
   }
   hipLaunchKernelGGL(kern, dim3(pl.grid), dim3(kThreads), pl.lds, stream,
                      static_cast<const uint8_t*>(wdev), x, y, s->N, s->K, s->B, pl.S, pl.SPL,
-                     pl.WPT, s->fwht_block, s->y_dtype);
+                     s->fwht_block, s->y_dtype);
   return hipGetLastError() == hipSuccess ? FB_OK : FB_ERR_HIP;
 }
 
