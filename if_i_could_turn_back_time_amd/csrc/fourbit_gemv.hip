@@ -58,6 +58,14 @@ __device__ __forceinline__ void store_y(void* y, int64_t idx, float v, int ydt) 
   }
 }
 
+// n / d for 0 <= n < 2^30 and 1 <= d < 2^16, with m = div_magic(d) from the host: the high
+// half of n * m is n / d or one less, and one compare fixes it.  Used instead of integer
+// division, which is a long instruction sequence on this GPU.
+__device__ __forceinline__ int fdiv(int n, int d, unsigned m) {
+  const int q = (int)__umulhi((unsigned)n, m);
+  return (q + 1) * d <= n ? q + 1 : q;
+}
+
 // GF4 decode of one 32-bit word (8 codes, layout order) into 4 fp16 pairs in element
 // order (e0,e1) (e2,e3) (e4,e5) (e6,e7).  tl/th: lo/hi byte-plane tables
 // {A'[0..3], A'[4..7], B'[0..3], B'[4..7]}.
@@ -204,25 +212,28 @@ __device__ __forceinline__ u32x4 x_load8(const uint16_t* __restrict__ x, int K, 
 
 // Chunk t of a slice is batch row t / per_row, values k0 + 8 * (t % per_row) ...; thread
 // j * kThreads + threadIdx.x of the workgroup takes chunk t in step j.
+// row_of(t) = t / per_row.
+template <typename RowOf>
 __device__ __forceinline__ void x_preload(XPre& xp, const uint16_t* __restrict__ x, int K, int k0,
-                                          int per_row, int nchunks) {
+                                          int per_row, int nchunks, RowOf row_of) {
 #pragma unroll
   for (int j = 0; j < kXPre; ++j) {
     const int t = threadIdx.x + j * kThreads;
     if (t < nchunks) {
-      const int b = t / per_row;
+      const int b = row_of(t);
       xp.v[j] = x_load8(x, K, b, k0 + (t - b * per_row) * 8);
     }
   }
 }
 
 // Plain staging: chunk t lands in its 128-value group of the slice layout.
+template <typename RowOf>
 __device__ void stage_plain(uint8_t* lds, const XPre& xp, const uint16_t* __restrict__ x, int K,
-                            int B, int k0, int nsl, int RS) {
+                            int B, int k0, int nsl, int RS, RowOf row_of) {
   const int per_row = nsl * 16;
   const int n = B * per_row;
   auto put = [&](int t, const u32x4& v) {
-    const int b = t / per_row;
+    const int b = row_of(t);
     const int c8 = t - b * per_row;
     *reinterpret_cast<u32x4*>(lds + b * RS + (c8 >> 4) * kSliceBytes + (c8 & 15) * 16) = v;
   };
@@ -232,7 +243,7 @@ __device__ void stage_plain(uint8_t* lds, const XPre& xp, const uint16_t* __rest
     if (t < n) put(t, xp.v[j]);
   }
   for (int t = threadIdx.x + kXPre * kThreads; t < n; t += kThreads) {
-    const int b = t / per_row;
+    const int b = row_of(t);
     put(t, x_load8(x, K, b, k0 + (t - b * per_row) * 8));
   }
 }
@@ -320,17 +331,6 @@ __device__ __forceinline__ f32x4 unit_partial(const Rec<FMT>& r, const uint8_t* 
   f32x4 acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int c = 0; c < 4; ++c) {
-    // The SIMD issues the oldest ready wave first; raising the priority as a unit
-    // progresses lets the waves that are furthest into their unit finish it first, so
-    // the units of young waves do not trail behind at the end.
-    if (c == 0)
-      __builtin_amdgcn_s_setprio(0);
-    else if (c == 1)
-      __builtin_amdgcn_s_setprio(1);
-    else if (c == 2)
-      __builtin_amdgcn_s_setprio(2);
-    else
-      __builtin_amdgcn_s_setprio(3);
     float scale = 1.0f;
     if constexpr (FMT == FB_FMT_E2M1)
       scale = __builtin_bit_cast(float, ((r.t0.x >> (8 * c)) & 0xFFu) << 23);
@@ -355,21 +355,24 @@ __device__ __forceinline__ f32x4 unit_partial(const Rec<FMT>& r, const uint8_t* 
 // ---------------------------------------------------------------------------------
 // The GEMV kernel
 // ---------------------------------------------------------------------------------
+// Arguments are ordered so that the first 16 dwords, which arrive preloaded in SGPRs, hold
+// everything the first loads need.  tq, tr: row tiles per workgroup = tq (+1 for the first
+// tr workgroups); GS: 512-element spans per row; RS: LDS bytes per staged x row; spl_m:
+// div_magic(SPL); xbytes: LDS bytes of staged x (the partial-sum slots follow).
 template <int FMT, int XDT>
-__global__ __launch_bounds__(kThreads) void gemv_kernel(const uint8_t* __restrict__ w,
-                                                        const void* __restrict__ x,
-                                                        void* __restrict__ y, int N, int K, int B,
-                                                        int S, int SPL, int fwht_block, int ydt) {
+__global__ __launch_bounds__(kThreads) void gemv_kernel(
+    const uint8_t* __restrict__ w, const void* __restrict__ x, void* __restrict__ y, int K, int B,
+    int SPL, int GS, int tq, int tr, int RS, unsigned spl_m, int S, int N, int fwht_block,
+    int ydt, int xbytes) {
   extern __shared__ __align__(16) uint8_t lds[];
   constexpr int BB = FMT == FB_FMT_GF4 ? fb::kGf4BlockBytes : fb::kE2m1BlockBytes;
-  const int GS = ((K >> 7) + 3) >> 2;  // spans per row
-  const int T = (N + 15) >> 4;          // row tiles
-  const int t0 = (int)((int64_t)blockIdx.x * T / gridDim.x);
-  const int t1 = (int)((int64_t)(blockIdx.x + 1) * T / gridDim.x);
+  const int g = blockIdx.x;
+  const int t0 = g * tq + min(g, tr);
+  const int t1 = t0 + tq + (g < tr ? 1 : 0);
   const int nsl = SPL * 4;
-  const int RS = x_row_stride(nsl);
   const int nu = (t1 - t0) * SPL;  // units of this workgroup in one slice
-  f32x4* slots = reinterpret_cast<f32x4*>(lds + x_lds_bytes(B, K, SPL, fwht_block));
+  auto span_of = [&](int u) { return u - fdiv(u, SPL, spl_m) * SPL; };
+  f32x4* slots = reinterpret_cast<f32x4*>(lds + xbytes);
   int* counter = reinterpret_cast<int*>(slots + (size_t)nu * 4 * B);
 
   uint8_t* zeros = reinterpret_cast<uint8_t*>(counter) + 16;  // 256 zero bytes
@@ -395,7 +398,7 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(const uint8_t* __restric
     return u;
   };
   auto unit_off = [&](int s, int u) -> unsigned {
-    const int lt = u / SPL;
+    const int lt = fdiv(u, SPL, spl_m);
     return (unsigned)(((int64_t)(t0 + lt) * GS + s * SPL + (u - lt * SPL)) * BB);
   };
 
@@ -403,7 +406,7 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(const uint8_t* __restric
   // LDS slot (added to the earlier slices' value), so the final sum has a fixed order
   // whichever wave did the unit.
   auto process = [&](const Rec<FMT>& r, int s, int u) {
-    const f32x4 acc = unit_partial<FMT, XDT>(r, xl + (u % SPL) * xspan);
+    const f32x4 acc = unit_partial<FMT, XDT>(r, xl + span_of(u) * xspan);
     if (col < B) {
       f32x4* sl = slots + ((size_t)u * 4 + q) * B + col;
       if (s == 0)
@@ -432,15 +435,17 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(const uint8_t* __restric
     const int k0 = s * SPL * 512;
     const int kw = min(K - k0, nsl * 128);  // rotated width of the slice
     const int per_row = fwht_block ? kw / 8 : nsl * 16;  // x chunks per batch row
+    // batch row of x chunk t: per_row = 64 SPL without a rotation
+    auto row_of = [&](int t) { return fwht_block ? t / per_row : fdiv(t >> 6, SPL, spl_m); };
     XPre xp;
-    x_preload(xp, xg, K, k0, per_row, B * per_row);
+    x_preload(xp, xg, K, k0, per_row, B * per_row, row_of);
     int u0 = wave, u1 = wave + kWaves;
     issue(s, u0, ring[0]);
     if (fwht_block)
       stage_fwht(lds, reinterpret_cast<float*>(lds + B * RS), xp, xg, K, B, k0, kw, nsl, RS,
                  fwht_block);
     else
-      stage_plain(lds, xp, xg, K, B, k0, nsl, RS);
+      stage_plain(lds, xp, xg, K, B, k0, nsl, RS, row_of);
     __syncthreads();  // x staged, counter set
     issue(s, u1, ring[1]);
     __builtin_amdgcn_sched_barrier(0);  // keep the prefetch ahead of the compute
@@ -466,10 +471,11 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(const uint8_t* __restric
 
   // y[col][row] = sum over the spans of the tile, in span order
   const int nt = t1 - t0;
-  for (int e = threadIdx.x; e < nt * 16 * B; e += kThreads) {
-    const int c = e % B;
-    const int r = (e / B) & 15;
-    const int lt = e / (16 * B);
+  for (int e = threadIdx.x; e < nt * 256; e += kThreads) {
+    const int c = e & 15;
+    if (c >= B) continue;
+    const int r = (e >> 4) & 15;
+    const int lt = e >> 8;
     const int row = (t0 + lt) * 16 + r;
     const f32x4* sl = slots + ((size_t)lt * SPL * 4 + (r >> 2)) * B + c;
     float sum = 0.0f;
@@ -556,8 +562,14 @@ struct Plan {
   int S = 0;     // K-slices staged one after the other
   int SPL = 0;   // spans per slice
   int grid = 0;  // workgroups
+  int GS = 0;    // spans per row
+  int tq = 0;    // row tiles per workgroup (the first tr workgroups take one more)
+  int tr = 0;
   size_t lds = 0;
 };
+
+// Multiplier of fdiv: floor(2^32 / d), or 2^32 - 1 for d = 1.
+unsigned div_magic(int d) { return d == 1 ? 0xFFFFFFFFu : (unsigned)((1ull << 32) / (unsigned)d); }
 
 // LDS of one workgroup: staged x, one partial-sum slot per unit, the unit counter, and
 // the zero block that MFMA columns past the batch read.
@@ -581,6 +593,9 @@ bool make_plan(const fb_shape_t* s, int cus, Plan& pl) {
     pl.S = S;
     pl.SPL = SPL;
     pl.grid = grid;
+    pl.GS = GS;
+    pl.tq = T / grid;
+    pl.tr = T % grid;
     pl.lds = lds;
     return true;
   }
@@ -605,8 +620,9 @@ int launch_gemv(const void* wdev, const void* x, void* y, const fb_shape_t* s, c
     attr_set.store(true, std::memory_order_release);
   }
   hipLaunchKernelGGL(kern, dim3(pl.grid), dim3(kThreads), pl.lds, stream,
-                     static_cast<const uint8_t*>(wdev), x, y, s->N, s->K, s->B, pl.S, pl.SPL,
-                     s->fwht_block, s->y_dtype);
+                     static_cast<const uint8_t*>(wdev), x, y, s->K, s->B, pl.SPL, pl.GS, pl.tq,
+                     pl.tr, x_row_stride(pl.SPL * 4), div_magic(pl.SPL), pl.S, s->N,
+                     s->fwht_block, s->y_dtype, x_lds_bytes(s->B, s->K, pl.SPL, s->fwht_block));
   return hipGetLastError() == hipSuccess ? FB_OK : FB_ERR_HIP;
 }
 

@@ -219,3 +219,22 @@ def test_workspace_contract():
     buf = ctypes.c_char_p(b"x" * 64)
     big = C.make_shape(8192, 28672, 17)
     assert C.lib().fb_gemv(buf, buf, buf, ctypes.byref(big), None, 0, None) == -9
+
+
+def test_magic_division_identity():
+    """The GEMV kernel divides by runtime values with one multiply-high and one compare:
+    q = hi32(n * m), m = floor(2^32 / d) (2^32 - 1 for d = 1), then q + 1 if (q + 1) d <= n.
+    Exhaustive over small n and d, sampled up to n < 2^30."""
+    import random
+    rnd = random.Random(5)
+
+    def magic(d):
+        return 0xFFFFFFFF if d == 1 else (1 << 32) // d
+
+    def fdiv(n, d):
+        q = (n * magic(d)) >> 32
+        return q + 1 if (q + 1) * d <= n else q
+
+    for d in list(range(1, 257)) + [1000, 4093, 32767, 32768, 65535]:
+        for n in list(range(0, 3000)) + [rnd.randrange(0, 1 << 30) for _ in range(300)]:
+            assert fdiv(n, d) == n // d, (n, d)
