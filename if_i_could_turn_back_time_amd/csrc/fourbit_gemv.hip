@@ -20,6 +20,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <cmath>
 #include <atomic>
 
 #include "fourbit.h"
@@ -215,10 +216,10 @@ __device__ __forceinline__ u32x4 x_load8(const uint16_t* __restrict__ x, int K, 
 // row_of(t) = t / per_row.
 template <typename RowOf>
 __device__ __forceinline__ void x_preload(XPre& xp, const uint16_t* __restrict__ x, int K, int k0,
-                                          int per_row, int nchunks, RowOf row_of) {
+                                          int per_row, int nchunks, RowOf row_of, int tid) {
 #pragma unroll
   for (int j = 0; j < kXPre; ++j) {
-    const int t = threadIdx.x + j * kThreads;
+    const int t = tid + j * kThreads;
     if (t < nchunks) {
       const int b = row_of(t);
       xp.v[j] = x_load8(x, K, b, k0 + (t - b * per_row) * 8);
@@ -229,7 +230,7 @@ __device__ __forceinline__ void x_preload(XPre& xp, const uint16_t* __restrict__
 // Plain staging: chunk t lands in its 128-value group of the slice layout.
 template <typename RowOf>
 __device__ void stage_plain(uint8_t* lds, const XPre& xp, const uint16_t* __restrict__ x, int K,
-                            int B, int k0, int nsl, int RS, RowOf row_of) {
+                            int B, int k0, int nsl, int RS, RowOf row_of, int tid) {
   const int per_row = nsl * 16;
   const int n = B * per_row;
   auto put = [&](int t, const u32x4& v) {
@@ -239,10 +240,10 @@ __device__ void stage_plain(uint8_t* lds, const XPre& xp, const uint16_t* __rest
   };
 #pragma unroll
   for (int j = 0; j < kXPre; ++j) {
-    const int t = threadIdx.x + j * kThreads;
+    const int t = tid + j * kThreads;
     if (t < n) put(t, xp.v[j]);
   }
-  for (int t = threadIdx.x + kXPre * kThreads; t < n; t += kThreads) {
+  for (int t = tid + kXPre * kThreads; t < n; t += kThreads) {
     const int b = row_of(t);
     put(t, x_load8(x, K, b, k0 + (t - b * per_row) * 8));
   }
@@ -252,7 +253,8 @@ __device__ void stage_plain(uint8_t* lds, const XPre& xp, const uint16_t* __rest
 // layout (rounded to fp16).  F: LDS scratch of B*kw floats; kw is a whole number of
 // blocks.  Stages go 4 at a time: a thread owns 16 values spaced h0 apart.
 __device__ void stage_fwht(uint8_t* lds, float* F, const XPre& xp, const uint16_t* __restrict__ x,
-                           int K, int B, int k0, int kw, int nsl, int RS, int fb) {
+                           int K, int B, int k0, int kw, int nsl, int RS, int fb, float sc,
+                           int tid) {
   const int per_row = kw / 8;
   const int n = B * per_row;
   auto put = [&](int t, const u32x4& v) {
@@ -264,10 +266,10 @@ __device__ void stage_fwht(uint8_t* lds, float* F, const XPre& xp, const uint16_
   };
 #pragma unroll
   for (int j = 0; j < kXPre; ++j) {
-    const int t = threadIdx.x + j * kThreads;
+    const int t = tid + j * kThreads;
     if (t < n) put(t, xp.v[j]);
   }
-  for (int t = threadIdx.x + kXPre * kThreads; t < n; t += kThreads) {
+  for (int t = tid + kXPre * kThreads; t < n; t += kThreads) {
     const int b = t / per_row;
     put(t, x_load8(x, K, b, k0 + (t - b * per_row) * 8));
   }
@@ -279,7 +281,7 @@ __device__ void stage_fwht(uint8_t* lds, float* F, const XPre& xp, const uint16_
     const int h0 = 1 << lg_h0;
     const int lg_nhi = lg_fb - lg_h0 - lg_span;
     const int ngroups = (B * kw) >> lg_span;
-    for (int t = threadIdx.x; t < ngroups; t += kThreads) {
+    for (int t = tid; t < ngroups; t += kThreads) {
       const int lo = t & (h0 - 1);
       const int rest = t >> lg_h0;
       const int hi = rest & ((1 << lg_nhi) - 1);
@@ -307,9 +309,8 @@ __device__ void stage_fwht(uint8_t* lds, float* F, const XPre& xp, const uint16_
     }
     __syncthreads();
   }
-  const float sc = 1.0f / __builtin_sqrtf((float)fb);
   const int width = nsl * 128;
-  for (int t = threadIdx.x; t < B * width; t += kThreads) {
+  for (int t = tid; t < B * width; t += kThreads) {
     const int b = t / width;
     const int k = t - b * width;
     const float v = k < kw ? F[b * kw + k] * sc : 0.0f;
@@ -355,15 +356,20 @@ __device__ __forceinline__ f32x4 unit_partial(const Rec<FMT>& r, const uint8_t* 
 // ---------------------------------------------------------------------------------
 // The GEMV kernel
 // ---------------------------------------------------------------------------------
-// Arguments are ordered so that the first 16 dwords, which arrive preloaded in SGPRs, hold
-// everything the first loads need.  tq, tr: row tiles per workgroup = tq (+1 for the first
+// Arguments are ordered so that the first 14 dwords, which arrive preloaded in SGPRs, hold
+// everything the first loads need; y, N, ydt and xbytes come through a scalar load that
+// completes while the first loads are in flight.  tq, tr: row tiles per workgroup = tq (+1 for the first
 // tr workgroups); GS: 512-element spans per row; RS: LDS bytes per staged x row; spl_m:
 // div_magic(SPL); xbytes: LDS bytes of staged x (the partial-sum slots follow).
-template <int FMT, int XDT>
+// MODE: kFlat = one K-slice, no rotation (the common case); kSliced = several K-slices, no
+// rotation; kRotated = rotation of x.  Each is compiled with only the staging it needs, which
+// keeps the kernel short and its registers few.
+enum { kFlat = 0, kSliced = 1, kRotated = 2 };
+template <int FMT, int XDT, int MODE>
 __global__ __launch_bounds__(kThreads) void gemv_kernel(
-    const uint8_t* __restrict__ w, const void* __restrict__ x, void* __restrict__ y, int K, int B,
-    int SPL, int GS, int tq, int tr, int RS, unsigned spl_m, int S, int N, int fwht_block,
-    int ydt, int xbytes) {
+    const uint8_t* __restrict__ w, const void* __restrict__ x, int K, int B, int SPL, int GS,
+    int tq, int tr, unsigned spl_m, int S, int fwht_block, int RS, void* __restrict__ y, int N,
+    int ydt, int xbytes, float fwht_scale) {
   extern __shared__ __align__(16) uint8_t lds[];
   constexpr int BB = FMT == FB_FMT_GF4 ? fb::kGf4BlockBytes : fb::kE2m1BlockBytes;
   const int g = blockIdx.x;
@@ -372,10 +378,12 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(
   const int nsl = SPL * 4;
   const int nu = (t1 - t0) * SPL;  // units of this workgroup in one slice
   auto span_of = [&](int u) { return u - fdiv(u, SPL, spl_m) * SPL; };
-  f32x4* slots = reinterpret_cast<f32x4*>(lds + xbytes);
-  int* counter = reinterpret_cast<int*>(slots + (size_t)nu * 4 * B);
+  // LDS: unit counter (16 B) | zero block (256 B) | staged x (xbytes) | partial-sum slots
+  int* counter = reinterpret_cast<int*>(lds);
+  uint8_t* zeros = lds + 16;
+  uint8_t* xst = lds + 16 + 256;
+  f32x4* slots = reinterpret_cast<f32x4*>(xst + xbytes);
 
-  uint8_t* zeros = reinterpret_cast<uint8_t*>(counter) + 16;  // 256 zero bytes
 
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform: SGPR math
   const int lane = threadIdx.x & 63;
@@ -383,7 +391,7 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(
   const int q = lane >> 4;    // K-quarter of the span / output row group
   // MFMA columns >= B multiply zeros (read from one 256-byte block whatever the span):
   // their results are not used, and zeros keep the matrix core from switching.
-  const uint8_t* xl = col < B ? lds + col * RS + q * kSliceBytes : zeros;
+  const uint8_t* xl = col < B ? xst + col * RS + q * kSliceBytes : zeros;
   const int xspan = col < B ? 4 * kSliceBytes : 0;  // x bytes per span for this lane
 
   // Unit u of a slice is span u % SPL of tile t0 + u / SPL.  After two fixed units per
@@ -429,23 +437,32 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(
   const uint16_t* xg = static_cast<const uint16_t*>(x);
   // Each wave's first two units are static (wave, wave + kWaves); the counter hands out
   // the rest.
-  if (threadIdx.x == 0) *counter = 2 * kWaves;
-  if (threadIdx.x < 16) reinterpret_cast<u32x4*>(zeros)[threadIdx.x] = u32x4{0u, 0u, 0u, 0u};
-  for (int s = 0; s < S; ++s) {
+  constexpr bool rot = MODE == kRotated;
+  const int nslices = MODE == kFlat ? 1 : S;
+  for (int s = 0; s < nslices; ++s) {
     const int k0 = s * SPL * 512;
     const int kw = min(K - k0, nsl * 128);  // rotated width of the slice
-    const int per_row = fwht_block ? kw / 8 : nsl * 16;  // x chunks per batch row
+    const int per_row = rot ? kw / 8 : nsl * 16;  // x chunks per batch row
     // batch row of x chunk t: per_row = 64 SPL without a rotation
-    auto row_of = [&](int t) { return fwht_block ? t / per_row : fdiv(t >> 6, SPL, spl_m); };
+    auto row_of = [&](int t) { return rot ? t / per_row : fdiv(t >> 6, SPL, spl_m); };
+    // With several slices, an opaque copy of the thread index keeps the compiler from
+    // hoisting the staging index math out of the slice loop (it would stay live, in
+    // registers the decode needs, for the whole kernel).
+    int tid = threadIdx.x;
+    if constexpr (MODE != kFlat) asm volatile("" : "+v"(tid));
     XPre xp;
-    x_preload(xp, xg, K, k0, per_row, B * per_row, row_of);
+    x_preload(xp, xg, K, k0, per_row, B * per_row, row_of, tid);
     int u0 = wave, u1 = wave + kWaves;
     issue(s, u0, ring[0]);
-    if (fwht_block)
-      stage_fwht(lds, reinterpret_cast<float*>(lds + B * RS), xp, xg, K, B, k0, kw, nsl, RS,
-                 fwht_block);
+    if (s == 0) {
+      if (threadIdx.x == 0) *counter = 2 * kWaves;
+      if (threadIdx.x < 16) reinterpret_cast<u32x4*>(zeros)[threadIdx.x] = u32x4{0u, 0u, 0u, 0u};
+    }
+    if constexpr (rot)
+      stage_fwht(xst, reinterpret_cast<float*>(xst + B * RS), xp, xg, K, B, k0, kw, nsl, RS,
+                 fwht_block, fwht_scale, tid);
     else
-      stage_plain(lds, xp, xg, K, B, k0, nsl, RS, row_of);
+      stage_plain(xst, xp, xg, K, B, k0, nsl, RS, row_of, tid);
     __syncthreads();  // x staged, counter set
     issue(s, u1, ring[1]);
     __builtin_amdgcn_sched_barrier(0);  // keep the prefetch ahead of the compute
@@ -571,8 +588,8 @@ struct Plan {
 // Multiplier of fdiv: floor(2^32 / d), or 2^32 - 1 for d = 1.
 unsigned div_magic(int d) { return d == 1 ? 0xFFFFFFFFu : (unsigned)((1ull << 32) / (unsigned)d); }
 
-// LDS of one workgroup: staged x, one partial-sum slot per unit, the unit counter, and
-// the zero block that MFMA columns past the batch read.
+// LDS of one workgroup: the unit counter, the zero block that MFMA columns past the batch
+// read, staged x, and one partial-sum slot per unit.
 size_t plan_lds(const fb_shape_t* s, int tpw, int SPL) {
   return (size_t)x_lds_bytes(s->B, s->K, SPL, s->fwht_block) + (size_t)tpw * SPL * 64 * s->B +
          16 + 256;
@@ -608,10 +625,10 @@ int device_cus() {
   return cu_count(dev);
 }
 
-template <int FMT, int XDT>
+template <int FMT, int XDT, int MODE>
 int launch_gemv(const void* wdev, const void* x, void* y, const fb_shape_t* s, const Plan& pl,
                 hipStream_t stream) {
-  auto kern = gemv_kernel<FMT, XDT>;
+  auto kern = gemv_kernel<FMT, XDT, MODE>;
   static std::atomic<bool> attr_set{false};
   if (!attr_set.load(std::memory_order_acquire)) {
     if (hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
@@ -620,10 +637,19 @@ int launch_gemv(const void* wdev, const void* x, void* y, const fb_shape_t* s, c
     attr_set.store(true, std::memory_order_release);
   }
   hipLaunchKernelGGL(kern, dim3(pl.grid), dim3(kThreads), pl.lds, stream,
-                     static_cast<const uint8_t*>(wdev), x, y, s->K, s->B, pl.SPL, pl.GS, pl.tq,
-                     pl.tr, x_row_stride(pl.SPL * 4), div_magic(pl.SPL), pl.S, s->N,
-                     s->fwht_block, s->y_dtype, x_lds_bytes(s->B, s->K, pl.SPL, s->fwht_block));
+                     static_cast<const uint8_t*>(wdev), x, s->K, s->B, pl.SPL, pl.GS, pl.tq,
+                     pl.tr, div_magic(pl.SPL), pl.S, s->fwht_block, x_row_stride(pl.SPL * 4), y,
+                     s->N, s->y_dtype, x_lds_bytes(s->B, s->K, pl.SPL, s->fwht_block),
+                     s->fwht_block ? 1.0f / std::sqrt((float)s->fwht_block) : 1.0f);
   return hipGetLastError() == hipSuccess ? FB_OK : FB_ERR_HIP;
+}
+
+template <int FMT, int XDT>
+int launch_mode(int mode, const void* wdev, const void* x, void* y, const fb_shape_t* s,
+                const Plan& pl, hipStream_t stream) {
+  if (mode == kFlat) return launch_gemv<FMT, XDT, kFlat>(wdev, x, y, s, pl, stream);
+  if (mode == kSliced) return launch_gemv<FMT, XDT, kSliced>(wdev, x, y, s, pl, stream);
+  return launch_gemv<FMT, XDT, kRotated>(wdev, x, y, s, pl, stream);
 }
 
 }  // namespace
@@ -649,10 +675,11 @@ int fb_gemv(const void* wdev, const void* x, void* y, const fb_shape_t* s, void*
   Plan pl;
   if (!make_plan(s, device_cus(), pl)) return FB_ERR_LDS;
   hipStream_t hs = static_cast<hipStream_t>(stream);
-  if (s->fmt == FB_FMT_GF4) return launch_gemv<FB_FMT_GF4, FB_DT_F16>(wdev, x, y, s, pl, hs);
+  const int mode = s->fwht_block ? kRotated : pl.S > 1 ? kSliced : kFlat;
+  if (s->fmt == FB_FMT_GF4) return launch_mode<FB_FMT_GF4, FB_DT_F16>(mode, wdev, x, y, s, pl, hs);
   if (s->x_dtype == FB_DT_BF16)
-    return launch_gemv<FB_FMT_E2M1, FB_DT_BF16>(wdev, x, y, s, pl, hs);
-  return launch_gemv<FB_FMT_E2M1, FB_DT_F16>(wdev, x, y, s, pl, hs);
+    return launch_mode<FB_FMT_E2M1, FB_DT_BF16>(mode, wdev, x, y, s, pl, hs);
+  return launch_mode<FB_FMT_E2M1, FB_DT_F16>(mode, wdev, x, y, s, pl, hs);
 }
 
 int fb_dequant(const void* wdev, void* w_out, int32_t out_dtype, const fb_shape_t* s,
