@@ -48,6 +48,16 @@ WORKLOADS = {
     "gf4fwht_k4096_n4096_b1": ("gf4", 4096, 4096, 1, "cfg1", True),
     "gf4fwht_k4096_n11008_b1": ("gf4", 4096, 11008, 1, "cfg1", True),
     "gf4fwht_k11008_n4096_b1": ("gf4", 11008, 4096, 1, "cfg1", True),
+    "gf4_k28672_n8192_b4": ("gf4", 28672, 8192, 4, "cfg4", False),
+    # small-batch dense contraction (batch 8 / 16): E2M1 as config 2, GF4 as config 1
+    "e2m1_k8192_n8192_b8": ("e2m1", 8192, 8192, 8, "cfg2", False),
+    "e2m1_k8192_n8192_b16": ("e2m1", 8192, 8192, 16, "cfg2", False),
+    "e2m1_k8192_n28672_b8": ("e2m1", 8192, 28672, 8, "cfg2", False),
+    "e2m1_k8192_n28672_b16": ("e2m1", 8192, 28672, 16, "cfg2", False),
+    "gf4_k8192_n8192_b8": ("gf4", 8192, 8192, 8, "cfg1", False),
+    "gf4_k8192_n8192_b16": ("gf4", 8192, 8192, 16, "cfg1", False),
+    "gf4_k8192_n28672_b8": ("gf4", 8192, 28672, 8, "cfg1", False),
+    "gf4_k8192_n28672_b16": ("gf4", 8192, 28672, 16, "cfg1", False),
 }
 DEFAULT = "gf4_k8192_n28672_b1"
 
@@ -212,13 +222,22 @@ def load_traffic(name: str):
 
 
 def run_workload(name: str, steps: int, warmup: int, want_cpu: bool, check: bool = True,
-                 warm: bool = False):
+                 warm: bool = False, cache: dict | None = None):
+    """cache: packed weights by (fmt, K, N, kind, rotation), reused across batch sizes (the
+    weights are drawn before the activations, so they do not depend on the batch)."""
     fmt, K, N, B, kind, fwht = WORKLOADS[name]
     xdt = torch.float16 if fmt == "gf4" else torch.bfloat16
     w, x = synth(kind, N, K, B, xdt)
     fb = fwht_block_for(K) if fwht else 0
+    key = (fmt, K, N, kind, fb)
     t = time.perf_counter()
-    pw = PackedWeight.quantize(w, fmt, fwht_block=fb, device="cuda:0")
+    if cache is not None and key in cache:
+        pw = cache[key]
+    else:
+        pw = PackedWeight.quantize(w, fmt, fwht_block=fb, device="cuda:0")
+        if cache is not None:
+            cache.clear()  # one layer's packed weights resident at a time
+            cache[key] = pw
     pack_s = time.perf_counter() - t
     del w
     xd = x.to("cuda:0")
@@ -292,12 +311,14 @@ def main():
 
     if args.sweep:
         Path(args.sweep_out).parent.mkdir(parents=True, exist_ok=True)
+        cache = {}
+        order = sorted(WORKLOADS, key=lambda n: WORKLOADS[n][:3] + WORKLOADS[n][4:])
         with open(args.sweep_out, "w") as f:
-            for name in WORKLOADS:
+            for name in order:
                 if name == args.workload:
                     continue
                 rec, pw = run_workload(name, max(50, args.steps // 2), args.warmup, False,
-                                       warm=args.warm)
+                                       warm=args.warm, cache=cache)
                 del pw
                 torch.cuda.empty_cache()
                 f.write(json.dumps(rec) + "\n")
