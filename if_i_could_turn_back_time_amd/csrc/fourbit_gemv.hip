@@ -250,78 +250,147 @@ __device__ void stage_plain(uint8_t* lds, const XPre& xp, const uint16_t* __rest
 }
 
 // Blockwise normalised FWHT (fp32 butterflies) of x[b, k0 : k0+kw] into the staged
-// layout (rounded to fp16).  F: LDS scratch of B*kw floats; kw is a whole number of
-// blocks.  Stages go 4 at a time: a thread owns 16 values spaced h0 apart.
-__device__ void stage_fwht(uint8_t* lds, float* F, const XPre& xp, const uint16_t* __restrict__ x,
+// layout (rounded to fp16); kw is a whole number of blocks of fb.
+//  - Stages 0..7 run in registers.  The B*kw values are cut into 256-value sub-blocks,
+//    taken by the waves in turn (sub-block i by wave i % kWaves); lane l holds values
+//    4l..4l+3: stages 0-1 are in-lane, stages 2-7 pair lanes l and l ^ 2^(s-2).
+//    The x of a wave's first kXPre sub-blocks is loaded by rot_preload before the slice's
+//    weight loads are issued.
+//  - Blocks larger than 256 go through LDS (F: B*kw floats) once: each 4096-value piece is
+//    read back with value e = (16w + l % 16) + 256 (r + 4 (l / 16)) in wave w, lane l,
+//    register r, so stages 8-9 are in-lane and stages 10-11 pair lanes l and l ^ 16, 32.
+// Staged positions k >= kw (up to the slice width) are zero.
+struct XRot {
+  uint2 v[kXPre];
+};
+
+__device__ __forceinline__ void rot_preload(XRot& xr, const uint16_t* __restrict__ x, int K,
+                                            int B, int k0, int kw, int tid) {
+  const int wave = tid >> 6, lane = tid & 63;
+  const int nsb = (kw + 255) >> 8;
+#pragma unroll
+  for (int i = 0; i < kXPre; ++i) {
+    const int sb = wave + i * kWaves;  // flat sub-block index over (row, sub-block)
+    if (sb < B * nsb) {
+      const int b = sb / nsb;
+      const int k = (sb - b * nsb) * 256 + lane * 4;
+      xr.v[i] = k < kw ? *reinterpret_cast<const uint2*>(x + (int64_t)b * K + k0 + k)
+                       : uint2{0u, 0u};
+    }
+  }
+}
+
+__device__ void stage_fwht(uint8_t* lds, float* F, const XRot& xr, const uint16_t* __restrict__ x,
                            int K, int B, int k0, int kw, int nsl, int RS, int fb, float sc,
                            int tid) {
-  const int per_row = kw / 8;
-  const int n = B * per_row;
-  auto put = [&](int t, const u32x4& v) {
-    const int b = t / per_row;
-    float* f = F + b * kw + (t - b * per_row) * 8;
-    const half8_t h = __builtin_bit_cast(half8_t, v);
-#pragma unroll
-    for (int e = 0; e < 8; ++e) f[e] = (float)h[e];
-  };
-#pragma unroll
-  for (int j = 0; j < kXPre; ++j) {
-    const int t = tid + j * kThreads;
-    if (t < n) put(t, xp.v[j]);
-  }
-  for (int t = tid + kXPre * kThreads; t < n; t += kThreads) {
-    const int b = t / per_row;
-    put(t, x_load8(x, K, b, k0 + (t - b * per_row) * 8));
-  }
-  __syncthreads();
+  const int wave = tid >> 6, lane = tid & 63;
   const int lg_fb = 31 - __builtin_clz(fb);
-  for (int lg_h0 = 0; lg_h0 < lg_fb; lg_h0 += 4) {
-    const int lg_span = min(4, lg_fb - lg_h0);
-    const int span = 1 << lg_span;
-    const int h0 = 1 << lg_h0;
-    const int lg_nhi = lg_fb - lg_h0 - lg_span;
-    const int ngroups = (B * kw) >> lg_span;
-    for (int t = tid; t < ngroups; t += kThreads) {
-      const int lo = t & (h0 - 1);
-      const int rest = t >> lg_h0;
-      const int hi = rest & ((1 << lg_nhi) - 1);
-      const int blk = rest >> lg_nhi;
-      float* base = F + blk * fb + ((hi << lg_span) << lg_h0) + lo;
-      float v[16];
+  const int nsb = (kw + 255) >> 8;  // 256-value sub-blocks per batch row
+  auto store_x = [&](int b, int k, float v) {
+    *(reinterpret_cast<_Float16*>(lds + b * RS + (k >> 7) * kSliceBytes) + (k & 127)) =
+        (_Float16)(v * sc);
+  };
+  auto bfly = [&](float& lo, float& hi) {
+    const float a = lo, c = hi;
+    lo = a + c;
+    hi = a - c;
+  };
+  int i = 0;
+  for (int sb = wave; sb < B * nsb; sb += kWaves, ++i) {
+    const int b = sb / nsb;
+    const int k = (sb - b * nsb) * 256 + lane * 4;
+    const bool live = k < kw;  // kw is a multiple of 128: whole lanes are in or out
+    uint2 raw = {0u, 0u};
+    if (i < kXPre) {
 #pragma unroll
-      for (int u = 0; u < 16; ++u) v[u] = u < span ? base[u * h0] : 0.0f;
+      for (int j = 0; j < kXPre; ++j)
+        if (j == i) raw = xr.v[j];
+    } else if (live) {
+      raw = *reinterpret_cast<const uint2*>(x + (int64_t)b * K + k0 + k);
+    }
+    const _Float16* h = reinterpret_cast<const _Float16*>(&raw);
+    float v[4] = {(float)h[0], (float)h[1], (float)h[2], (float)h[3]};
+    if (lg_fb > 0) {
+      bfly(v[0], v[1]);
+      bfly(v[2], v[3]);
+    }
+    if (lg_fb > 1) {
+      bfly(v[0], v[2]);
+      bfly(v[1], v[3]);
+    }
 #pragma unroll
-      for (int s = 1; s < 16; s <<= 1) {
-        if (s < span) {
+    for (int st = 0; st < 6; ++st) {
+      if (st + 2 < lg_fb) {  // uniform
+        const int m = 1 << st;
+        const bool upper = (lane & m) != 0;
 #pragma unroll
-          for (int u = 0; u < 16; ++u) {
-            if ((u & s) == 0) {
-              const float a = v[u], c = v[u + s];
-              v[u] = a + c;
-              v[u + s] = a - c;
-            }
+        for (int e = 0; e < 4; ++e) {
+          const float o = __shfl_xor(v[e], m);
+          v[e] = upper ? o - v[e] : v[e] + o;
+        }
+      }
+    }
+    if (!live) continue;
+    if (lg_fb <= 8) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) store_x(b, k + e, v[e]);
+    } else {
+      *reinterpret_cast<f32x4*>(F + b * kw + k) = f32x4{v[0], v[1], v[2], v[3]};
+    }
+  }
+  if (lg_fb > 8) {
+    __syncthreads();
+    const int total = B * kw;
+    for (int base = 0; base < total; base += 4096) {
+      float v[4];
+      int e[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        e[r] = base + (wave * 16 + (lane & 15)) + 256 * (r + 4 * (lane >> 4));
+        v[r] = e[r] < total ? F[e[r]] : 0.0f;
+      }
+      if (lg_fb > 8) {
+        bfly(v[0], v[1]);
+        bfly(v[2], v[3]);
+      }
+      if (lg_fb > 9) {
+        bfly(v[0], v[2]);
+        bfly(v[1], v[3]);
+      }
+#pragma unroll
+      for (int st = 0; st < 2; ++st) {
+        if (st + 10 < lg_fb) {  // uniform
+          const int m = 16 << st;
+          const bool upper = (lane & m) != 0;
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const float o = __shfl_xor(v[r], m);
+            v[r] = upper ? o - v[r] : v[r] + o;
           }
         }
       }
 #pragma unroll
-      for (int u = 0; u < 16; ++u)
-        if (u < span) base[u * h0] = v[u];
+      for (int r = 0; r < 4; ++r) {
+        if (e[r] < total) {
+          const int b = e[r] / kw;
+          store_x(b, e[r] - b * kw, v[r]);
+        }
+      }
     }
-    __syncthreads();
   }
+  // zeros past the rotated width (the weight stream is zero there too)
   const int width = nsl * 128;
-  for (int t = tid; t < B * width; t += kThreads) {
-    const int b = t / width;
-    const int k = t - b * width;
-    const float v = k < kw ? F[b * kw + k] * sc : 0.0f;
-    *reinterpret_cast<_Float16*>(lds + b * RS + (k >> 7) * kSliceBytes + (k & 127) * 2) =
-        (_Float16)v;
+  for (int t = tid; t < B * ((width - kw) >> 3); t += kThreads) {
+    const int b = t / ((width - kw) >> 3);
+    const int k = kw + (t - b * ((width - kw) >> 3)) * 8;
+    *reinterpret_cast<u32x4*>(lds + b * RS + (k >> 7) * kSliceBytes + (k & 127) * 2) =
+        u32x4{0u, 0u, 0u, 0u};
   }
 }
 
 __host__ __device__ inline int x_lds_bytes(int B, int K, int SPL, int fwht_block) {
   int b = B * x_row_stride(SPL * 4);
-  if (fwht_block) b += B * min(K, SPL * 512) * 4;
+  if (fwht_block > 256) b += B * min(K, SPL * 512) * 4;  // fp32 scratch of the rotation
   return (b + 15) & ~15;
 }
 
@@ -451,7 +520,11 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(
     int tid = threadIdx.x;
     if constexpr (MODE != kFlat) asm volatile("" : "+v"(tid));
     XPre xp;
-    x_preload(xp, xg, K, k0, per_row, B * per_row, row_of, tid);
+    XRot xr;
+    if constexpr (rot)
+      rot_preload(xr, xg, K, B, k0, kw, tid);
+    else
+      x_preload(xp, xg, K, k0, per_row, B * per_row, row_of, tid);
     int u0 = wave, u1 = wave + kWaves;
     issue(s, u0, ring[0]);
     if (s == 0) {
@@ -459,7 +532,7 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(
       if (threadIdx.x < 16) reinterpret_cast<u32x4*>(zeros)[threadIdx.x] = u32x4{0u, 0u, 0u, 0u};
     }
     if constexpr (rot)
-      stage_fwht(xst, reinterpret_cast<float*>(xst + B * RS), xp, xg, K, B, k0, kw, nsl, RS,
+      stage_fwht(xst, reinterpret_cast<float*>(xst + B * RS), xr, xg, K, B, k0, kw, nsl, RS,
                  fwht_block, fwht_scale, tid);
     else
       stage_plain(xst, xp, xg, K, B, k0, nsl, RS, row_of, tid);
