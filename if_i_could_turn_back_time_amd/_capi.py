@@ -29,7 +29,8 @@ ABI_VERSION = 1
 # every symbol include/fourbit.h declares
 EXPORTED = (
     "fb_abi_version", "fb_strerror", "fb_validate", "fb_device_bytes", "fb_workspace_bytes",
-    "fb_quantize_gf4", "fb_quantize_e2m1", "fb_fwht_rows_f32", "fb_to_device",
+    "fb_quantize_gf4", "fb_quantize_gf4_masked", "fb_pack_levels_gf4", "fb_quantize_e2m1",
+    "fb_fwht_rows_f32", "fb_to_device",
     "fb_from_device", "fb_dequant_host", "fb_gemv", "fb_dequant",
 )
 
@@ -61,6 +62,8 @@ def lib() -> ctypes.CDLL:
         "fb_device_bytes": (sz, [sp]),
         "fb_workspace_bytes": (sz, [sp]),
         "fb_quantize_gf4": (ctypes.c_int, [vp, i32, i32, vp, vp, i32]),
+        "fb_quantize_gf4_masked": (ctypes.c_int, [vp, vp, i32, i32, vp, vp, i32]),
+        "fb_pack_levels_gf4": (ctypes.c_int, [vp, vp, i32, i32, vp, vp, i32]),
         "fb_quantize_e2m1": (ctypes.c_int, [vp, i32, i32, vp, vp, i32]),
         "fb_fwht_rows_f32": (ctypes.c_int, [vp, i32, i32, i32, i32]),
         "fb_to_device": (ctypes.c_int, [vp, vp, vp, sp]),
@@ -106,14 +109,39 @@ def _host_contig(t: torch.Tensor, dtype) -> torch.Tensor:
 
 
 # ------------------------------------------------------------------ host packers
-def quantize_gf4(w: torch.Tensor, nthreads: int | None = None):
-    """fp32 [N,K] -> (codes uint8 [N,K/2], codebook uint16-as-int16 [N,K/128,16])."""
+def quantize_gf4(w: torch.Tensor, nthreads: int | None = None, keep: torch.Tensor | None = None):
+    """fp32 [N,K] -> (codes uint8 [N,K/2], codebook uint16-as-int16 [N,K/128,16]).
+
+    ``keep`` (bool/uint8 [N,K], optional): entries where it is 0 decode to exactly 0
+    (fb_quantize_gf4_masked)."""
     w = _host_contig(w, torch.float32)
     N, K = w.shape
     codes = torch.empty(N, K // 2, dtype=torch.uint8)
     book = torch.empty(N, max(K // 128, 1), 16, dtype=torch.int16)
-    check(lib().fb_quantize_gf4(_ptr(w), N, K, _ptr(codes), _ptr(book),
-                                nthreads or nthreads_default()))
+    nt = nthreads or nthreads_default()
+    if keep is None:
+        check(lib().fb_quantize_gf4(_ptr(w), N, K, _ptr(codes), _ptr(book), nt))
+    else:
+        keep = _host_contig(keep != 0, torch.uint8)
+        if keep.shape != w.shape:
+            raise ValueError("keep mask must have the weight's shape")
+        check(lib().fb_quantize_gf4_masked(_ptr(w), _ptr(keep), N, K, _ptr(codes),
+                                           _ptr(book), nt))
+    return codes, book
+
+
+def pack_levels_gf4(levels: torch.Tensor, scale: torch.Tensor, nthreads: int | None = None):
+    """Integer levels fp32 [N,K] and per-row scale [N] -> GF4 (codes, codebook) with
+    codebook entries fp16(scale * level) (fb_pack_levels_gf4)."""
+    levels = _host_contig(levels, torch.float32)
+    N, K = levels.shape
+    scale = _host_contig(scale.reshape(-1), torch.float32)
+    if scale.numel() != N:
+        raise ValueError("scale needs one entry per row")
+    codes = torch.empty(N, K // 2, dtype=torch.uint8)
+    book = torch.empty(N, max(K // 128, 1), 16, dtype=torch.int16)
+    check(lib().fb_pack_levels_gf4(_ptr(levels), _ptr(scale), N, K, _ptr(codes), _ptr(book),
+                                   nthreads or nthreads_default()))
     return codes, book
 
 

@@ -103,7 +103,7 @@ struct JenksScratch {
 void jenks_group(const float* vals, int n, int k, uint8_t* codes, uint16_t* book,
                  JenksScratch& S) {
   for (int t = 0; t < n; ++t) S.order[t] = t;
-  std::stable_sort(S.order.begin(), S.order.end(),
+  std::stable_sort(S.order.begin(), S.order.begin() + n,
                    [&](int a, int b) { return (double)vals[a] < (double)vals[b]; });
   for (int t = 0; t < n; ++t) S.v[t] = (double)vals[S.order[t]];
   S.S1[0] = 0.0;
@@ -161,6 +161,40 @@ void jenks_group(const float* vals, int n, int k, uint8_t* codes, uint16_t* book
   }
 }
 
+// One group with a keep mask.  Masked entries take an exact-zero codebook entry; the
+// kept values are partitioned into min(15, kept) classes by jenks_group.  The zero entry
+// goes after every strictly negative centroid, so the codebook stays non-decreasing,
+// and entries past the last used one repeat it.  With nothing masked this is
+// jenks_group with 16 classes.
+void jenks_group_masked(const float* vals, const uint8_t* keep, int n, uint8_t* codes,
+                        uint16_t* book, JenksScratch& S) {
+  float sub[128];
+  int pos[128];
+  int m = 0;
+  for (int t = 0; t < n; ++t)
+    if (keep[t]) {
+      sub[m] = vals[t];
+      pos[m] = t;
+      ++m;
+    }
+  if (m == n) {
+    jenks_group(vals, n, 16, codes, book, S);
+    return;
+  }
+  const int k = std::min(15, m);
+  uint8_t c[128];
+  uint16_t cb[16];
+  if (k > 0) jenks_group(sub, m, k, c, cb, S);
+  int z = 0;
+  while (z < k && (cb[z] & 0x8000u) && (cb[z] & 0x7fffu)) ++z;  // strictly negative
+  for (int j = 0; j < z; ++j) book[j] = cb[j];
+  book[z] = 0;
+  for (int j = z; j < k; ++j) book[j + 1] = cb[j];
+  for (int j = k + 1; j < 16; ++j) book[j] = book[k];
+  for (int t = 0; t < n; ++t) codes[t] = (uint8_t)z;
+  for (int i = 0; i < m; ++i) codes[pos[i]] = (uint8_t)(c[i] + (c[i] >= z ? 1 : 0));
+}
+
 // ---------------------------------------------------------------------------------
 // E2M1 rounding: |q| onto {0,.5,1,1.5,2,3,4,6}, nearest, ties to even index, sat 6.
 // ---------------------------------------------------------------------------------
@@ -199,10 +233,11 @@ const char* fb_strerror(int code) {
     case FB_ERR_ALIGN: return "fourbit: device pointers must be 16-byte aligned";
     case FB_ERR_WORKSPACE: return "fourbit: workspace smaller than fb_workspace_bytes()";
     case FB_ERR_BATCH: return "fourbit: batch size not supported by this entry point";
-    case FB_ERR_VALUE: return "fourbit: non-finite weight";
+    case FB_ERR_VALUE: return "fourbit: non-finite weight or scale, non-positive scale, non-integer level, or a codebook entry beyond fp16 range";
     case FB_ERR_HIP: return "fourbit: HIP runtime call failed";
     case FB_ERR_THREADS: return "fourbit: nthreads must be >= 1";
     case FB_ERR_LDS: return "fourbit: activation vector does not fit the kernel's LDS budget";
+    case FB_ERR_LEVELS: return "fourbit: the integer levels of a 128-group span more than 16 values";
     default: return "fourbit: unknown error";
   }
 }
@@ -250,6 +285,75 @@ int fb_quantize_gf4(const float* w, int32_t N, int32_t K, uint8_t* codes, uint16
     }
   });
   return FB_OK;
+}
+
+int fb_quantize_gf4_masked(const float* w, const uint8_t* keep, int32_t N, int32_t K,
+                           uint8_t* codes, uint16_t* codebook, int32_t nthreads) {
+  if (!keep) return fb_quantize_gf4(w, N, K, codes, codebook, nthreads);
+  if (!w || !codes || !codebook) return FB_ERR_NULL;
+  if (N < 1 || K < 128 || K % 128) return FB_ERR_SHAPE;
+  if (nthreads < 1) return FB_ERR_THREADS;
+  const int64_t total = (int64_t)N * K;
+  for (int64_t t = 0; t < total; ++t)
+    if (keep[t] && !std::isfinite(w[t])) return FB_ERR_VALUE;
+  const int G = K / 128;
+  parallel_for((int64_t)N * G, nthreads, [&](int64_t b, int64_t e) {
+    JenksScratch S(128, 16);
+    uint8_t c[128];
+    for (int64_t it = b; it < e; ++it) {
+      const int64_t n = it / G, g = it % G;
+      const int64_t off = n * K + g * 128;
+      jenks_group_masked(w + off, keep + off, 128, c, codebook + it * 16, S);
+      uint8_t* dst = codes + n * (K / 2) + g * 64;
+      for (int j = 0; j < 64; ++j) dst[j] = (uint8_t)(c[2 * j] | (c[2 * j + 1] << 4));
+    }
+  });
+  return FB_OK;
+}
+
+int fb_pack_levels_gf4(const float* levels, const float* scale, int32_t N, int32_t K,
+                       uint8_t* codes, uint16_t* codebook, int32_t nthreads) {
+  if (!levels || !scale || !codes || !codebook) return FB_ERR_NULL;
+  if (N < 1 || K < 128 || K % 128) return FB_ERR_SHAPE;
+  if (nthreads < 1) return FB_ERR_THREADS;
+  for (int32_t n = 0; n < N; ++n)
+    if (!(std::isfinite(scale[n]) && scale[n] > 0.0f)) return FB_ERR_VALUE;
+  const int G = K / 128;
+  std::atomic<int> status{FB_OK};
+  parallel_for((int64_t)N * G, nthreads, [&](int64_t b, int64_t e) {
+    for (int64_t it = b; it < e; ++it) {
+      const int64_t n = it / G, g = it % G;
+      const float* v = levels + n * K + g * 128;
+      float lo = std::numeric_limits<float>::infinity(), hi = -lo;
+      for (int t = 0; t < 128; ++t) {
+        if (!std::isfinite(v[t]) || std::floor(v[t]) != v[t]) {
+          status.store(FB_ERR_VALUE);
+          return;
+        }
+        lo = std::min(lo, v[t]);
+        hi = std::max(hi, v[t]);
+      }
+      lo += 0.0f;  // -0 -> +0, so a group of zeros has a +0 entry
+      if (hi - lo > 15.0f) {
+        status.store(FB_ERR_LEVELS);
+        return;
+      }
+      const int used = (int)(hi - lo);
+      uint16_t* bk = codebook + it * 16;
+      for (int j = 0; j < 16; ++j) {
+        const float lev = lo + (float)std::min(j, used);
+        bk[j] = f32_to_f16_rne(scale[n] * lev);
+        if ((bk[j] & 0x7fffu) >= 0x7c00u) {
+          status.store(FB_ERR_VALUE);
+          return;
+        }
+      }
+      uint8_t* dst = codes + n * (K / 2) + g * 64;
+      for (int j = 0; j < 64; ++j)
+        dst[j] = (uint8_t)((int)(v[2 * j] - lo) | ((int)(v[2 * j + 1] - lo) << 4));
+    }
+  });
+  return status.load();
 }
 
 int fb_quantize_e2m1(const float* w, int32_t N, int32_t K, uint8_t* codes, uint8_t* scales,

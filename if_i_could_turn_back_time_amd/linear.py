@@ -12,6 +12,12 @@ HIP kernel, which decodes in registers.
 Extra keyword arguments: ``fmt`` ('gf4' | 'e2m1'), ``hadamard`` (False, True for the
 default block, or an explicit power-of-two block: the weight is rotated offline and x
 in-kernel) and ``nthreads`` for the host packer.
+
+``in_features`` need not be a multiple of the 128-wide group: the packed weight gets
+zero columns up to the next multiple (masked, so they decode to exactly 0 and do not
+move the last group's codebook) and ``forward`` pads x with zeros to match.
+``QuantLinear.from_reference`` packs the reference layer's own committed 4-bit weight
+(``layers.py:39-45``) exactly, through integer-level GF4 codebooks.
 """
 from __future__ import annotations
 
@@ -19,11 +25,18 @@ import copy
 
 import torch
 import torch.nn as nn
+import torch.nn.functional as F
 
 from . import _capi as C
 
 LAYOUT_VERSION = 1
 MAX_GEMV_BATCH = 16
+GROUP = 128
+
+
+def packed_k(K: int) -> int:
+    """K of the packed weight: in_features rounded up to a multiple of 128."""
+    return (K + GROUP - 1) // GROUP * GROUP
 
 
 def fwht_block_for(K: int) -> int:
@@ -33,6 +46,40 @@ def fwht_block_for(K: int) -> int:
         return 4096
     b = K & -K
     return min(b, 4096)
+
+
+def packed_linear(wdev: torch.Tensor, N: int, K: int, fmt: str, fwht_block: int,
+                  x: torch.Tensor, bias: torch.Tensor | None = None) -> torch.Tensor:
+    """``F.linear(x, W, bias)`` for a packed 4-bit ``W [N, K]`` (device stream ``wdev``
+    of a ``packed_k(K)``-wide weight), through fb_gemv in chunks of 16 rows of x.
+
+    x may have any leading shape and dtype: it is cast to fp16 (GF4, or any rotation) or
+    kept in fp16/bf16 (E2M1; fp32 becomes bf16) and zero-padded to ``packed_k(K)``; y
+    has x's dtype (fp32 for other dtypes).  No CPU path: x must be on the GPU."""
+    if not x.is_cuda:
+        raise RuntimeError("the packed 4-bit linear runs the HIP kernel: move the module and "
+                           "input to a ROCm GPU")
+    kp = packed_k(K)
+    lead = x.shape[:-1]
+    x2 = x.reshape(-1, K)
+    if fmt == "gf4" or fwht_block:
+        xk = x2.to(torch.float16)
+    else:
+        xk = x2 if x2.dtype in (torch.float16, torch.bfloat16) else x2.to(torch.bfloat16)
+    if kp != K:
+        xk = F.pad(xk, (0, kp - K))
+    xk = xk.contiguous()
+    ydt = x.dtype if x.dtype in C.DTYPE_CODE else torch.float32
+    y = torch.empty(x2.shape[0], N, dtype=ydt, device=x.device)
+    f = C.FMT_BY_NAME[fmt]
+    for b0 in range(0, x2.shape[0], MAX_GEMV_BATCH):
+        b1 = min(b0 + MAX_GEMV_BATCH, x2.shape[0])
+        shape = C.make_shape(N, kp, b1 - b0, f, fwht_block, C.DTYPE_CODE[xk.dtype],
+                             C.DTYPE_CODE[ydt])
+        C.gemv(wdev, xk[b0:b1], y[b0:b1], shape)
+    if bias is not None:
+        y = y + bias.to(ydt)
+    return y.reshape(*lead, N)
 
 
 class PackedWeight:
@@ -52,18 +99,32 @@ class PackedWeight:
 
     @classmethod
     def quantize(cls, w: torch.Tensor, fmt: str = "gf4", fwht_block: int = 0, device=None,
-                 nthreads: int | None = None) -> "PackedWeight":
+                 nthreads: int | None = None, keep: torch.Tensor | None = None) -> "PackedWeight":
+        """Packs fp32 ``w [N,K]``.  ``keep`` (GF4 only, no rotation): entries where it is
+        0 decode to exactly 0."""
         w = w.detach().float().cpu().contiguous()
         N, K = w.shape
+        if keep is not None and (fmt != "gf4" or fwht_block):
+            raise ValueError("keep masks apply to unrotated GF4 packing only")
         if fwht_block:
             w = C.fwht_rows(w, fwht_block, nthreads)
         if fmt == "gf4":
-            codes, meta = C.quantize_gf4(w, nthreads)
+            codes, meta = C.quantize_gf4(w, nthreads, keep)
         elif fmt == "e2m1":
             codes, meta = C.quantize_e2m1(w, nthreads)
         else:
             raise ValueError(f"unknown fmt {fmt!r}")
         return cls(fmt, N, K, codes, meta, fwht_block, device)
+
+    @classmethod
+    def from_levels(cls, levels: torch.Tensor, scale: torch.Tensor, device=None,
+                    nthreads: int | None = None) -> "PackedWeight":
+        """Integer levels ``[N,K]`` times a per-row ``scale [N]`` as GF4 codebooks
+        (fb_pack_levels_gf4): decodes to ``fp16(fp32(scale * level))``."""
+        levels = levels.detach().float().cpu()
+        N, K = levels.shape
+        codes, meta = C.pack_levels_gf4(levels, scale, nthreads)
+        return cls("gf4", N, K, codes, meta, 0, device)
 
     def shape(self, B: int, x_dtype: torch.dtype, y_dtype: torch.dtype) -> C.FbShape:
         return C.make_shape(self.N, self.K, B, self.fmt, self.fwht_block,
@@ -111,7 +172,8 @@ class QuantLinear(nn.Linear):
     """4-bit quantized ``nn.Linear`` (reference: ``layers.py:11-45``)."""
 
     def __init__(self, linear_module: nn.Linear, bitwidth: int = 4, mask=None, *,
-                 fmt: str = "gf4", hadamard=False, nthreads: int | None = None):
+                 fmt: str = "gf4", hadamard=False, nthreads: int | None = None,
+                 pack: bool = True):
         super().__init__(linear_module.in_features, linear_module.out_features,
                          bias=(linear_module.bias is not None))
         if bitwidth != 4:
@@ -119,8 +181,9 @@ class QuantLinear(nn.Linear):
         if fmt not in C.FMT_BY_NAME:
             raise ValueError(f"fmt must be 'gf4' or 'e2m1', got {fmt!r}")
         K = linear_module.in_features
-        if K % 128:
-            raise ValueError("in_features must be a multiple of 128")
+        self.k_pack = packed_k(K)
+        if hadamard and K % GROUP:
+            raise ValueError("hadamard rotation needs in_features to be a multiple of 128")
         self.weight.requires_grad = False
         self.weight.data = linear_module.weight.data.clone()
         if linear_module.bias is not None:
@@ -137,45 +200,84 @@ class QuantLinear(nn.Linear):
         self.register_buffer("wdev", torch.empty(0, dtype=torch.uint8), persistent=False)
         self.hard_quant = False
         self.register_load_state_dict_post_hook(QuantLinear._rebuild_after_load)
-        self.quantize()
+        if pack:
+            self.quantize()
+
+    @classmethod
+    def from_reference(cls, ref, *, nthreads: int | None = None) -> "QuantLinear":
+        """Packs a reference ``QuantLinear`` (``layers.py:11-45``; the module or its
+        ``state_dict`` with ``weight, s, Q, Theta, mask`` and optional ``bias``) in its
+        own 4-bit format: the committed weight ``mask * s * round(Q + [h(Theta) > 0.5])``
+        (``layers.py:39-45``) as integer levels with the per-row scale ``s``
+        (fb_pack_levels_gf4).  The packed weight decodes to ``fp16`` of the reference's
+        committed fp32 weight, element for element; ``weight`` holds that fp32 weight.
+        Raises if ``mask`` is not 0/1 or a 128-group spans more than 16 levels."""
+        sd = ref.state_dict() if isinstance(ref, nn.Module) else ref
+        s = sd["s"].detach().float().cpu()
+        Q = sd["Q"].detach().float().cpu()
+        mask = sd["mask"].detach().float().cpu()
+        if not bool(((mask == 0) | (mask == 1)).all()):
+            raise ValueError("from_reference needs a 0/1 mask")
+        N, K = Q.shape
+        # layers.py:41-43
+        theta = (torch.sigmoid(sd["Theta"].detach().float().cpu()) * 1.2 - .1 > 0.5).float()
+        q_round = torch.round(Q + theta)
+        bias = sd.get("bias")
+        lin = nn.Linear(K, N, bias=bias is not None)
+        with torch.no_grad():
+            lin.weight.copy_(mask * s * q_round)
+            if bias is not None:
+                lin.bias.copy_(bias.detach().float().cpu())
+        q = cls(lin, 4, mask=mask, fmt="gf4", nthreads=nthreads, pack=False)
+        levels = F.pad(q_round * mask, (0, q.k_pack - K))
+        q._set_packed(PackedWeight.from_levels(levels, s.reshape(-1), nthreads=nthreads))
+        return q
 
     # -- packing ------------------------------------------------------------------
     def quantize(self) -> None:
-        """(Re)packs ``weight`` (times ``mask``) into 4-bit codes + codebooks/scales."""
+        """(Re)packs ``weight`` (times ``mask``) into 4-bit codes + codebooks/scales.
+        Unrotated GF4 keeps masked (and padding) entries at exactly 0."""
         w = self.weight.data.detach().float().cpu()
+        N, K = w.shape
+        keep = None
         if self.mask is not None:
             w = w * self.mask.float().cpu()
-        pw = PackedWeight.quantize(w, self.fmt, self.fwht_block, nthreads=self.nthreads)
+            keep = self.mask.cpu() != 0
+        pad = self.k_pack - K
+        if pad:
+            w = F.pad(w, (0, pad))
+            keep = F.pad(torch.ones(N, K, dtype=torch.bool) if keep is None else keep, (0, pad))
+        if self.fmt != "gf4" or self.fwht_block:
+            keep = None  # E2M1 codes zeros exactly; a rotation mixes masked and kept
+        self._set_packed(PackedWeight.quantize(w, self.fmt, self.fwht_block,
+                                               nthreads=self.nthreads, keep=keep))
+
+    pack = quantize
+
+    def _set_packed(self, pw: PackedWeight) -> None:
         dev = self.weight.device
         self.codes = pw.codes.to(dev)
         self.meta = pw.meta.to(dev)
         self.wdev = pw.wdev.to(dev)
 
-    pack = quantize
-
     def _shape(self, B=1, x_dtype=torch.float16, y_dtype=torch.float16) -> C.FbShape:
-        return C.make_shape(self.out_features, self.in_features, B, C.FMT_BY_NAME[self.fmt],
+        return C.make_shape(self.out_features, self.k_pack, B, C.FMT_BY_NAME[self.fmt],
                             self.fwht_block, C.DTYPE_CODE[x_dtype], C.DTYPE_CODE[y_dtype])
 
     def _load_from_state_dict(self, state_dict, prefix, local_metadata, strict, missing_keys,
                               unexpected_keys, error_msgs):
-        # packed buffers take the checkpoint's shape/dtype (format may differ from ctor)
+        # packed buffers take the checkpoint's shape/dtype (format may differ from ctor),
+        # and the mask is present exactly when the checkpoint has one
         for name in ("codes", "meta", "fb_header"):
             key = prefix + name
             if key in state_dict:
                 cur = getattr(self, name)
                 setattr(self, name, torch.empty_like(state_dict[key], device=cur.device))
+        key = prefix + "mask"
+        self.mask = (torch.empty_like(state_dict[key], device=self.weight.device)
+                     if key in state_dict else None)
         super()._load_from_state_dict(state_dict, prefix, local_metadata, strict, missing_keys,
                                       unexpected_keys, error_msgs)
-
-    def _workspace(self, shape: C.FbShape):
-        need = C.workspace_bytes(shape)
-        if not need:
-            return None
-        ws = getattr(self, "_ws_cache", None)
-        if ws is None or ws.numel() < need or ws.device != self.wdev.device:
-            ws = self._ws_cache = C.new_workspace(shape, self.wdev.device)
-        return ws
 
     def _rebuild_after_load(self, incompatible_keys) -> None:
         hdr = self.fb_header.tolist()
@@ -192,7 +294,8 @@ class QuantLinear(nn.Linear):
     def dequantized_weight(self) -> torch.Tensor:
         """Exact fp32 decode of the packed weight (in the rotated basis when
         ``fwht_block`` is set)."""
-        return C.dequant_host(self.codes.cpu(), self.meta.cpu(), self._shape())
+        w = C.dequant_host(self.codes.cpu(), self.meta.cpu(), self._shape())
+        return w[:, :self.in_features].contiguous()
 
     def commit(self) -> None:
         """Reference ``commit()`` (``layers.py:39-45``) stores the hard-rounded weight
@@ -206,26 +309,8 @@ class QuantLinear(nn.Linear):
             self.hard_quant = True
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
-        if not x.is_cuda:
-            raise RuntimeError("QuantLinear.forward runs the HIP kernel: move the module and "
-                               "input to a ROCm GPU")
-        K, N = self.in_features, self.out_features
-        lead = x.shape[:-1]
-        x2 = x.reshape(-1, K)
-        if self.fmt == "gf4" or self.fwht_block:
-            xk = x2.to(torch.float16)
-        else:
-            xk = x2 if x2.dtype in (torch.float16, torch.bfloat16) else x2.to(torch.bfloat16)
-        xk = xk.contiguous()
-        ydt = x.dtype if x.dtype in C.DTYPE_CODE else torch.float32
-        y = torch.empty(x2.shape[0], N, dtype=ydt, device=x.device)
-        for b0 in range(0, x2.shape[0], MAX_GEMV_BATCH):
-            b1 = min(b0 + MAX_GEMV_BATCH, x2.shape[0])
-            shape = self._shape(b1 - b0, xk.dtype, ydt)
-            C.gemv(self.wdev, xk[b0:b1], y[b0:b1], shape, self._workspace(shape))
-        if self.bias is not None:
-            y = y + self.bias.to(ydt)
-        return y.reshape(*lead, N)
+        return packed_linear(self.wdev, self.out_features, self.in_features, self.fmt,
+                             self.fwht_block, x, self.bias)
 
     def extra_repr(self) -> str:
         return (f"in_features={self.in_features}, out_features={self.out_features}, "

@@ -40,10 +40,11 @@ typedef enum {
   FB_ERR_ALIGN = -7,         /* pointer not 16-byte aligned                        */
   FB_ERR_WORKSPACE = -8,     /* workspace too small                                */
   FB_ERR_BATCH = -9,         /* batch size not supported by this entry point       */
-  FB_ERR_VALUE = -10,        /* non-finite input to a quantizer                    */
+  FB_ERR_VALUE = -10,        /* non-finite / non-integer / out-of-range packer input */
   FB_ERR_HIP = -11,          /* a HIP runtime call failed                          */
   FB_ERR_THREADS = -12,      /* nthreads < 1                                       */
-  FB_ERR_LDS = -13           /* activation does not fit the kernel's LDS budget    */
+  FB_ERR_LDS = -13,          /* activation does not fit the kernel's LDS budget    */
+  FB_ERR_LEVELS = -14        /* integer levels of one 128-group span > 16 values    */
 } fb_status;
 
 typedef enum { FB_FMT_GF4 = 0, FB_FMT_E2M1 = 1 } fb_fmt;
@@ -91,6 +92,26 @@ size_t fb_workspace_bytes(const fb_shape_t* s);
  * (cuda_helpers.py:151-184) from 2 to 16 classes. */
 int fb_quantize_gf4(const float* w, int32_t N, int32_t K, uint8_t* codes, uint16_t* codebook,
                     int32_t nthreads);
+
+/* GF4 with a keep mask (uint8 [N,K], 0 = masked, NULL = none, i.e. fb_quantize_gf4).
+ * Masked weights decode to exactly 0, as the reference's mask * s * (...) does
+ * (layers.py:37, :43): in every group that has a masked entry, the kept values get
+ * min(15, kept) Jenks classes and the codebook gains an exact-zero entry, placed after
+ * the strictly negative centroids; entries past the last used one repeat it.  Masked
+ * values are never read (they may be non-finite). */
+int fb_quantize_gf4_masked(const float* w, const uint8_t* keep, int32_t N, int32_t K,
+                           uint8_t* codes, uint16_t* codebook, int32_t nthreads);
+
+/* Integer-level weights (levels fp32 [N,K], integer-valued; scale fp32 [N], > 0) as
+ * GF4: per 128-group, lo = min level, code = level - lo, codebook[j] =
+ * fp16_rne(fp32(scale[n] * (lo + min(j, hi - lo)))).  Exact up to the fp16 rounding
+ * of scale * level.  This is the reference's own 4-bit weight: QuantLinear.commit
+ * stores mask * s * round(Q + Theta) (layers.py:39-45, level = mask * round(...)) and
+ * brecq's AdaRound quantizer returns clamp(mask * (W_floor + h), qmin, qmax) * delta
+ * (brecq.py:81-92).  FB_ERR_LEVELS when a group spans more than 16 levels (the
+ * reference's [-8, 8] can, rarely, in one group). */
+int fb_pack_levels_gf4(const float* levels, const float* scale, int32_t N, int32_t K,
+                       uint8_t* codes, uint16_t* codebook, int32_t nthreads);
 
 /* E2M1 + E8M0 per 32-group (OCP MX v1.0): e = floor(log2 amax) - 2, codes by RNE with
  * saturation at +-6, amax = 0 -> scale byte 127.  Replaces the uniform grids of

@@ -142,6 +142,63 @@ def gf4_quantize(w: np.ndarray, group: int = GF4_GROUP, k: int = GF4_LEVELS):
     return codes.reshape(N, K), books.reshape(N, G, k)
 
 
+def gf4_quantize_masked(w: np.ndarray, keep: np.ndarray, group: int = GF4_GROUP):
+    """GF4 with a keep mask: masked weights decode to exactly 0.
+
+    The reference multiplies the dequantized weight by its mask (``layers.py:37``,
+    ``:43``), so pruned weights stay exactly zero; plain Jenks-16 can put zeros in a
+    class with a non-zero mean.  Per group with at least one masked entry: Jenks with
+    ``min(15, kept)`` classes over the kept values (stable-sorted, as
+    ``gf4_quantize``), an exact-zero entry inserted after the strictly negative
+    centroids, the rest of the 16 entries repeating the last used one; masked codes
+    point at the zero entry.  Groups with nothing masked are ``gf4_quantize``'s.
+    Group-by-group loop (test sizes only).
+    """
+    w = np.asarray(w, np.float32)
+    keep = np.asarray(keep) != 0
+    N, K = w.shape
+    G = K // group
+    codes = np.zeros((N, K), np.uint8)
+    books = np.zeros((N, G, 16), np.uint16)
+    full = keep.reshape(N, G, group).all(-1)
+    if full.any():
+        c, b = gf4_quantize(w.reshape(N, G, group)[full], group)
+        codes.reshape(N, G, group)[full] = c
+        books[full] = b[:, 0]
+    for n in range(N):
+        for g in range(G):
+            sl = slice(g * group, (g + 1) * group)
+            kp = keep[n, sl]
+            if kp.all():
+                continue
+            vals = w[n, sl][kp].astype(np.float64)
+            m = vals.size
+            k = min(15, m)
+            book = np.zeros(16, np.uint16)
+            c = np.zeros(group, np.uint8)
+            if k:
+                order = np.argsort(vals, kind="stable")
+                vs = vals[order]
+                bounds, _ = jenks_breaks(vs[None], k)
+                bounds = bounds[0]
+                S1 = np.concatenate([[0.0], np.cumsum(vs)])
+                cb = f64_to_f16_bits(
+                    (S1[bounds[1:]] - S1[bounds[:-1]]) / (bounds[1:] - bounds[:-1]))
+                cls_sorted = (np.arange(m)[:, None] >= bounds[None, 1:-1]).sum(-1)
+                cls = np.empty(m, np.int64)
+                cls[order] = cls_sorted
+                z = int((cb.view(np.float16).astype(np.float64) < 0).sum())
+                book[:z] = cb[:z]
+                book[z] = 0
+                book[z + 1:k + 1] = cb[z:]
+                book[k + 1:] = book[k]
+                c[:] = z
+                c[np.flatnonzero(kp)] = cls + (cls >= z)
+            codes[n, sl] = c
+            books[n, g] = book
+    return codes, books
+
+
 def gf4_dequant(codes: np.ndarray, codebook: np.ndarray, group: int = GF4_GROUP) -> np.ndarray:
     """w[n,k] = codebook[n, k/group, code[n,k]] as fp16 bits (uint16 [N, K])."""
     N, K = codes.shape
@@ -308,3 +365,50 @@ def quantlinear_commit_weight(w, theta, mask=None, bitwidth=4):
     Qr = torch.round(Q + th)
     m = torch.ones_like(w) if mask is None else torch.as_tensor(mask, dtype=torch.float32)
     return m * s * Qr, s, Qr * (m != 0)
+
+
+def levels_to_gf4(levels, scale, group: int = GF4_GROUP):
+    """Integer-level weight ``scale[n] * level[n,k]`` as a GF4 codebook.
+
+    Per group: ``lo = min level`` (+0.0 so a -0 minimum becomes +0), code = level - lo,
+    ``codebook[j] = fp16_rne(fp32(scale[n] * (lo + min(j, hi - lo))))``.  Raises when a
+    group spans more than 16 levels.  The weight it encodes is the reference's
+    committed one, ``mask * s * Q_round`` (``layers.py:43``: fp32 product, then one
+    rounding to fp16 here), and brecq's ``clamp(...) * delta`` (``brecq.py:88-92``).
+    Returns ``(codes uint8 [N, K] unpacked, codebook uint16 [N, K/group, 16])``.
+    """
+    lv = np.asarray(levels, np.float32)
+    sc = np.asarray(scale, np.float32).reshape(-1)
+    N, K = lv.shape
+    G = K // group
+    lg = lv.reshape(N, G, group)
+    if not np.isfinite(lg).all() or (np.floor(lg) != lg).any():
+        raise ValueError("levels must be finite integers")
+    lo = lg.min(-1) + np.float32(0.0)
+    hi = lg.max(-1)
+    if ((hi - lo) > 15).any():
+        raise ValueError("a group spans more than 16 levels")
+    j = np.arange(16, dtype=np.float32)
+    lev = lo[..., None] + np.minimum(j[None, None, :], (hi - lo)[..., None])
+    prod = (sc[:, None, None] * lev).astype(np.float32)
+    book = prod.astype(np.float16).view(np.uint16)
+    codes = (lg - lo[..., None]).astype(np.uint8).reshape(N, K)
+    return codes, book
+
+
+def adaround_hard_levels(W_floor, alpha, mask, qmin: int, qmax: int):
+    """Integer levels of brecq's AdaRound quantizer with the rounding made hard.
+
+    ``AdaRoundQuantizer.forward`` (``brecq.py:81-92``) returns
+    ``clamp(mask * (W_floor + h), qmin, qmax) * delta`` with
+    ``h = clip(sigmoid(alpha) * 1.2 - 0.1, 0, 1)``; the hard level rounds h as the
+    reference's ``QuantLinear.commit`` rounds its Theta (``layers.py:41``: h > 0.5 -> 1).
+    Where ``|alpha|`` saturates the clip, h is already 0 or 1 and the result equals the
+    soft forward exactly.  fp32 torch arithmetic as in the reference.
+    """
+    Wf = torch.as_tensor(W_floor, dtype=torch.float32)
+    a = torch.as_tensor(alpha, dtype=torch.float32)
+    m = torch.as_tensor(mask, dtype=torch.float32)
+    h = torch.clamp(torch.sigmoid(a) * 1.2 - 0.1, 0, 1)
+    hard = (h > 0.5).float()
+    return torch.clamp(m * (Wf + hard), qmin, qmax)

@@ -10,7 +10,8 @@ import torch
 
 from oracle import fourbit_oracle as O
 from if_i_could_turn_back_time_amd import _capi as C
-from if_i_could_turn_back_time_amd import PackedWeight, QuantLinear
+from if_i_could_turn_back_time_amd import PackedWeight, QuantLinear, quantize_module
+from model_fixtures import lenet300_from_fixture, reference_state
 
 pytestmark = pytest.mark.gpu
 ROOT = Path(__file__).resolve().parents[1]
@@ -198,3 +199,104 @@ def test_quantlinear_forward_gpu():
         extra = {torch.float16: 2.0 ** -11, torch.bfloat16: 2.0 ** -8, torch.float32: 0.0}[xdt]
         ok, emax, _ = within_tol(y.reshape(-1, 300), yref, extra)
         assert ok, f"{fmt}/{xdt}: {emax}"
+
+
+def oracle_weight(q: QuantLinear) -> torch.Tensor:
+    """Oracle decode of a QuantLinear's packed buffers, cut to in_features."""
+    codes = O.unpack_nibbles(q.codes.cpu().numpy())
+    meta = q.meta.cpu().numpy().view(np.uint16) if q.fmt == "gf4" else q.meta.cpu().numpy()
+    return O.dequant_f32(q.fmt, codes, meta)[:, :q.in_features]
+
+
+def test_ragged_k_masked_forward_gpu():
+    """in_features = 300 (x zero-padded to 384 for the kernel), 70% of weights masked."""
+    say("ragged K / masked")
+    g = torch.Generator().manual_seed(21)
+    lin = torch.nn.Linear(300, 100)
+    mask = (torch.rand(100, 300, generator=g) > 0.7).float()
+    for fmt, xdt in (("gf4", torch.float16), ("e2m1", torch.bfloat16)):
+        q = QuantLinear(lin, mask=mask, fmt=fmt).to(DEV)
+        x = torch.randn(5, 300, generator=g).to(xdt)
+        y = q(x.to(DEV))
+        W = oracle_weight(q)
+        assert (W[mask == 0] == 0).all()
+        yref = torch.nn.functional.linear(x.float(), W, lin.bias.detach())
+        ok, emax, _ = within_tol(y, yref)
+        assert ok, f"{fmt}: {emax}"
+
+
+def test_from_reference_forward_gpu():
+    """The reference QuantLinear's committed 4-bit weight (layers.py:39-45) through the
+    GEMV: within tolerance of the oracle decode, and of F.linear with the reference's own
+    fp32 committed weight once the fp16 rounding of the codebook entries (|rel| <= 2^-11
+    per weight) is allowed for."""
+    say("from_reference")
+    for N, K in ((96, 256), (40, 200)):
+        sd = reference_state(N, K, seed=N + K)
+        Wq, _, _ = O.quantlinear_commit_weight(sd["weight"], sd["Theta"], sd["mask"])
+        q = QuantLinear.from_reference(sd).to(DEV)
+        x = torch.randn(3, K).half()
+        y = q(x.to(DEV))
+        ok, emax, _ = within_tol(y, torch.nn.functional.linear(x.float(), oracle_weight(q),
+                                                               sd["bias"]))
+        assert ok, f"oracle {N}x{K}: {emax}"
+        yref = torch.nn.functional.linear(x.float(), Wq, sd["bias"])
+        bound = ATOL + RTOL * yref.abs() + 2.0 ** -11 * (x.float().abs() @ Wq.abs().T)
+        err = (y.float().cpu() - yref).abs()
+        assert bool((err <= bound).all()), f"reference {N}x{K}: {float(err.max())}"
+
+
+def test_brecq_replace_forward_gpu():
+    """brecq's AdaRound layer (brecq.py:59-92) packed by replace_forward: with |alpha|
+    saturating the gate, the packed forward matches the reference's soft forward
+    F.linear(x, clamp(mask*(W_floor+h), qmin, qmax)*delta) up to fp16 codebook rounding."""
+    from types import SimpleNamespace
+    from if_i_could_turn_back_time_amd import replace_forward
+    say("brecq replace_forward")
+    g = torch.Generator().manual_seed(31)
+    lin = torch.nn.Linear(256, 64)
+    delta = lin.weight.data.abs().amax(dim=1, keepdim=True) / 7
+    W = lin.weight.data / delta
+    alpha = torch.sign(torch.randn(64, 256, generator=g)) * 4.0
+    wq = SimpleNamespace(W_floor=torch.floor(W), alpha=alpha, mask=torch.ones(64, 256),
+                         quantizer=SimpleNamespace(delta=delta, qmin=-8, qmax=7))
+    lin.weight_quantizer = wq
+    lin = lin.to(DEV)
+    replace_forward(lin)
+    x = torch.randn(4, 256, generator=g).half()
+    y = lin(x.to(DEV))
+    h = torch.clamp(torch.sigmoid(alpha) * 1.2 - 0.1, 0, 1)
+    Wsoft = torch.clamp(wq.mask * (wq.W_floor + h), -8, 7) * delta
+    bias = lin.bias.detach().cpu()
+    yref = torch.nn.functional.linear(x.float(), Wsoft, bias)
+    bound = ATOL + RTOL * yref.abs() + 2.0 ** -11 * (x.float().abs() @ Wsoft.abs().T)
+    err = (y.float().cpu() - yref).abs()
+    assert bool((err <= bound).all()), float(err.max())
+
+
+def test_lenet300_fixture_forward_gpu():
+    """The reference's pruned LeNet300 (784-300-100-10, ~98% zeros) with every Linear
+    swapped for the packed layer (GF4 with masks, and E2M1): each layer's GEMV within
+    tolerance of the oracle decode on that layer's own input, batch 40 (3 launches of
+    <= 16 rows per layer)."""
+    say("lenet300")
+    g = torch.Generator().manual_seed(41)
+    x = torch.rand(40, 1, 28, 28, generator=g)
+    for fmt in ("gf4", "e2m1"):
+        q = quantize_module(lenet300_from_fixture(), fmt=fmt).to(DEV)
+        h = x.flatten(1)
+        for i in (1, 3, 5):
+            y = q[i](h.to(DEV))
+            # GF4 takes x in fp16 (rounded here too); E2M1 rounds fp32 x to bf16 in the
+            # layer, which the 2^-8 relative allowance covers
+            xin = h.half().float() if fmt == "gf4" else h.float()
+            Wo = oracle_weight(q[i])
+            yref = torch.nn.functional.linear(xin, Wo, q[i].bias.detach().cpu())
+            bound = ATOL + RTOL * yref.abs()
+            if fmt == "e2m1":
+                bound = bound + 2.0 ** -8 * (xin.abs() @ Wo.abs().T)
+            err = (y.float().cpu() - yref).abs()
+            assert bool((err <= bound).all()), f"{fmt} layer {i}: {float(err.max())}"
+            h = torch.relu(yref)
+        logits = q(x.to(DEV)).float().cpu()
+        assert logits.shape == (40, 10) and torch.isfinite(logits).all()

@@ -12,6 +12,7 @@ import torch
 from oracle import fourbit_oracle as O
 from if_i_could_turn_back_time_amd import _capi as C
 from if_i_could_turn_back_time_amd import PackedWeight, QuantLinear, fwht_block_for, quantize_module
+from model_fixtures import lenet300_from_fixture, reference_state
 
 ROOT = Path(__file__).resolve().parents[1]
 GOLDEN = sorted((ROOT / "tests" / "golden").glob("*.npz"))
@@ -238,3 +239,149 @@ def test_magic_division_identity():
     for d in list(range(1, 257)) + [1000, 4093, 32767, 32768, 65535]:
         for n in list(range(0, 3000)) + [rnd.randrange(0, 1 << 30) for _ in range(300)]:
             assert fdiv(n, d) == n // d, (n, d)
+
+
+# ----------------------------------------------------------------------------- masks, levels
+@pytest.mark.parametrize("density", [0.0, 0.02, 0.3, 0.9, 1.0])
+def test_native_gf4_masked_bit_exact_vs_oracle(density):
+    g = torch.Generator().manual_seed(int(density * 100))
+    w = torch.randn(12, 512, generator=g) * 0.02
+    keep = torch.rand(12, 512, generator=g) < density
+    keep[0] = True                                      # a fully kept row
+    w[~keep] = float("nan")                             # masked values are never read
+    codes, book = C.quantize_gf4(w, 4, keep)
+    oc, ob = O.gf4_quantize_masked(w.numpy(), keep.numpy())
+    assert np.array_equal(O.unpack_nibbles(codes.numpy()), oc)
+    assert np.array_equal(book.numpy().view(np.uint16), ob)
+    c0, b0 = C.quantize_gf4(w[:1], 4)                   # no mask: fb_quantize_gf4
+    assert torch.equal(codes[:1], c0) and torch.equal(book[:1], b0)
+
+
+def test_native_pack_levels_bit_exact_and_errors():
+    g = torch.Generator().manual_seed(2)
+    N, K = 10, 384
+    lev = (torch.randint(-8, -6, (N, K // 128, 1), generator=g)
+           + torch.randint(0, 16, (N, K // 128, 128), generator=g)).reshape(N, K).float()
+    lev[0, :128] = -0.0
+    s = torch.rand(N, generator=g) * 0.01 + 1e-4
+    codes, book = C.pack_levels_gf4(lev, s, 3)
+    oc, ob = O.levels_to_gf4(lev.numpy(), s.numpy())
+    assert np.array_equal(O.unpack_nibbles(codes.numpy()), oc)
+    assert np.array_equal(book.numpy().view(np.uint16), ob)
+    bad = lev.clone()
+    bad[4, 0], bad[4, 1] = -8, 8
+    with pytest.raises(RuntimeError, match="span more than 16"):
+        C.pack_levels_gf4(bad, s)
+    bad = lev.clone()
+    bad[4, 7] = 1.5
+    with pytest.raises(RuntimeError, match="non-integer"):
+        C.pack_levels_gf4(bad, s)
+    with pytest.raises(RuntimeError, match="scale"):
+        C.pack_levels_gf4(lev, torch.zeros(N))
+    with pytest.raises(RuntimeError, match="fp16 range"):
+        C.pack_levels_gf4(lev, torch.full((N,), 1e4))
+
+
+def test_quantlinear_ragged_k_keeps_masked_and_padding_zero():
+    """in_features not a multiple of 128: the packed weight is zero-padded to the next
+    multiple; masked and padded entries decode to exactly 0 (GF4) and the kept
+    values of a group are unaffected by the padding."""
+    g = torch.Generator().manual_seed(4)
+    lin = torch.nn.Linear(300, 40)
+    with torch.no_grad():
+        lin.weight.copy_(torch.randn(40, 300, generator=g) * 0.02)
+    mask = (torch.rand(40, 300, generator=g) > 0.7).float()
+    q = QuantLinear(lin, mask=mask)
+    assert q.k_pack == 384 and q.codes.shape == (40, 192) and q.meta.shape == (40, 3, 16)
+    full = C.dequant_host(q.codes, q.meta, q._shape())
+    assert (full[:, 300:] == 0).all()
+    dq = q.dequantized_weight()
+    assert dq.shape == (40, 300) and (dq[mask == 0] == 0).all()
+    wp = torch.nn.functional.pad(lin.weight.data * mask, (0, 84))
+    keep = torch.nn.functional.pad(mask != 0, (0, 84))
+    oc, ob = O.gf4_quantize_masked(wp.numpy(), keep.numpy())
+    assert np.array_equal(O.unpack_nibbles(q.codes.numpy()), oc)
+    qe = QuantLinear(lin, mask=mask, fmt="e2m1")
+    assert (qe.dequantized_weight()[mask == 0] == 0).all()
+    with pytest.raises(ValueError):
+        QuantLinear(lin, hadamard=True)
+
+
+@pytest.mark.parametrize("K", [256, 200])
+def test_from_reference_decodes_the_committed_weight(K):
+    sd = reference_state(24, K, seed=K)
+    Wq, _, _ = O.quantlinear_commit_weight(sd["weight"], sd["Theta"], sd["mask"])
+    q = QuantLinear.from_reference(sd)
+    assert q.fmt == "gf4" and q.k_pack == 256
+    assert torch.equal(q.weight.data, Wq)                       # the reference's commit
+    dq = q.dequantized_weight()
+    assert torch.equal(dq, Wq.half().float())                   # fp16 of it, value for value
+    assert torch.equal(q.bias.data, sd["bias"])
+    # Jenks-16 on the committed weight finds the same grid (<= 16 values per group)
+    q2 = QuantLinear(q, mask=sd["mask"])
+    assert torch.equal(q2.dequantized_weight(), dq)
+    # the state_dict round trip keeps the level codebooks
+    q3 = QuantLinear(torch.nn.Linear(K, 24), pack=False)
+    q3.load_state_dict(q.state_dict())
+    assert torch.equal(q3.wdev, q.wdev)
+
+
+def test_replace_forward_packs_adaround_levels():
+    from types import SimpleNamespace
+    from if_i_could_turn_back_time_amd import adaround_levels, pack_quantized_linears
+    g = torch.Generator().manual_seed(8)
+    lin = torch.nn.Linear(200, 32)
+    delta = torch.rand(32, 1, generator=g) * 0.01 + 1e-3
+    W = lin.weight.data / delta
+    wq = SimpleNamespace(W_floor=torch.floor(W), alpha=torch.randn(32, 200, generator=g) * 4,
+                         mask=(lin.weight.data != 0).float(),
+                         quantizer=SimpleNamespace(delta=delta, qmin=-8, qmax=7))
+    lin.weight_quantizer = wq
+    net = torch.nn.Sequential(lin, torch.nn.ReLU())
+    pack_quantized_linears(net)
+    lv, d = adaround_levels(wq)
+    assert torch.equal(lv, O.adaround_hard_levels(wq.W_floor, wq.alpha, wq.mask, -8, 7))
+    pw = lin.packed_weight
+    dec = pw.dequant_host()[:, :200]
+    assert torch.equal(dec, (delta * lv).half().float())
+    with pytest.raises(RuntimeError, match="GPU"):
+        net(torch.randn(2, 200))
+
+
+# ----------------------------------------------------------------------------- LeNet300
+def test_lenet300_fixture_packs_and_round_trips():
+    """The reference's pruned LeNet300 checkpoint: sparsity equals the reference's own log
+    (0.97860, sparisty_log_2025-12-09_18-58-19_0.99_SGD_Agg_80.txt); packed with masks
+    from the zero weights, every pruned weight decodes to exactly 0 and groups with at most
+    15 distinct kept values decode exactly (fp16); the packed state_dict survives
+    torch.save / torch.load(weights_only=True)."""
+    import io
+    net = lenet300_from_fixture()
+    ws = [net[i].weight.data for i in (1, 3, 5)]
+    zeros = sum(int((w == 0).sum()) for w in ws)
+    assert round(zeros / sum(w.numel() for w in ws), 5) == 0.97860
+    q = quantize_module(net, fmt="gf4")
+    for i, w in zip((1, 3, 5), ws):
+        dq = q[i].dequantized_weight()
+        assert (dq[w == 0] == 0).all()
+        assert int((dq != 0).sum()) <= int((w != 0).sum())
+        kp = q[i].k_pack
+        wp = torch.nn.functional.pad(w, (0, kp - w.shape[1])).reshape(w.shape[0], -1, 128)
+        few = torch.tensor([len(torch.unique(grp[grp != 0])) <= 15 for grp in wp.reshape(-1, 128)])
+        exact = (dq.half().float() == w.half().float())
+        exact = torch.nn.functional.pad(exact, (0, kp - w.shape[1]), value=True)
+        assert exact.reshape(-1, 128)[few].all()
+        oc, ob = O.gf4_quantize_masked(torch.nn.functional.pad(w, (0, kp - w.shape[1])).numpy(),
+                                       torch.nn.functional.pad(w != 0, (0, kp - w.shape[1])).numpy())
+        assert np.array_equal(O.unpack_nibbles(q[i].codes.numpy()), oc)
+        assert np.array_equal(q[i].meta.numpy().view(np.uint16), ob)
+    buf = io.BytesIO()
+    torch.save(q.state_dict(), buf)
+    buf.seek(0)
+    sd = torch.load(buf, weights_only=True)
+    fresh = quantize_module(lenet300_from_fixture(), fmt="e2m1", pack=False)
+    fresh.load_state_dict(sd)
+    for i in (1, 3, 5):
+        assert fresh[i].fmt == "gf4"
+        assert torch.equal(fresh[i].wdev, q[i].wdev)
+        assert torch.equal(fresh[i].dequantized_weight(), q[i].dequantized_weight())

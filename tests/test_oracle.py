@@ -274,3 +274,115 @@ def test_quantlinear_commit_restatement():
         assert torch.equal(lvl, torch.round(lvl))
         r = (w - Wq) / s                        # floor: r in [0, 1); floor+1: r in [-1, 0)
         assert r.min() >= lo - 1e-5 and r.max() < hi + 1e-5
+
+
+# ----------------------------------------------------------------------------- masked GF4
+def _masked_case(rng, group, kept):
+    v = (rng.normal(size=group) * 0.02).astype(np.float32)
+    keep = np.zeros(group, bool)
+    keep[rng.choice(group, size=kept, replace=False)] = True
+    v[~keep] = np.float32(rng.normal() * 5)   # masked values must not matter
+    return v, keep
+
+
+def test_gf4_masked_brute_force_small_groups():
+    """min(15, kept) classes over the kept values of a 32-wide group, checked against an
+    exhaustive search over every contiguous partition of the sorted kept values
+    (C(m-1, 14) partitions for m = 16..19); masked entries decode to exactly 0."""
+    rng = np.random.default_rng(11)
+    for kept in (0, 1, 5, 15, 16, 17, 19, 32):
+        v, keep = _masked_case(rng, 32, kept)
+        codes, book = O.gf4_quantize_masked(v[None], keep[None], group=32)
+        dec = O.gf4_dequant(codes, book, group=32).view(np.float16).astype(np.float64)[0]
+        bk = book[0, 0].view(np.float16).astype(np.float64)
+        assert (np.diff(bk) >= 0).all()                       # non-decreasing codebook
+        assert (dec[~keep] == 0).all() and not np.signbit(dec[~keep]).any()
+        kv = np.sort(v[keep].astype(np.float64))
+        if 0 < kept <= 15:                                    # one class per value: exact
+            assert np.array_equal(dec[keep], v[keep].astype(np.float16).astype(np.float64))
+        elif 15 < kept < 32:
+            cost, _ = _brute_partition(kv, 15)
+            # the partition the codes define, costed in fp64 on the raw values
+            cls = codes[0][keep]
+            got = sum(((v[keep][cls == c].astype(np.float64)
+                        - v[keep][cls == c].astype(np.float64).mean()) ** 2).sum()
+                      for c in np.unique(cls))
+            assert len(np.unique(cls)) == 15
+            assert abs(got - cost) <= 1e-12 + 1e-9 * cost
+        elif kept == 32:                                      # nothing masked: plain GF4
+            c2, b2 = O.gf4_quantize(v[None], group=32)
+            assert np.array_equal(codes, c2) and np.array_equal(book, b2)
+
+
+def test_gf4_masked_zero_entry_position():
+    """The zero entry sits after the strictly negative centroids (known answer)."""
+    v = np.array([-3, -2, -1, 1, 2, 3, 9, 9], np.float32) / 8
+    keep = np.array([1, 1, 1, 1, 1, 1, 0, 0], bool)
+    codes, book = O.gf4_quantize_masked(v[None], keep[None], group=8)
+    bk = book[0, 0].view(np.float16).astype(np.float32)
+    assert bk.tolist() == [-3 / 8, -2 / 8, -1 / 8, 0, 1 / 8, 2 / 8, 3 / 8] + [3 / 8] * 9
+    assert codes[0].tolist() == [0, 1, 2, 4, 5, 6, 3, 3]
+
+
+# ----------------------------------------------------------------------------- integer levels
+def test_levels_to_gf4_closed_form():
+    """decode == fp16(fp32(scale * level)) element by element (computed without the
+    codebook), for levels anywhere in [-8, 8] as long as each group spans <= 16."""
+    rng = np.random.default_rng(3)
+    N, K = 8, 512
+    base = rng.integers(-8, -6, size=(N, K // 128, 1))
+    lev = (base + rng.integers(0, 16, size=(N, K // 128, 128))).reshape(N, K).astype(np.float32)
+    lev[0, :128] = 0.0
+    lev[1, :128] = -0.0                                      # signed zeros decode to +0
+    scale = (rng.random(N) * 0.01 + 1e-4).astype(np.float32)
+    codes, book = O.levels_to_gf4(lev, scale)
+    dec = O.gf4_dequant(codes, book).view(np.float16)
+    want = (scale[:, None] * lev).astype(np.float32).astype(np.float16)
+    assert np.array_equal(dec.astype(np.float32), want.astype(np.float32))
+    assert book[1, 0, 0] == 0                                 # +0 bits
+    assert (np.diff(book.view(np.float16).astype(np.float32), axis=-1) >= 0).all()
+    bad = lev.copy()
+    bad[2, 0], bad[2, 1] = -8, 8                             # 17 levels in one group
+    with pytest.raises(ValueError):
+        O.levels_to_gf4(bad, scale)
+    bad = lev.copy()
+    bad[3, 5] = 0.5
+    with pytest.raises(ValueError):
+        O.levels_to_gf4(bad, scale)
+
+
+def test_quantlinear_commit_levels_encode_reference_weight():
+    """The reference's committed weight mask*s*round(Q+gate) (layers.py:39-45) is
+    scale * level with level = mask * Q_round: through levels_to_gf4 it decodes to
+    fp16 of the reference's fp32 weight, value for value."""
+    g = torch.Generator().manual_seed(5)
+    w = torch.randn(16, 256, generator=g) * 0.02
+    theta = torch.randn(16, 256, generator=g) * 3
+    mask = (torch.rand(16, 256, generator=g) > 0.3).float()
+    Wq, s, lvl = O.quantlinear_commit_weight(w, theta, mask)
+    codes, book = O.levels_to_gf4(lvl.numpy(), s.numpy())
+    dec = O.gf4_dequant(codes, book).view(np.float16).astype(np.float32)
+    assert np.array_equal(dec, Wq.numpy().astype(np.float16).astype(np.float32))
+
+
+# ----------------------------------------------------------------------------- AdaRound
+def test_adaround_hard_levels_known_answer():
+    W_floor = torch.tensor([[2.0, -3.0, 0.0, 7.0, -8.0, -9.0]])
+    alpha = torch.tensor([[5.0, -5.0, 5.0, 5.0, -5.0, -5.0]])
+    mask = torch.tensor([[1.0, 1.0, 0.0, 1.0, 1.0, 1.0]])
+    lv = O.adaround_hard_levels(W_floor, alpha, mask, -8, 7)
+    assert lv.tolist() == [[3.0, -3.0, 0.0, 7.0, -8.0, -8.0]]   # 8 -> 7 and -9 -> -8 clamped
+
+
+def test_adaround_hard_equals_soft_where_saturated():
+    """brecq.py:81-92 soft forward, restated with the continuous gate: where |alpha| >= 3
+    the clip makes h exactly 0 or 1, so the hard levels reproduce it exactly."""
+    g = torch.Generator().manual_seed(9)
+    W = torch.randn(8, 64, generator=g) * 4
+    W_floor = torch.floor(W)
+    alpha = torch.sign(torch.randn(8, 64, generator=g)) * (3 + torch.rand(8, 64, generator=g) * 5)
+    mask = (torch.rand(8, 64, generator=g) > 0.2).float()
+    soft_h = torch.clamp(torch.sigmoid(alpha) * 1.2 - 0.1, 0, 1)
+    assert bool(((soft_h == 0) | (soft_h == 1)).all())
+    soft = torch.clamp(mask * (W_floor + soft_h), -8, 7)
+    assert torch.equal(O.adaround_hard_levels(W_floor, alpha, mask, -8, 7), soft)
