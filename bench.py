@@ -221,8 +221,28 @@ def load_traffic(name: str):
     return None
 
 
+def time_gpu_pack(w: torch.Tensor, pw: PackedWeight, reps: int = 3):
+    """The GPU Jenks packer (fb_quantize_gf4_gpu) on the same weights the host packer
+    packed: best-of-reps seconds with the weights already in HBM, and whether its bytes
+    equal the host packer's."""
+    wd = w.to("cuda:0")
+    best = float("inf")
+    for _ in range(reps):
+        torch.cuda.synchronize()
+        t0 = torch.cuda.Event(enable_timing=True)
+        t1 = torch.cuda.Event(enable_timing=True)
+        t0.record()
+        codes, book = C.quantize_gf4_gpu(wd)
+        t1.record()
+        torch.cuda.synchronize()
+        best = min(best, t0.elapsed_time(t1) / 1e3)
+    same = bool(torch.equal(codes.cpu(), pw.codes) and torch.equal(book.cpu(), pw.meta))
+    del wd, codes, book
+    return {"gpu_s": best, "identical_to_host": same}
+
+
 def run_workload(name: str, steps: int, warmup: int, want_cpu: bool, check: bool = True,
-                 warm: bool = False, cache: dict | None = None):
+                 warm: bool = False, cache: dict | None = None, pack_check: bool = False):
     """cache: packed weights by (fmt, K, N, kind, rotation), reused across batch sizes (the
     weights are drawn before the activations, so they do not depend on the batch)."""
     fmt, K, N, B, kind, fwht = WORKLOADS[name]
@@ -239,6 +259,9 @@ def run_workload(name: str, steps: int, warmup: int, want_cpu: bool, check: bool
             cache.clear()  # one layer's packed weights resident at a time
             cache[key] = pw
     pack_s = time.perf_counter() - t
+    gpu_pack = None
+    if pack_check and fmt == "gf4":
+        gpu_pack = time_gpu_pack(w if not fb else C.fwht_rows(w, fb), pw)
     del w
     xd = x.to("cuda:0")
     y = torch.empty(B, N, dtype=xdt, device="cuda:0")
@@ -256,7 +279,7 @@ def run_workload(name: str, steps: int, warmup: int, want_cpu: bool, check: bool
         "GBps_warm": None if ms_warm is None else nbytes / (ms_warm * 1e-3) / 1e9,
         "us_per_call_graph": None if ms_graph is None else ms_graph * 1e3,
         "GBps_graph": None if ms_graph is None else nbytes / (ms_graph * 1e-3) / 1e9,
-        "tokens_per_s_equiv": B / (ms * 1e-3), "pack_s": pack_s,
+        "tokens_per_s_equiv": B / (ms * 1e-3), "pack_s": pack_s, "gpu_pack": gpu_pack,
     }
     if check:  # spot parity: sampled rows vs exact host decode + F.linear (fp32)
         yk = torch.empty(B, N, dtype=torch.float32, device="cuda:0")
@@ -285,6 +308,8 @@ def main():
     ap.add_argument("--sweep", action="store_true", help="also time every config shape")
     ap.add_argument("--sweep-out", default="bench_sweep.jsonl")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-pack-check", action="store_true",
+                    help="skip timing the GPU packer against the host packer")
     ap.add_argument("--warm", action="store_true",
                     help="also time one weight copy (Infinity-Cache warm) and a HIP graph")
     ap.add_argument("--calib-copy", type=int, default=0, metavar="BYTES",
@@ -327,7 +352,7 @@ def main():
                       f"parity {rec.get('parity_ok')}", file=sys.stderr, flush=True)
 
     rec, pw = run_workload(args.workload, args.steps, args.warmup, not args.no_cpu,
-                           warm=args.warm)
+                           warm=args.warm, pack_check=not args.no_pack_check)
     fmt, K, N, B = rec["fmt"], rec["K"], rec["N"], rec["B"]
     achieved = rec["GBps"]
     out = {
@@ -357,6 +382,8 @@ def main():
             "GBps_warm_single_copy": rec["GBps_warm"],
             "us_per_call_hipgraph_warm": rec["us_per_call_graph"],
             "parity_ok": rec.get("parity_ok"),
+            "pack_host_s": rec["pack_s"],
+            "pack_gpu": rec["gpu_pack"],
         },
         "roofline": {
             "bound": "hbm", "achieved": achieved, "peak": PEAK_GBS, "unit": "GB/s",

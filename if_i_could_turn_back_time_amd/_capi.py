@@ -31,7 +31,7 @@ EXPORTED = (
     "fb_abi_version", "fb_strerror", "fb_validate", "fb_device_bytes", "fb_workspace_bytes",
     "fb_quantize_gf4", "fb_quantize_gf4_masked", "fb_pack_levels_gf4", "fb_quantize_e2m1",
     "fb_fwht_rows_f32", "fb_to_device",
-    "fb_from_device", "fb_dequant_host", "fb_gemv", "fb_dequant",
+    "fb_from_device", "fb_dequant_host", "fb_gemv", "fb_dequant", "fb_quantize_gf4_gpu",
 )
 
 
@@ -71,6 +71,7 @@ def lib() -> ctypes.CDLL:
         "fb_dequant_host": (ctypes.c_int, [vp, vp, vp, sp]),
         "fb_gemv": (ctypes.c_int, [vp, vp, vp, sp, vp, sz, vp]),
         "fb_dequant": (ctypes.c_int, [vp, vp, i32, sp, vp]),
+        "fb_quantize_gf4_gpu": (ctypes.c_int, [vp, vp, i32, i32, vp, vp, vp]),
     }
     for name, (res, args) in sigs.items():
         fn = getattr(L, name)
@@ -237,3 +238,29 @@ def dequant_device(wdev: torch.Tensor, shape: FbShape, out_dtype=torch.float32) 
     check(lib().fb_dequant(_ptr(wdev), _ptr(out), DTYPE_CODE[out_dtype], ctypes.byref(shape),
                            _stream(wdev.device)))
     return out
+
+
+def quantize_gf4_gpu(w: torch.Tensor, keep: torch.Tensor | None = None):
+    """GF4 packing on the GPU (fb_quantize_gf4_gpu): fp32 device ``w [N,K]`` (and an
+    optional keep mask) -> device ``(codes uint8 [N,K/2], codebook int16 [N,K/128,16])``,
+    bit-identical to :func:`quantize_gf4`.  Raises on non-finite kept weights (checked
+    with one torch reduction before the launch)."""
+    if not w.is_cuda:
+        raise RuntimeError("fb_quantize_gf4_gpu needs a device tensor (ROCm GPU)")
+    w = w.detach().to(torch.float32).contiguous()
+    N, K = w.shape
+    kp = None
+    if keep is not None:
+        kp = (keep != 0).to(device=w.device, dtype=torch.uint8).contiguous()
+        if kp.shape != w.shape:
+            raise ValueError("keep mask must have the weight's shape")
+        finite = torch.isfinite(w) | (kp == 0)
+    else:
+        finite = torch.isfinite(w)
+    if not bool(finite.all()):
+        raise RuntimeError(strerror(-10))
+    codes = torch.empty(N, K // 2, dtype=torch.uint8, device=w.device)
+    book = torch.empty(N, max(K // 128, 1), 16, dtype=torch.int16, device=w.device)
+    check(lib().fb_quantize_gf4_gpu(_ptr(w), _ptr(kp) if kp is not None else None, N, K,
+                                    _ptr(codes), _ptr(book), _stream(w.device)))
+    return codes, book

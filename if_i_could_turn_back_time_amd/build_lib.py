@@ -59,13 +59,17 @@ def build(verbose: bool = False) -> Path:
     inc = [f"-I{INCLUDE}", f"-I{CSRC}"]
     host_o = BUILD / "fourbit_host.o"
     gemv_o = BUILD / "fourbit_gemv.o"
+    pack_o = BUILD / "fourbit_pack.o"
     steps = [
         ["g++", *HOST_FLAGS, *inc, "-c", str(CSRC / "fourbit_host.cpp"), "-o", str(host_o)],
         [_hipcc(), *HIP_FLAGS, *inc, "-c", str(CSRC / "fourbit_gemv.hip"), "-o", str(gemv_o)],
+        # the GPU packer must round every fp64 operation as the host packer does
+        [_hipcc(), *HIP_FLAGS, "-ffp-contract=off", *inc, "-c", str(CSRC / "fourbit_pack.hip"),
+         "-o", str(pack_o)],
     ]
     tmp = LIB.with_suffix(".so.tmp")
     steps.append([_hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", str(host_o), str(gemv_o),
-                  "-o", str(tmp), "-lpthread"])
+                  str(pack_o), "-o", str(tmp), "-lpthread"])
     for cmd in steps:
         if verbose:
             print(" ".join(cmd), flush=True)

@@ -584,10 +584,10 @@ __global__ __launch_bounds__(256) void dequant_kernel(const uint8_t* __restrict_
   constexpr int BB = FMT == FB_FMT_GF4 ? fb::kGf4BlockBytes : fb::kE2m1BlockBytes;
   const int G = K >> 7;
   const int GS = (G + 3) >> 2;
-  const int item = blockIdx.x * 256 + threadIdx.x;
-  if (item >= N * G) return;
-  const int n = item / G;
-  const int g = item - n * G;
+  const int64_t item = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (item >= (int64_t)N * G) return;
+  const int n = (int)(item / G);
+  const int g = (int)(item - (int64_t)n * G);
   Rec<FMT> r;
   load_rec_global<FMT>(w + ((int64_t)(n >> 4) * GS + (g >> 2)) * BB, (n & 15) + 16 * (g & 3), r);
   const int64_t o0 = (int64_t)n * K + g * 128;
@@ -763,8 +763,8 @@ int fb_dequant(const void* wdev, void* w_out, int32_t out_dtype, const fb_shape_
   if (out_dtype != FB_DT_F32 && out_dtype != FB_DT_F16 && out_dtype != FB_DT_BF16)
     return FB_ERR_DTYPE;
   if (!aligned16(wdev)) return FB_ERR_ALIGN;
-  const int items = s->N * (s->K / 128);
-  const int grid = (items + 255) / 256;
+  const int64_t items = (int64_t)s->N * (s->K / 128);  // < 2^31 (fb_validate)
+  const int grid = (int)((items + 255) / 256);
   hipStream_t hs = static_cast<hipStream_t>(stream);
   if (s->fmt == FB_FMT_GF4)
     hipLaunchKernelGGL(dequant_kernel<FB_FMT_GF4>, dim3(grid), dim3(256), 0, hs,

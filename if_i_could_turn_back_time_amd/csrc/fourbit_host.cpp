@@ -247,6 +247,7 @@ int fb_validate(const fb_shape_t* s) {
   if (s->fmt != FB_FMT_GF4 && s->fmt != FB_FMT_E2M1) return FB_ERR_FORMAT;
   if (s->N < 1 || s->K < 128 || s->K % 128 != 0 || s->B < 1) return FB_ERR_SHAPE;
   if (s->N > (1 << 26) || s->K > (1 << 24)) return FB_ERR_SHAPE;
+  if ((int64_t)s->N * (s->K / 128) > INT32_MAX) return FB_ERR_SHAPE;  // < 2^31 groups
   if (s->fmt == FB_FMT_GF4 && s->group != 128) return FB_ERR_GROUP;
   if (s->fmt == FB_FMT_E2M1 && s->group != 32) return FB_ERR_GROUP;
   if (s->fwht_block != 0 && (!is_pow2(s->fwht_block) || s->fwht_block < 2 ||

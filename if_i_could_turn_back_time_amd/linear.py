@@ -11,7 +11,8 @@ HIP kernel, which decodes in registers.
 
 Extra keyword arguments: ``fmt`` ('gf4' | 'e2m1'), ``hadamard`` (False, True for the
 default block, or an explicit power-of-two block: the weight is rotated offline and x
-in-kernel) and ``nthreads`` for the host packer.
+in-kernel), ``nthreads`` for the host packer and ``packer`` ('host' | 'gpu': where the
+GF4 Jenks search runs; both give the same bytes).
 
 ``in_features`` need not be a multiple of the 128-wide group: the packed weight gets
 zero columns up to the next multiple (masked, so they decode to exactly 0 and do not
@@ -99,16 +100,25 @@ class PackedWeight:
 
     @classmethod
     def quantize(cls, w: torch.Tensor, fmt: str = "gf4", fwht_block: int = 0, device=None,
-                 nthreads: int | None = None, keep: torch.Tensor | None = None) -> "PackedWeight":
+                 nthreads: int | None = None, keep: torch.Tensor | None = None,
+                 packer: str = "host") -> "PackedWeight":
         """Packs fp32 ``w [N,K]``.  ``keep`` (GF4 only, no rotation): entries where it is
-        0 decode to exactly 0."""
+        0 decode to exactly 0.  ``packer='gpu'`` runs the GF4 Jenks search on the GPU
+        (``device``, or cuda:0), with the same bytes as the host packer; E2M1 packing is
+        a single pass and always runs on the host."""
         w = w.detach().float().cpu().contiguous()
         N, K = w.shape
         if keep is not None and (fmt != "gf4" or fwht_block):
             raise ValueError("keep masks apply to unrotated GF4 packing only")
+        if packer not in ("host", "gpu"):
+            raise ValueError(f"packer must be 'host' or 'gpu', got {packer!r}")
         if fwht_block:
             w = C.fwht_rows(w, fwht_block, nthreads)
-        if fmt == "gf4":
+        if fmt == "gf4" and packer == "gpu":
+            dev = device if device is not None and torch.device(device).type == "cuda" else "cuda:0"
+            codes, meta = C.quantize_gf4_gpu(w.to(dev), None if keep is None else keep.to(dev))
+            codes, meta = codes.cpu(), meta.cpu()
+        elif fmt == "gf4":
             codes, meta = C.quantize_gf4(w, nthreads, keep)
         elif fmt == "e2m1":
             codes, meta = C.quantize_e2m1(w, nthreads)
@@ -173,7 +183,7 @@ class QuantLinear(nn.Linear):
 
     def __init__(self, linear_module: nn.Linear, bitwidth: int = 4, mask=None, *,
                  fmt: str = "gf4", hadamard=False, nthreads: int | None = None,
-                 pack: bool = True):
+                 pack: bool = True, packer: str = "host"):
         super().__init__(linear_module.in_features, linear_module.out_features,
                          bias=(linear_module.bias is not None))
         if bitwidth != 4:
@@ -191,6 +201,7 @@ class QuantLinear(nn.Linear):
         self.fmt = fmt
         self.fwht_block = (fwht_block_for(K) if hadamard is True else int(hadamard or 0))
         self.nthreads = nthreads
+        self.packer = packer
         self.register_buffer("mask", None if mask is None else torch.as_tensor(mask).float())
         self.register_buffer("codes", torch.empty(0, dtype=torch.uint8))
         self.register_buffer("meta", torch.empty(0, dtype=torch.uint8))
@@ -250,7 +261,9 @@ class QuantLinear(nn.Linear):
         if self.fmt != "gf4" or self.fwht_block:
             keep = None  # E2M1 codes zeros exactly; a rotation mixes masked and kept
         self._set_packed(PackedWeight.quantize(w, self.fmt, self.fwht_block,
-                                               nthreads=self.nthreads, keep=keep))
+                                               device=self.weight.device,
+                                               nthreads=self.nthreads, keep=keep,
+                                               packer=self.packer))
 
     pack = quantize
 

@@ -149,6 +149,18 @@ int fb_dequant_host(const uint8_t* codes, const void* meta, float* w_out, const 
 int fb_gemv(const void* wdev, const void* x, void* y, const fb_shape_t* s, void* ws,
             size_t ws_bytes, void* stream);
 
+/* GF4 packer on the GPU: the same arithmetic as fb_quantize_gf4 (keep == NULL) and
+ * fb_quantize_gf4_masked, one wavefront per (row, 128-group), fp64; the outputs are
+ * bit-identical to the host packers.  w fp32 [N,K], keep uint8 [N,K] or NULL, codes uint8
+ * [N,K/2] and codebook uint16 [N,K/128,16] are device pointers (canonical layout; convert
+ * with fb_to_device).  Asynchronous on the stream.  Non-finite kept weights are not
+ * detected here (the host packers reject them): their group's output is unspecified, so
+ * callers check first.  Replaces the reference's GPU Jenks search
+ * (cuda_helpers.py:151-211, one thread per split of a 2-class problem) with the 16-class
+ * DP. */
+int fb_quantize_gf4_gpu(const float* w, const uint8_t* keep, int32_t N, int32_t K,
+                        uint8_t* codes, uint16_t* codebook, void* stream);
+
 /* Device decode of the whole weight: w_out [N,K] of out_dtype (F32 always exact; F16
  * exact for GF4; BF16 exact for E2M1 within the bf16 normal range).  The same decode
  * code as fb_gemv; used for bit-exact parity.  Replaces the dequantizer expression

@@ -300,3 +300,61 @@ def test_lenet300_fixture_forward_gpu():
             h = torch.relu(yref)
         logits = q(x.to(DEV)).float().cpu()
         assert logits.shape == (40, 10) and torch.isfinite(logits).all()
+
+
+def _structured_weights(g, N, K):
+    w = torch.randn(N, K, generator=g) * 0.02
+    w[0, :128] = 0.0                                          # all zeros
+    w[1, :128] = 0.0625                                       # constant
+    w[2, :128] = torch.tensor([-0.03, 0.01, 0.02]).repeat(43)[:128]   # 3 distinct values
+    w[3] = torch.round(w[3] * 200) / 200                      # heavy ties
+    w[4, :128] = torch.randn(128, generator=g) * 1e3          # wide range
+    w[4, 128:256] = torch.randn(128, generator=g) * 1e-30     # tiny normals
+    w[5, :64] = -0.0                                          # signed zeros
+    w[5, 64:128] = torch.randn(64, generator=g) * 1e-40       # fp32 subnormals
+    w[6, :128] = torch.arange(128, dtype=torch.float32)       # 128 distinct, sorted
+    w[7, :128] = -torch.arange(128, dtype=torch.float32)      # reverse sorted
+    return w
+
+
+@pytest.mark.parametrize("density", [None, 1.0, 0.9, 0.3, 0.05, 0.0])
+def test_gpu_packer_bit_exact_vs_host(density):
+    """fb_quantize_gf4_gpu produces the host packer's bytes (fb_quantize_gf4 without a
+    mask, fb_quantize_gf4_masked with one): structured groups, ties, signed zeros, a wide
+    dynamic range, and every kept count from 0 to 128 across the masked cases."""
+    say("gpu packer", density)
+    g = torch.Generator().manual_seed(61)
+    N, K = 72, 1024
+    w = _structured_weights(g, N, K)
+    keep = None
+    if density is not None:
+        keep = torch.rand(N, K, generator=g) < density
+        for r in range(8, 8 + 40):                            # kept counts 0..117 in steps of 3
+            keep[r, :128] = torch.arange(128) < 3 * (r - 8)
+    hc, hb = C.quantize_gf4(w, 8, keep)
+    dc, db = C.quantize_gf4_gpu(w.to(DEV), None if keep is None else keep.to(DEV))
+    torch.cuda.synchronize()
+    assert torch.equal(dc.cpu(), hc)
+    assert torch.equal(db.cpu(), hb)
+
+
+def test_gpu_packer_rejects_nonfinite():
+    w = torch.zeros(2, 128)
+    w[1, 3] = float("inf")
+    with pytest.raises(RuntimeError, match="non-finite"):
+        C.quantize_gf4_gpu(w.to(DEV))
+    keep = torch.ones(2, 128, dtype=torch.bool)
+    keep[1, 3] = False                                        # masked: never read
+    C.quantize_gf4_gpu(w.to(DEV), keep.to(DEV))
+
+
+def test_quantlinear_gpu_packer_matches_host_on_lenet300():
+    """QuantLinear(packer='gpu') on the pruned LeNet300 (masked, ragged in_features):
+    the same packed buffers as the host packer."""
+    say("lenet300 gpu packer")
+    host = quantize_module(lenet300_from_fixture())
+    gpu = quantize_module(lenet300_from_fixture().to(DEV), packer="gpu")
+    for i in (1, 3, 5):
+        assert torch.equal(gpu[i].codes.cpu(), host[i].codes)
+        assert torch.equal(gpu[i].meta.cpu(), host[i].meta)
+        assert torch.equal(gpu[i].wdev.cpu(), host[i].wdev)
