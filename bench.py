@@ -199,6 +199,23 @@ def cpu_baseline(pw: PackedWeight, x: torch.Tensor, budget_s: float = 12.0):
     B = x.shape[0]
     frac = rows / N
     sample_bytes = pw.algorithmic_bytes(B) * frac
+    # secondary: F.linear on an already-dequantized fp32 weight (the hard_quant forward,
+    # layers.py:34-35), same rows
+    codes = O.unpack_nibbles(codes_all[:rows].numpy())
+    if pw.fmt_name == "gf4":
+        Wc = O.dequant_f32("gf4", codes, meta_all[:rows].numpy().view(np.uint16))
+    else:
+        Wc = O.dequant_f32("e2m1", codes, meta_all[:rows].numpy())
+    torch.nn.functional.linear(x.float(), Wc)
+    hq = []
+    t_start = time.perf_counter()
+    while len(hq) < 10 or (time.perf_counter() - t_start) < 2.0:
+        t = time.perf_counter()
+        torch.nn.functional.linear(x.float(), Wc)
+        hq.append(time.perf_counter() - t)
+        if time.perf_counter() - t_start > 4.0:
+            break
+    hq_med = float(np.median(hq))
     return {
         "value": sample_bytes / med / 1e9,
         "unit": "GB/s",
@@ -208,6 +225,11 @@ def cpu_baseline(pw: PackedWeight, x: torch.Tensor, budget_s: float = 12.0):
                    f"median of {len(times)} calls); CPU: {platform.processor() or platform.machine()}, "
                    f"os.cpu_count()={threads}"),
         "us_per_call_full_layer_est": med / frac * 1e6,
+        "hard_quant_cached_fp32": {
+            "GBps_of_packed_bytes": sample_bytes / hq_med / 1e9,
+            "us_per_call_full_layer_est": hq_med / frac * 1e6,
+            "note": "F.linear on a cached fp32 weight (reads N*K*4 bytes, not the packed ones)",
+        },
     }
 
 
@@ -242,7 +264,8 @@ def time_gpu_pack(w: torch.Tensor, pw: PackedWeight, reps: int = 3):
 
 
 def run_workload(name: str, steps: int, warmup: int, want_cpu: bool, check: bool = True,
-                 warm: bool = False, cache: dict | None = None, pack_check: bool = False):
+                 warm: bool = False, cache: dict | None = None, pack_check: bool = False,
+                 packer: str = "host"):
     """cache: packed weights by (fmt, K, N, kind, rotation), reused across batch sizes (the
     weights are drawn before the activations, so they do not depend on the batch)."""
     fmt, K, N, B, kind, fwht = WORKLOADS[name]
@@ -254,7 +277,7 @@ def run_workload(name: str, steps: int, warmup: int, want_cpu: bool, check: bool
     if cache is not None and key in cache:
         pw = cache[key]
     else:
-        pw = PackedWeight.quantize(w, fmt, fwht_block=fb, device="cuda:0")
+        pw = PackedWeight.quantize(w, fmt, fwht_block=fb, device="cuda:0", packer=packer)
         if cache is not None:
             cache.clear()  # one layer's packed weights resident at a time
             cache[key] = pw
@@ -310,6 +333,9 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-pack-check", action="store_true",
                     help="skip timing the GPU packer against the host packer")
+    ap.add_argument("--packer", choices=("host", "gpu"), default="host",
+                    help="where the GF4 Jenks search runs when packing the synthetic weights "
+                         "(same bytes either way)")
     ap.add_argument("--warm", action="store_true",
                     help="also time one weight copy (Infinity-Cache warm) and a HIP graph")
     ap.add_argument("--calib-copy", type=int, default=0, metavar="BYTES",
@@ -343,7 +369,7 @@ def main():
                 if name == args.workload:
                     continue
                 rec, pw = run_workload(name, max(50, args.steps // 2), args.warmup, False,
-                                       warm=args.warm, cache=cache)
+                                       warm=args.warm, cache=cache, packer=args.packer)
                 del pw
                 torch.cuda.empty_cache()
                 f.write(json.dumps(rec) + "\n")
@@ -352,7 +378,7 @@ def main():
                       f"parity {rec.get('parity_ok')}", file=sys.stderr, flush=True)
 
     rec, pw = run_workload(args.workload, args.steps, args.warmup, not args.no_cpu,
-                           warm=args.warm, pack_check=not args.no_pack_check)
+                           warm=args.warm, pack_check=not args.no_pack_check, packer=args.packer)
     fmt, K, N, B = rec["fmt"], rec["K"], rec["N"], rec["B"]
     achieved = rec["GBps"]
     out = {
@@ -384,6 +410,8 @@ def main():
             "parity_ok": rec.get("parity_ok"),
             "pack_host_s": rec["pack_s"],
             "pack_gpu": rec["gpu_pack"],
+            "cpu_hard_quant_cached_fp32": (rec["cpu_baseline"] or {}).get("hard_quant_cached_fp32")
+            if rec.get("cpu_baseline") else None,
         },
         "roofline": {
             "bound": "hbm", "achieved": achieved, "peak": PEAK_GBS, "unit": "GB/s",
