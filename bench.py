@@ -58,6 +58,8 @@ WORKLOADS = {
     "gf4_k8192_n8192_b16": ("gf4", 8192, 8192, 16, "cfg1", False),
     "gf4_k8192_n28672_b8": ("gf4", 8192, 28672, 8, "cfg1", False),
     "gf4_k8192_n28672_b16": ("gf4", 8192, 28672, 16, "cfg1", False),
+    # the reference's own 4-bit weight (QuantLinear.commit) as GF4 integer-level codebooks
+    "int4ref_k8192_n28672_b1": ("int4ref", 8192, 28672, 1, "cfg4", False),
 }
 DEFAULT = "gf4_k8192_n28672_b1"
 
@@ -269,7 +271,7 @@ def run_workload(name: str, steps: int, warmup: int, want_cpu: bool, check: bool
     """cache: packed weights by (fmt, K, N, kind, rotation), reused across batch sizes (the
     weights are drawn before the activations, so they do not depend on the batch)."""
     fmt, K, N, B, kind, fwht = WORKLOADS[name]
-    xdt = torch.float16 if fmt == "gf4" else torch.bfloat16
+    xdt = torch.float16 if fmt in ("gf4", "int4ref") else torch.bfloat16
     w, x = synth(kind, N, K, B, xdt)
     fb = fwht_block_for(K) if fwht else 0
     key = (fmt, K, N, kind, fb)
@@ -277,13 +279,19 @@ def run_workload(name: str, steps: int, warmup: int, want_cpu: bool, check: bool
     if cache is not None and key in cache:
         pw = cache[key]
     else:
-        pw = PackedWeight.quantize(w, fmt, fwht_block=fb, device="cuda:0", packer=packer)
+        if fmt == "int4ref":
+            # layers.py:23-26 and :39-45 with the rounding gate closed: level = floor(w / s),
+            # s = amax / 7 + 1e-12, packed as integer levels times s
+            sc = w.abs().amax(dim=1, keepdim=True) / 7 + 1e-12
+            pw = PackedWeight.from_levels(torch.floor(w / sc), sc.reshape(-1), device="cuda:0")
+        else:
+            pw = PackedWeight.quantize(w, fmt, fwht_block=fb, device="cuda:0", packer=packer)
         if cache is not None:
             cache.clear()  # one layer's packed weights resident at a time
             cache[key] = pw
     pack_s = time.perf_counter() - t
     gpu_pack = None
-    if pack_check and fmt == "gf4":
+    if pack_check and fmt == "gf4" and pw.fmt_name == "gf4":
         gpu_pack = time_gpu_pack(w if not fb else C.fwht_rows(w, fb), pw)
     del w
     xd = x.to("cuda:0")

@@ -358,3 +358,38 @@ def test_quantlinear_gpu_packer_matches_host_on_lenet300():
         assert torch.equal(gpu[i].codes.cpu(), host[i].codes)
         assert torch.equal(gpu[i].meta.cpu(), host[i].meta)
         assert torch.equal(gpu[i].wdev.cpu(), host[i].wdev)
+
+
+def test_gemv_in_hip_graph_replays_match_eager():
+    """fb_gemv captured in a HIP graph (it records kernel launches only: no memset nodes,
+    no workspace): several replays, with eager work and synchronisations between them,
+    each equal to the eager result, bit for bit."""
+    say("hip graph")
+    g = torch.Generator().manual_seed(71)
+    for fmt, N, K, B, fb in (("gf4", 4096, 2048, 1, 0), ("e2m1", 3000, 1024, 4, 0),
+                             ("gf4", 2048, 4096, 2, 4096)):
+        w = torch.randn(N, K, generator=g) * 0.02
+        pw = PackedWeight.quantize(w, fmt, fwht_block=fb, device=DEV)
+        xdt = torch.float16 if fmt == "gf4" else torch.bfloat16
+        x = torch.randn(B, K, generator=g).to(xdt).to(DEV)
+        y = torch.empty(B, N, dtype=torch.float32, device=DEV)
+        pw.gemv(x, out=y)
+        torch.cuda.synchronize()
+        eager = y.clone()
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.stream(s):
+            pw.gemv(x, out=y)  # warm-up on the capture stream
+            torch.cuda.synchronize()
+            with torch.cuda.graph(graph, stream=s):
+                pw.gemv(x, out=y)
+        torch.cuda.synchronize()
+        for rep in range(4):
+            y.fill_(float("nan"))                      # eager work between replays
+            x2 = (x.float() * 2).to(xdt)               # unrelated eager kernel
+            torch.cuda.synchronize()
+            graph.replay()
+            torch.cuda.synchronize()
+            assert torch.equal(y, eager), f"{fmt} fb={fb} replay {rep}"
+            assert x2.shape == x.shape
