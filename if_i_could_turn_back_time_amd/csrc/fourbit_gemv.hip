@@ -527,6 +527,12 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(
       x_preload(xp, xg, K, k0, per_row, B * per_row, row_of, tid);
     int u0 = wave, u1 = wave + kWaves;
     issue(s, u0, ring[0]);
+    // The next slice's x (into registers) and first weight unit are requested before the
+    // barrier that closes the previous slice, so their latency overlaps the slowest wave.
+    if (s > 0) {  // every wave is done with the previous slice: x may be restaged
+      __syncthreads();
+      if (threadIdx.x == 0) *counter = 2 * kWaves;
+    }
     if (s == 0) {
       if (threadIdx.x == 0) *counter = 2 * kWaves;
       if (threadIdx.x < 16) reinterpret_cast<u32x4*>(zeros)[threadIdx.x] = u32x4{0u, 0u, 0u, 0u};
@@ -555,9 +561,8 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(
       if (u0 >= nu) break;
       process(ring[0], s, u0);
     }
-    __syncthreads();  // slice done: x may be restaged, slots are complete
-    if (threadIdx.x == 0) *counter = 2 * kWaves;
   }
+  __syncthreads();  // every slice done: slots are complete
 
   // y[col][row] = sum over the spans of the tile, in span order
   const int nt = t1 - t0;
