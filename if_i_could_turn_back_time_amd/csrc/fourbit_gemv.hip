@@ -264,26 +264,28 @@ struct XRot {
   uint2 v[kXPre];
 };
 
+// The loads are unconditional (lanes past kw, and waves past the last sub-block, read
+// values that stage_fwht does not use), so the four are issued back to back and nothing
+// waits for them before stage_fwht.
 __device__ __forceinline__ void rot_preload(XRot& xr, const uint16_t* __restrict__ x, int K,
                                             int B, int k0, int kw, int tid) {
-  const int wave = tid >> 6, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
   const int nsb = (kw + 255) >> 8;
 #pragma unroll
   for (int i = 0; i < kXPre; ++i) {
-    const int sb = wave + i * kWaves;  // flat sub-block index over (row, sub-block)
-    if (sb < B * nsb) {
-      const int b = sb / nsb;
-      const int k = (sb - b * nsb) * 256 + lane * 4;
-      xr.v[i] = k < kw ? *reinterpret_cast<const uint2*>(x + (int64_t)b * K + k0 + k)
-                       : uint2{0u, 0u};
-    }
+    // flat sub-block index over (row, sub-block), uniform; past the last one the wave
+    // re-reads its first (the values are not used) so that no load is conditional
+    const int sb = wave + i * kWaves < B * nsb ? wave + i * kWaves : min(wave, B * nsb - 1);
+    const int b = sb / nsb;
+    const int k = (sb - b * nsb) * 256 + lane * 4;
+    xr.v[i] = *reinterpret_cast<const uint2*>(x + (int64_t)b * K + k0 + (k < kw ? k : 0));
   }
 }
 
 __device__ void stage_fwht(uint8_t* lds, float* F, const XRot& xr, const uint16_t* __restrict__ x,
                            int K, int B, int k0, int kw, int nsl, int RS, int fb, float sc,
                            int tid) {
-  const int wave = tid >> 6, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
   const int lg_fb = 31 - __builtin_clz(fb);
   const int nsb = (kw + 255) >> 8;  // 256-value sub-blocks per batch row
   auto store_x = [&](int b, int k, float v) {
@@ -305,6 +307,7 @@ __device__ void stage_fwht(uint8_t* lds, float* F, const XRot& xr, const uint16_
 #pragma unroll
       for (int j = 0; j < kXPre; ++j)
         if (j == i) raw = xr.v[j];
+      if (!live) raw = uint2{0u, 0u};
     } else if (live) {
       raw = *reinterpret_cast<const uint2*>(x + (int64_t)b * K + k0 + k);
     }
@@ -425,11 +428,12 @@ __device__ __forceinline__ f32x4 unit_partial(const Rec<FMT>& r, const uint8_t* 
 // ---------------------------------------------------------------------------------
 // The GEMV kernel
 // ---------------------------------------------------------------------------------
-// Arguments are ordered so that the first 14 dwords, which arrive preloaded in SGPRs, hold
-// everything the first loads need; y, N, ydt and xbytes come through a scalar load that
-// completes while the first loads are in flight.  tq, tr: row tiles per workgroup = tq (+1 for the first
-// tr workgroups); GS: 512-element spans per row; RS: LDS bytes per staged x row; spl_m:
-// div_magic(SPL); xbytes: LDS bytes of staged x (the partial-sum slots follow).
+// The first 14 argument dwords arrive preloaded in SGPRs and hold everything but the
+// output; y, N and ydt come through a scalar load that completes long before the epilogue
+// needs them (the LDS size of staged x and the rotation scale are derived in the kernel, so
+// nothing early waits for that load).  tq, tr: row tiles per workgroup = tq (+1 for the
+// first tr workgroups); GS: 512-element spans per row; RS: LDS bytes per staged x row;
+// spl_m: div_magic(SPL).
 // MODE: kFlat = one K-slice, no rotation (the common case); kSliced = several K-slices, no
 // rotation; kRotated = rotation of x.  Each is compiled with only the staging it needs, which
 // keeps the kernel short and its registers few.
@@ -438,8 +442,10 @@ template <int FMT, int XDT, int MODE>
 __global__ __launch_bounds__(kThreads) void gemv_kernel(
     const uint8_t* __restrict__ w, const void* __restrict__ x, int K, int B, int SPL, int GS,
     int tq, int tr, unsigned spl_m, int S, int fwht_block, int RS, void* __restrict__ y, int N,
-    int ydt, int xbytes, float fwht_scale) {
+    int ydt) {
   extern __shared__ __align__(16) uint8_t lds[];
+  const int xbytes = x_lds_bytes(B, K, SPL, fwht_block);  // staged x; the slots follow
+  const float fwht_scale = MODE == kRotated ? 1.0f / __builtin_sqrtf((float)fwht_block) : 1.0f;
   constexpr int BB = FMT == FB_FMT_GF4 ? fb::kGf4BlockBytes : fb::kE2m1BlockBytes;
   const int g = blockIdx.x;
   const int t0 = g * tq + min(g, tr);
@@ -526,6 +532,9 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(
     else
       x_preload(xp, xg, K, k0, per_row, B * per_row, row_of, tid);
     int u0 = wave, u1 = wave + kWaves;
+    // the rotation cannot start before its x has arrived, and x loads queued behind the
+    // first weight unit arrive later: wait for x first
+    if constexpr (rot) __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
     issue(s, u0, ring[0]);
     // The next slice's x (into registers) and first weight unit are requested before the
     // barrier that closes the previous slice, so their latency overlaps the slowest wave.
@@ -717,8 +726,7 @@ int launch_gemv(const void* wdev, const void* x, void* y, const fb_shape_t* s, c
   hipLaunchKernelGGL(kern, dim3(pl.grid), dim3(kThreads), pl.lds, stream,
                      static_cast<const uint8_t*>(wdev), x, s->K, s->B, pl.SPL, pl.GS, pl.tq,
                      pl.tr, div_magic(pl.SPL), pl.S, s->fwht_block, x_row_stride(pl.SPL * 4), y,
-                     s->N, s->y_dtype, x_lds_bytes(s->B, s->K, pl.SPL, s->fwht_block),
-                     s->fwht_block ? 1.0f / std::sqrt((float)s->fwht_block) : 1.0f);
+                     s->N, s->y_dtype);
   return hipGetLastError() == hipSuccess ? FB_OK : FB_ERR_HIP;
 }
 
