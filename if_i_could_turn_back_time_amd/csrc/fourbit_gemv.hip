@@ -253,7 +253,7 @@ __device__ void stage_plain(uint8_t* lds, const XPre& xp, const uint16_t* __rest
 // layout (rounded to fp16); kw is a whole number of blocks of fb.
 //  - Stages 0..7 run in registers.  The B*kw values are cut into 256-value sub-blocks,
 //    taken by the waves in turn (sub-block i by wave i % kWaves); lane l holds values
-//    4l..4l+3: stages 0-1 are in-lane, stages 2-7 pair lanes l and l ^ 2^(s-2).
+//    4l..4l+3: stages 0-1 are in-lane, stages 2-7 pair lanes l and l ^ 2^(s-2) (lane_xor).
 //    The x of a wave's first kXPre sub-blocks is loaded by rot_preload before the slice's
 //    weight loads are issued.
 //  - Blocks larger than 256 go through LDS (F: B*kw floats) once: each 4096-value piece is
@@ -280,6 +280,32 @@ __device__ __forceinline__ void rot_preload(XRot& xr, const uint16_t* __restrict
     const int k = (sb - b * nsb) * 256 + lane * 4;
     xr.v[i] = *reinterpret_cast<const uint2*>(x + (int64_t)b * K + k0 + (k < kw ? k : 0));
   }
+}
+
+// v of lane ^ m for a compile-time m (after unrolling): m = 1, 2 by DPP quad permutes and
+// m = 4, 8 by DPP row shifts (one per direction, selected by the lane bit), all on the VALU;
+// m = 16 by ds_swizzle (xor within 32 lanes); m = 32 by ds_bpermute.
+__device__ __forceinline__ float lane_xor(float v, int m, int lane) {
+  const int iv = __builtin_bit_cast(int, v);
+  int r;
+  if (m == 1) {
+    r = __builtin_amdgcn_update_dpp(0, iv, 0xB1, 0xF, 0xF, false);  // quad_perm [1,0,3,2]
+  } else if (m == 2) {
+    r = __builtin_amdgcn_update_dpp(0, iv, 0x4E, 0xF, 0xF, false);  // quad_perm [2,3,0,1]
+  } else if (m == 4) {
+    const int up = __builtin_amdgcn_update_dpp(0, iv, 0x104, 0xF, 0xF, false);  // from lane + 4
+    const int dn = __builtin_amdgcn_update_dpp(0, iv, 0x114, 0xF, 0xF, false);  // from lane - 4
+    r = (lane & 4) ? dn : up;
+  } else if (m == 8) {
+    const int up = __builtin_amdgcn_update_dpp(0, iv, 0x108, 0xF, 0xF, false);  // from lane + 8
+    const int dn = __builtin_amdgcn_update_dpp(0, iv, 0x118, 0xF, 0xF, false);  // from lane - 8
+    r = (lane & 8) ? dn : up;
+  } else if (m == 16) {
+    r = __builtin_amdgcn_ds_swizzle(iv, 0x401F);  // bitmask mode: xor 16 within 32 lanes
+  } else {
+    r = __builtin_amdgcn_ds_bpermute((lane ^ m) << 2, iv);
+  }
+  return __builtin_bit_cast(float, r);
 }
 
 __device__ void stage_fwht(uint8_t* lds, float* F, const XRot& xr, const uint16_t* __restrict__ x,
@@ -328,7 +354,7 @@ __device__ void stage_fwht(uint8_t* lds, float* F, const XRot& xr, const uint16_
         const bool upper = (lane & m) != 0;
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          const float o = __shfl_xor(v[e], m);
+          const float o = lane_xor(v[e], m, lane);
           v[e] = upper ? o - v[e] : v[e] + o;
         }
       }
@@ -367,7 +393,7 @@ __device__ void stage_fwht(uint8_t* lds, float* F, const XRot& xr, const uint16_
           const bool upper = (lane & m) != 0;
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
-            const float o = __shfl_xor(v[r], m);
+            const float o = lane_xor(v[r], m, lane);
             v[r] = upper ? o - v[r] : v[r] + o;
           }
         }
