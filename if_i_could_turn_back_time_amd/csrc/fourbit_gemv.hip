@@ -308,6 +308,10 @@ __device__ __forceinline__ float lane_xor(float v, int m, int lane) {
   return __builtin_bit_cast(float, r);
 }
 
+// Position of value p in the fp32 rotation scratch: 16 floats of padding after every 1024,
+// so the four 1024-apart lane groups of a phase-2 read fall in different banks.
+__host__ __device__ __forceinline__ int fpad(int p) { return p + (p >> 10) * 16; }
+
 __device__ void stage_fwht(uint8_t* lds, float* F, const XRot& xr, const uint16_t* __restrict__ x,
                            int K, int B, int k0, int kw, int nsl, int RS, int fb, float sc,
                            int tid) {
@@ -364,19 +368,21 @@ __device__ void stage_fwht(uint8_t* lds, float* F, const XRot& xr, const uint16_
 #pragma unroll
       for (int e = 0; e < 4; ++e) store_x(b, k + e, v[e]);
     } else {
-      *reinterpret_cast<f32x4*>(F + b * kw + k) = f32x4{v[0], v[1], v[2], v[3]};
+      const int p = b * kw + k;
+      *reinterpret_cast<f32x4*>(F + fpad(p)) = f32x4{v[0], v[1], v[2], v[3]};
     }
   }
   if (lg_fb > 8) {
     __syncthreads();
     const int total = B * kw;
+    const float inv_kw = 1.0f / (float)kw;
     for (int base = 0; base < total; base += 4096) {
       float v[4];
       int e[4];
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         e[r] = base + (wave * 16 + (lane & 15)) + 256 * (r + 4 * (lane >> 4));
-        v[r] = e[r] < total ? F[e[r]] : 0.0f;
+        v[r] = e[r] < total ? F[fpad(e[r])] : 0.0f;
       }
       if (lg_fb > 8) {
         bfly(v[0], v[1]);
@@ -401,7 +407,10 @@ __device__ void stage_fwht(uint8_t* lds, float* F, const XRot& xr, const uint16_
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         if (e[r] < total) {
-          const int b = e[r] / kw;
+          // e < 16 * kw < 2^24: the float quotient is within one of e / kw
+          int b = (int)((float)e[r] * inv_kw);
+          b -= b * kw > e[r] ? 1 : 0;
+          b += (b + 1) * kw <= e[r] ? 1 : 0;
           store_x(b, e[r] - b * kw, v[r]);
         }
       }
@@ -419,7 +428,7 @@ __device__ void stage_fwht(uint8_t* lds, float* F, const XRot& xr, const uint16_
 
 __host__ __device__ inline int x_lds_bytes(int B, int K, int SPL, int fwht_block) {
   int b = B * x_row_stride(SPL * 4);
-  if (fwht_block > 256) b += B * min(K, SPL * 512) * 4;  // fp32 scratch of the rotation
+  if (fwht_block > 256) b += fpad(B * min(K, SPL * 512)) * 4 + 64;  // fp32 scratch of the rotation
   return (b + 15) & ~15;
 }
 
