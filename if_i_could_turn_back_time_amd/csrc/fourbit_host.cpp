@@ -212,6 +212,13 @@ uint8_t e2m1_index(double a) {
 
 bool is_pow2(int v) { return v > 0 && (v & (v - 1)) == 0; }
 
+// Threads for the layout transforms (pure permutations): one per 64K items, at most the
+// machine's hardware threads (and 16).
+int layout_threads(int64_t items) {
+  const int hw = (int)std::max(1u, std::thread::hardware_concurrency());
+  return (int)std::max<int64_t>(1, std::min<int64_t>({items / 65536 + 1, hw, 16}));
+}
+
 }  // namespace
 
 // ===================================================================================
@@ -425,17 +432,20 @@ int fb_to_device(const uint8_t* codes, const void* meta, void* wdev, const fb_sh
   const int64_t items = (int64_t)s->N * ipr;
   std::memset(wdev, 0, fb_device_bytes(s));
   uint8_t* out = (uint8_t*)wdev;
-  for (int64_t i = 0; i < items; ++i) {
-    const int64_t n = i / ipr, g = i % ipr;
-    const uint8_t* crow = codes + n * (s->K / 2) + g * 64;  // 128 codes = 64 bytes
-    if (s->fmt == FB_FMT_GF4) {
-      const uint16_t* book = (const uint16_t*)meta + (n * ipr + g) * 16;
-      fb::gf4_encode_item(crow, book, out, n, g, s->K);
-    } else {
-      const uint8_t* sc = (const uint8_t*)meta + (n * ipr + g) * 4;
-      fb::e2m1_encode_item(crow, sc, out, n, g, s->K);
+  // items write disjoint bytes of the stream
+  parallel_for(items, layout_threads(items), [&](int64_t b, int64_t e) {
+    for (int64_t i = b; i < e; ++i) {
+      const int64_t n = i / ipr, g = i % ipr;
+      const uint8_t* crow = codes + n * (s->K / 2) + g * 64;  // 128 codes = 64 bytes
+      if (s->fmt == FB_FMT_GF4) {
+        const uint16_t* book = (const uint16_t*)meta + (n * ipr + g) * 16;
+        fb::gf4_encode_item(crow, book, out, n, g, s->K);
+      } else {
+        const uint8_t* sc = (const uint8_t*)meta + (n * ipr + g) * 4;
+        fb::e2m1_encode_item(crow, sc, out, n, g, s->K);
+      }
     }
-  }
+  });
   return FB_OK;
 }
 
@@ -446,17 +456,19 @@ int fb_from_device(const void* wdev, uint8_t* codes, void* meta, const fb_shape_
   const int64_t ipr = s->K / fb::kItemCodes;
   const int64_t items = (int64_t)s->N * ipr;
   const uint8_t* in = (const uint8_t*)wdev;
-  for (int64_t i = 0; i < items; ++i) {
-    const int64_t n = i / ipr, g = i % ipr;
-    uint8_t* crow = codes + n * (s->K / 2) + g * 64;
-    if (s->fmt == FB_FMT_GF4) {
-      uint16_t* book = (uint16_t*)meta + (n * ipr + g) * 16;
-      fb::gf4_decode_item(in, n, g, s->K, crow, book);
-    } else {
-      uint8_t* sc = (uint8_t*)meta + (n * ipr + g) * 4;
-      fb::e2m1_decode_item(in, n, g, s->K, crow, sc);
+  parallel_for(items, layout_threads(items), [&](int64_t b, int64_t e) {
+    for (int64_t i = b; i < e; ++i) {
+      const int64_t n = i / ipr, g = i % ipr;
+      uint8_t* crow = codes + n * (s->K / 2) + g * 64;
+      if (s->fmt == FB_FMT_GF4) {
+        uint16_t* book = (uint16_t*)meta + (n * ipr + g) * 16;
+        fb::gf4_decode_item(in, n, g, s->K, crow, book);
+      } else {
+        uint8_t* sc = (uint8_t*)meta + (n * ipr + g) * 4;
+        fb::e2m1_decode_item(in, n, g, s->K, crow, sc);
+      }
     }
-  }
+  });
   return FB_OK;
 }
 
