@@ -220,8 +220,20 @@ def gemv(wdev: torch.Tensor, x: torch.Tensor, y: torch.Tensor, shape: FbShape,
     """y[B,N] = x'[B,K] . W^T on the GPU (asynchronous on the current stream)."""
     if not (wdev.is_cuda and x.is_cuda and y.is_cuda):
         raise RuntimeError("fb_gemv needs device tensors (ROCm GPU)")
+    if not (wdev.device == x.device == y.device):
+        raise ValueError(f"fb_gemv operands are on different devices: weight {wdev.device}, "
+                         f"x {x.device}, y {y.device}")
     if not (x.is_contiguous() and y.is_contiguous()):
         raise ValueError("x and y must be contiguous")
+    if x.dtype not in DTYPE_CODE or y.dtype not in DTYPE_CODE:
+        raise ValueError("x and y must be float16, bfloat16 or float32 tensors")
+    if DTYPE_CODE[x.dtype] != shape.x_dtype or DTYPE_CODE[y.dtype] != shape.y_dtype:
+        raise ValueError("x / y dtypes do not match the shape's x_dtype / y_dtype")
+    if tuple(x.shape) != (shape.B, shape.K) or tuple(y.shape) != (shape.B, shape.N):
+        raise ValueError(f"x {tuple(x.shape)} / y {tuple(y.shape)} do not match the shape "
+                         f"(B={shape.B}, K={shape.K}, N={shape.N})")
+    if wdev.numel() < device_bytes(shape):
+        raise ValueError("weight stream is smaller than fb_device_bytes(shape)")
     need = workspace_bytes(shape)
     if need and (workspace is None or workspace.numel() < need):
         workspace = new_workspace(shape, x.device)
@@ -234,6 +246,8 @@ def gemv(wdev: torch.Tensor, x: torch.Tensor, y: torch.Tensor, shape: FbShape,
 def dequant_device(wdev: torch.Tensor, shape: FbShape, out_dtype=torch.float32) -> torch.Tensor:
     if not wdev.is_cuda:
         raise RuntimeError("fb_dequant needs a device tensor (ROCm GPU)")
+    if wdev.numel() < device_bytes(shape):
+        raise ValueError("weight stream is smaller than fb_device_bytes(shape)")
     out = torch.empty(shape.N, shape.K, dtype=out_dtype, device=wdev.device)
     check(lib().fb_dequant(_ptr(wdev), _ptr(out), DTYPE_CODE[out_dtype], ctypes.byref(shape),
                            _stream(wdev.device)))
