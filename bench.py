@@ -4,7 +4,7 @@
 A "step" is one fused dequant-GEMV call over one layer for one batch of activations,
 with the packed weight and x already resident in HBM.  The default workload is the
 north-star layer: GF4 (Jenks-16 codebooks, group 128), K=8192 -> N=28672, batch 1
-(BASELINE.json configs[3]).  Prints ONE JSON line (the contract in the repo README);
+(BASELINE.json configs[3]).  Prints ONE JSON line (metric, value, unit, roofline, cpu_baseline, ...);
 ``--sweep`` additionally writes one line per config shape to ``--sweep-out``.
 
 Throughput = algorithmic bytes per call / time per call, with
