@@ -32,6 +32,7 @@ EXPORTED = (
     "fb_quantize_gf4", "fb_quantize_gf4_masked", "fb_pack_levels_gf4", "fb_quantize_e2m1",
     "fb_fwht_rows_f32", "fb_to_device",
     "fb_from_device", "fb_dequant_host", "fb_gemv", "fb_dequant", "fb_quantize_gf4_gpu",
+    "fb_quantize_e2m1_gpu",
 )
 
 
@@ -72,6 +73,7 @@ def lib() -> ctypes.CDLL:
         "fb_gemv": (ctypes.c_int, [vp, vp, vp, sp, vp, sz, vp]),
         "fb_dequant": (ctypes.c_int, [vp, vp, i32, sp, vp]),
         "fb_quantize_gf4_gpu": (ctypes.c_int, [vp, vp, i32, i32, vp, vp, vp]),
+        "fb_quantize_e2m1_gpu": (ctypes.c_int, [vp, i32, i32, vp, vp, vp]),
     }
     for name, (res, args) in sigs.items():
         fn = getattr(L, name)
@@ -278,3 +280,20 @@ def quantize_gf4_gpu(w: torch.Tensor, keep: torch.Tensor | None = None):
     check(lib().fb_quantize_gf4_gpu(_ptr(w), _ptr(kp) if kp is not None else None, N, K,
                                     _ptr(codes), _ptr(book), _stream(w.device)))
     return codes, book
+
+
+def quantize_e2m1_gpu(w: torch.Tensor):
+    """E2M1 packing on the GPU (fb_quantize_e2m1_gpu): fp32 device ``w [N,K]`` -> device
+    ``(codes uint8 [N,K/2], scales uint8 [N,K/32])``, bit-identical to
+    :func:`quantize_e2m1`.  Raises on non-finite weights."""
+    if not w.is_cuda:
+        raise RuntimeError("fb_quantize_e2m1_gpu needs a device tensor (ROCm GPU)")
+    w = w.detach().to(torch.float32).contiguous()
+    N, K = w.shape
+    if not bool(torch.isfinite(w).all()):
+        raise RuntimeError(strerror(-10))
+    codes = torch.empty(N, K // 2, dtype=torch.uint8, device=w.device)
+    scales = torch.empty(N, max(K // 32, 1), dtype=torch.uint8, device=w.device)
+    check(lib().fb_quantize_e2m1_gpu(_ptr(w), N, K, _ptr(codes), _ptr(scales),
+                                     _stream(w.device)))
+    return codes, scales

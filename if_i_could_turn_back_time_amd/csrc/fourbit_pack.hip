@@ -1,5 +1,6 @@
-// GF4 packer on the GPU: the Jenks-16 (and masked Jenks) quantizer of fourbit_host.cpp,
-// one wavefront per (row, 128-group), fp64, producing the same bytes as the host packer.
+// Packers on the GPU, producing the same bytes as the host packers of fourbit_host.cpp:
+// GF4 (the Jenks-16 and masked Jenks quantizer, one wavefront per (row, 128-group), fp64)
+// and E2M1 (32 lanes per 32-group).
 //
 // Every fp64 expression is the host's, evaluated in the host's order, and this file is
 // compiled with -ffp-contract=off (no fused multiply-adds), so each operation rounds
@@ -237,6 +238,52 @@ __global__ __launch_bounds__(64) void gf4_pack_kernel(const float* __restrict__ 
   }
 }
 
+// E2M1 + E8M0 per 32-group, 32 lanes per group (a wave packs two groups): the host
+// packer's rule (fb_quantize_e2m1) in fp32, which is exact here: amax's exponent comes from
+// frexp, q = v * 2^-e is a power-of-two scaling, and the rounding midpoints are fp32 values.
+__device__ __forceinline__ int e2m1_index(float a) {
+  const float mids[7] = {0.25f, 0.75f, 1.25f, 1.75f, 2.5f, 3.5f, 5.0f};
+  int idx = 0;
+  bool tie = false;
+#pragma unroll
+  for (int t = 0; t < 7; ++t) {
+    idx += a > mids[t] ? 1 : 0;
+    tie = tie || a == mids[t];
+  }
+  if (tie && (idx & 1)) ++idx;
+  return idx < 7 ? idx : 7;
+}
+
+__global__ __launch_bounds__(256) void e2m1_pack_kernel(const float* __restrict__ w,
+                                                        int64_t groups,
+                                                        uint8_t* __restrict__ codes,
+                                                        uint8_t* __restrict__ scales) {
+  const int lane = threadIdx.x & 63;
+  const int t = lane & 31;                        // value index in the group
+  const int64_t wave = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6;
+  const int64_t nwaves = ((int64_t)gridDim.x * blockDim.x) >> 6;
+  for (int64_t it0 = wave * 2; it0 < groups; it0 += nwaves * 2) {  // uniform per wave
+    const int64_t it = it0 + (lane >> 5);
+    const bool live = it < groups;
+    const float v = live ? w[it * 32 + t] : 0.0f;
+    float amax = __builtin_fabsf(v);
+#pragma unroll
+    for (int m = 16; m >= 1; m >>= 1) amax = fmaxf(amax, __shfl_xor(amax, m, 32));
+    int ex = 0;
+    if (amax > 0.0f) {
+      int e2;
+      (void)frexpf(amax, &e2);  // amax = m * 2^e2, m in [0.5, 1)
+      ex = e2 - 1 - 2;
+      ex = ex < -127 ? -127 : (ex > 127 ? 127 : ex);
+    }
+    const float q = ldexpf(v, -ex);
+    const int code = (__builtin_signbit(v) ? 8 : 0) | e2m1_index(__builtin_fabsf(q));
+    const int hi = __shfl_xor(code, 1, 32);
+    if (live && !(t & 1)) codes[it * 16 + (t >> 1)] = (uint8_t)(code | (hi << 4));
+    if (live && t == 0) scales[it] = (uint8_t)(ex + 127);
+  }
+}
+
 }  // namespace
 
 extern "C" {
@@ -253,3 +300,15 @@ int fb_quantize_gf4_gpu(const float* w, const uint8_t* keep, int32_t N, int32_t 
 }
 
 }  // extern "C"
+
+extern "C" int fb_quantize_e2m1_gpu(const float* w, int32_t N, int32_t K, uint8_t* codes,
+                                    uint8_t* scales, void* stream) {
+  if (!w || !codes || !scales) return FB_ERR_NULL;
+  if (N < 1 || K < 128 || K % 128) return FB_ERR_SHAPE;
+  const int64_t groups = (int64_t)N * (K / 32);
+  const int64_t blocks = (groups + 7) / 8;  // 8 groups per 256-thread block
+  const int grid = (int)(blocks < (1 << 20) ? blocks : (1 << 20));
+  hipLaunchKernelGGL(e2m1_pack_kernel, dim3(grid), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), w, groups, codes, scales);
+  return hipGetLastError() == hipSuccess ? FB_OK : FB_ERR_HIP;
+}

@@ -103,9 +103,8 @@ class PackedWeight:
                  nthreads: int | None = None, keep: torch.Tensor | None = None,
                  packer: str = "host") -> "PackedWeight":
         """Packs fp32 ``w [N,K]``.  ``keep`` (GF4 only, no rotation): entries where it is
-        0 decode to exactly 0.  ``packer='gpu'`` runs the GF4 Jenks search on the GPU
-        (``device``, or cuda:0), with the same bytes as the host packer; E2M1 packing is
-        a single pass and always runs on the host."""
+        0 decode to exactly 0.  ``packer='gpu'`` packs on the GPU (``device``, or cuda:0)
+        with the same bytes as the host packer."""
         w = w.detach().float().cpu().contiguous()
         N, K = w.shape
         if keep is not None and (fmt != "gf4" or fwht_block):
@@ -120,6 +119,10 @@ class PackedWeight:
             codes, meta = codes.cpu(), meta.cpu()
         elif fmt == "gf4":
             codes, meta = C.quantize_gf4(w, nthreads, keep)
+        elif fmt == "e2m1" and packer == "gpu":
+            dev = device if device is not None and torch.device(device).type == "cuda" else "cuda:0"
+            codes, meta = C.quantize_e2m1_gpu(w.to(dev))
+            codes, meta = codes.cpu(), meta.cpu()
         elif fmt == "e2m1":
             codes, meta = C.quantize_e2m1(w, nthreads)
         else:

@@ -161,6 +161,12 @@ int fb_gemv(const void* wdev, const void* x, void* y, const fb_shape_t* s, void*
 int fb_quantize_gf4_gpu(const float* w, const uint8_t* keep, int32_t N, int32_t K,
                         uint8_t* codes, uint16_t* codebook, void* stream);
 
+/* E2M1 packer on the GPU: the same rule and bytes as fb_quantize_e2m1, 32 lanes per
+ * 32-group.  w fp32 [N,K], codes uint8 [N,K/2] and scales uint8 [N,K/32] are device
+ * pointers; asynchronous on the stream; non-finite weights are not detected here. */
+int fb_quantize_e2m1_gpu(const float* w, int32_t N, int32_t K, uint8_t* codes, uint8_t* scales,
+                         void* stream);
+
 /* Device decode of the whole weight: w_out [N,K] of out_dtype (F32 always exact; F16
  * exact for GF4; BF16 exact for E2M1 within the bf16 normal range).  The same decode
  * code as fb_gemv; used for bit-exact parity.  Replaces the dequantizer expression

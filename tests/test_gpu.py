@@ -393,3 +393,55 @@ def test_gemv_in_hip_graph_replays_match_eager():
             torch.cuda.synchronize()
             assert torch.equal(y, eager), f"{fmt} fb={fb} replay {rep}"
             assert x2.shape == x.shape
+
+
+def test_concurrent_streams_match_serial():
+    """Calls on two streams at once (two layers, interleaved launches) give the same bits as
+    the same calls one after the other: the library keeps no state between calls."""
+    say("two streams")
+    g = torch.Generator().manual_seed(81)
+    layers = []
+    for fmt, N, K in (("gf4", 8192, 4096), ("e2m1", 6000, 8192)):
+        pw = PackedWeight.quantize(torch.randn(N, K, generator=g) * 0.02, fmt, device=DEV,
+                                   packer="gpu" if fmt == "gf4" else "host")
+        xdt = torch.float16 if fmt == "gf4" else torch.bfloat16
+        xs = [torch.randn(2, K, generator=g).to(xdt).to(DEV) for _ in range(6)]
+        layers.append((pw, xs))
+    serial = [[pw.gemv(x, out_dtype=torch.float32) for x in xs] for pw, xs in layers]
+    torch.cuda.synchronize()
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+    outs = [[None] * 6 for _ in layers]
+    for i in range(6):
+        for j, ((pw, xs), s) in enumerate(zip(layers, streams)):
+            s.wait_stream(torch.cuda.current_stream())
+            with torch.cuda.stream(s):
+                outs[j][i] = pw.gemv(xs[i], out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    for j in range(2):
+        for i in range(6):
+            assert torch.equal(outs[j][i], serial[j][i]), (j, i)
+
+
+def test_gpu_e2m1_packer_bit_exact_vs_host():
+    """fb_quantize_e2m1_gpu produces the host packer's bytes: random rows, exact rounding
+    midpoints (ties to the even index), saturation, signed zeros, all-zero groups, fp32
+    subnormals and large magnitudes."""
+    say("gpu e2m1 packer")
+    g = torch.Generator().manual_seed(91)
+    N, K = 40, 1024
+    w = torch.randn(N, K, generator=g) * 0.02
+    grid = torch.tensor([0.0, 0.5, 1.0, 1.5, 2.0, 3.0, 4.0, 6.0])
+    mids = torch.tensor([0.25, 0.75, 1.25, 1.75, 2.5, 3.5, 5.0])
+    w[0, :32] = torch.cat([grid, -grid, mids, -mids, torch.tensor([6.0, 5.99, 7.0, 12.0,
+                                                                    -0.0, 0.0, 0.1, -0.3, 4.5,
+                                                                    5.5])])[:32]
+    w[1, :32] = 0.0
+    w[2, :32] = -0.0
+    w[3] = torch.randn(K, generator=g) * 1e-40            # subnormal fp32
+    w[4] = torch.randn(K, generator=g) * 1e30
+    w[5, :32] = mids.repeat(5)[:32] * 2.0 ** -20          # midpoints at another scale
+    hc, hs = C.quantize_e2m1(w)
+    dc, ds = C.quantize_e2m1_gpu(w.to(DEV))
+    torch.cuda.synchronize()
+    assert torch.equal(dc.cpu(), hc)
+    assert torch.equal(ds.cpu(), hs)
