@@ -33,7 +33,7 @@ typedef __bf16 bf168_t __attribute__((ext_vector_type(8)));
 typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
-constexpr int kWaves = 16;
+constexpr int kWaves = 16;  // waves of a full-CU workgroup (the rotated path always uses it)
 constexpr int kThreads = kWaves * 64;
 constexpr int kLdsLimit = 160 * 1024;
 constexpr int kSliceBytes = 272;  // 128 x 16-bit values + 16-byte pad (bank spread)
@@ -212,14 +212,14 @@ __device__ __forceinline__ u32x4 x_load8(const uint16_t* __restrict__ x, int K, 
 }
 
 // Chunk t of a slice is batch row t / per_row, values k0 + 8 * (t % per_row) ...; thread
-// j * kThreads + threadIdx.x of the workgroup takes chunk t in step j.
+// j * NT + threadIdx.x of an NT-thread workgroup takes chunk t in step j.
 // row_of(t) = t / per_row.
-template <typename RowOf>
+template <int NT, typename RowOf>
 __device__ __forceinline__ void x_preload(XPre& xp, const uint16_t* __restrict__ x, int K, int k0,
                                           int per_row, int nchunks, RowOf row_of, int tid) {
 #pragma unroll
   for (int j = 0; j < kXPre; ++j) {
-    const int t = tid + j * kThreads;
+    const int t = tid + j * NT;
     if (t < nchunks) {
       const int b = row_of(t);
       xp.v[j] = x_load8(x, K, b, k0 + (t - b * per_row) * 8);
@@ -228,7 +228,7 @@ __device__ __forceinline__ void x_preload(XPre& xp, const uint16_t* __restrict__
 }
 
 // Plain staging: chunk t lands in its 128-value group of the slice layout.
-template <typename RowOf>
+template <int NT, typename RowOf>
 __device__ void stage_plain(uint8_t* lds, const XPre& xp, const uint16_t* __restrict__ x, int K,
                             int B, int k0, int nsl, int RS, RowOf row_of, int tid) {
   const int per_row = nsl * 16;
@@ -240,10 +240,10 @@ __device__ void stage_plain(uint8_t* lds, const XPre& xp, const uint16_t* __rest
   };
 #pragma unroll
   for (int j = 0; j < kXPre; ++j) {
-    const int t = tid + j * kThreads;
+    const int t = tid + j * NT;
     if (t < n) put(t, xp.v[j]);
   }
-  for (int t = tid + kXPre * kThreads; t < n; t += kThreads) {
+  for (int t = tid + kXPre * NT; t < n; t += NT) {
     const int b = row_of(t);
     put(t, x_load8(x, K, b, k0 + (t - b * per_row) * 8));
   }
@@ -473,8 +473,11 @@ __device__ __forceinline__ f32x4 unit_partial(const Rec<FMT>& r, const uint8_t* 
 // rotation; kRotated = rotation of x.  Each is compiled with only the staging it needs, which
 // keeps the kernel short and its registers few.
 enum { kFlat = 0, kSliced = 1, kRotated = 2 };
-template <int FMT, int XDT, int MODE>
-__global__ __launch_bounds__(kThreads) void gemv_kernel(
+// NW: waves per workgroup.  16 (one workgroup per CU) in general; 8 (two per CU) for
+// layers with few row tiles per CU, where twice the workgroups, each with half the waves,
+// finish sooner.
+template <int FMT, int XDT, int MODE, int NW>
+__global__ __launch_bounds__(NW * 64) void gemv_kernel(
     const uint8_t* __restrict__ w, const void* __restrict__ x, int K, int B, int SPL, int GS,
     int tq, int tr, unsigned spl_m, int S, int fwht_block, int RS, void* __restrict__ y, int N,
     int ydt) {
@@ -482,6 +485,8 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(
   const int xbytes = x_lds_bytes(B, K, SPL, fwht_block);  // staged x; the slots follow
   const float fwht_scale = MODE == kRotated ? 1.0f / __builtin_sqrtf((float)fwht_block) : 1.0f;
   constexpr int BB = FMT == FB_FMT_GF4 ? fb::kGf4BlockBytes : fb::kE2m1BlockBytes;
+  constexpr int NT = NW * 64;
+  static_assert(MODE != kRotated || NW == kWaves, "the rotation staging assumes 16 waves");
   const int g = blockIdx.x;
   const int t0 = g * tq + min(g, tr);
   const int t1 = t0 + tq + (g < tr ? 1 : 0);
@@ -545,7 +550,7 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(
     load_rec<FMT>(rs, real ? unit_off(s, u) : 0u, lane, r);
   };
   const uint16_t* xg = static_cast<const uint16_t*>(x);
-  // Each wave's first two units are static (wave, wave + kWaves); the counter hands out
+  // Each wave's first two units are static (wave, wave + NW); the counter hands out
   // the rest.
   constexpr bool rot = MODE == kRotated;
   const int nslices = MODE == kFlat ? 1 : S;
@@ -565,8 +570,8 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(
     if constexpr (rot)
       rot_preload(xr, xg, K, B, k0, kw, tid);
     else
-      x_preload(xp, xg, K, k0, per_row, B * per_row, row_of, tid);
-    int u0 = wave, u1 = wave + kWaves;
+      x_preload<NT>(xp, xg, K, k0, per_row, B * per_row, row_of, tid);
+    int u0 = wave, u1 = wave + NW;
     // the rotation cannot start before its x has arrived, and x loads queued behind the
     // first weight unit arrive later: wait for x first
     if constexpr (rot) __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
@@ -575,17 +580,17 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(
     // barrier that closes the previous slice, so their latency overlaps the slowest wave.
     if (s > 0) {  // every wave is done with the previous slice: x may be restaged
       __syncthreads();
-      if (threadIdx.x == 0) *counter = 2 * kWaves;
+      if (threadIdx.x == 0) *counter = 2 * NW;
     }
     if (s == 0) {
-      if (threadIdx.x == 0) *counter = 2 * kWaves;
+      if (threadIdx.x == 0) *counter = 2 * NW;
       if (threadIdx.x < 16) reinterpret_cast<u32x4*>(zeros)[threadIdx.x] = u32x4{0u, 0u, 0u, 0u};
     }
     if constexpr (rot)
       stage_fwht(xst, reinterpret_cast<float*>(xst + B * RS), xr, xg, K, B, k0, kw, nsl, RS,
                  fwht_block, fwht_scale, tid);
     else
-      stage_plain(xst, xp, xg, K, B, k0, nsl, RS, row_of, tid);
+      stage_plain<NT>(xst, xp, xg, K, B, k0, nsl, RS, row_of, tid);
     __syncthreads();  // x staged, counter set
     issue(s, u1, ring[1]);
     __builtin_amdgcn_sched_barrier(0);  // keep the prefetch ahead of the compute
@@ -610,7 +615,7 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(
 
   // y[col][row] = sum over the spans of the tile, in span order
   const int nt = t1 - t0;
-  for (int e = threadIdx.x; e < nt * 256; e += kThreads) {
+  for (int e = threadIdx.x; e < nt * 256; e += NT) {
     const int c = e & 15;
     if (c >= B) continue;
     const int r = (e >> 4) & 15;
@@ -704,6 +709,7 @@ struct Plan {
   int GS = 0;    // spans per row
   int tq = 0;    // row tiles per workgroup (the first tr workgroups take one more)
   int tr = 0;
+  int nw = 0;    // waves per workgroup: 16 (one workgroup per CU) or 8 (two per CU)
   size_t lds = 0;
 };
 
@@ -717,26 +723,37 @@ size_t plan_lds(const fb_shape_t* s, int tpw, int SPL) {
          16 + 256;
 }
 
-// One workgroup per CU (up to the number of row tiles); the fewest K-slices whose LDS fits.
+// The fewest K-slices whose LDS fits.  One 16-wave workgroup per CU (up to the number of
+// row tiles), or, for unrotated batch-1 layers with few row tiles per CU (GF4 at most 3,
+// E2M1 at most 2) and LDS that fits twice in a CU, two 8-wave workgroups per CU (measured
+// 0.3-1.4 us faster there; no faster on large layers, slower at batch 2 and 4).
 bool make_plan(const fb_shape_t* s, int cus, Plan& pl) {
   const int GS = (s->K / 128 + 3) / 4;
   const int T = (s->N + 15) / 16;
-  const int grid = std::max(1, std::min(T, cus));
-  const int tpw = (T + grid - 1) / grid;  // most tiles a workgroup owns
-  for (int S = 1; S <= GS; ++S) {
-    if (GS % S) continue;
-    const int SPL = GS / S;
-    if (s->fwht_block && S > 1 && (SPL * 512) % s->fwht_block) continue;
-    const size_t lds = plan_lds(s, tpw, SPL);
-    if (lds > (size_t)kLdsLimit) continue;
-    pl.S = S;
-    pl.SPL = SPL;
-    pl.grid = grid;
-    pl.GS = GS;
-    pl.tq = T / grid;
-    pl.tr = T % grid;
-    pl.lds = lds;
-    return true;
+  const int half_tiles = (s->fmt == FB_FMT_GF4 ? 3 : 2) * cus;
+  const bool half = !s->fwht_block && s->B == 1 && T <= half_tiles;
+  for (int pass = half ? 0 : 1; pass < 2; ++pass) {
+    const int nw = pass == 0 ? kWaves / 2 : kWaves;
+    const size_t limit = pass == 0 ? (size_t)kLdsLimit / 2 : (size_t)kLdsLimit;
+    const int grid = std::max(1, std::min(T, pass == 0 ? 2 * cus : cus));
+    const int tpw = (T + grid - 1) / grid;  // most tiles a workgroup owns
+    for (int S = 1; S <= GS; ++S) {
+      if (GS % S) continue;
+      if (pass == 0 && S > 1) break;  // two workgroups per CU only with one K-slice
+      const int SPL = GS / S;
+      if (s->fwht_block && S > 1 && (SPL * 512) % s->fwht_block) continue;
+      const size_t lds = plan_lds(s, tpw, SPL);
+      if (lds > limit) continue;
+      pl.S = S;
+      pl.SPL = SPL;
+      pl.grid = grid;
+      pl.GS = GS;
+      pl.tq = T / grid;
+      pl.tr = T % grid;
+      pl.nw = nw;
+      pl.lds = lds;
+      return true;
+    }
   }
   return false;
 }
@@ -747,10 +764,10 @@ int device_cus() {
   return cu_count(dev);
 }
 
-template <int FMT, int XDT, int MODE>
+template <int FMT, int XDT, int MODE, int NW>
 int launch_gemv(const void* wdev, const void* x, void* y, const fb_shape_t* s, const Plan& pl,
                 hipStream_t stream) {
-  auto kern = gemv_kernel<FMT, XDT, MODE>;
+  auto kern = gemv_kernel<FMT, XDT, MODE, NW>;
   static std::atomic<bool> attr_set{false};
   if (!attr_set.load(std::memory_order_acquire)) {
     if (hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
@@ -758,7 +775,7 @@ int launch_gemv(const void* wdev, const void* x, void* y, const fb_shape_t* s, c
       return FB_ERR_HIP;
     attr_set.store(true, std::memory_order_release);
   }
-  hipLaunchKernelGGL(kern, dim3(pl.grid), dim3(kThreads), pl.lds, stream,
+  hipLaunchKernelGGL(kern, dim3(pl.grid), dim3(NW * 64), pl.lds, stream,
                      static_cast<const uint8_t*>(wdev), x, s->K, s->B, pl.SPL, pl.GS, pl.tq,
                      pl.tr, div_magic(pl.SPL), pl.S, s->fwht_block, x_row_stride(pl.SPL * 4), y,
                      s->N, s->y_dtype);
@@ -768,9 +785,13 @@ int launch_gemv(const void* wdev, const void* x, void* y, const fb_shape_t* s, c
 template <int FMT, int XDT>
 int launch_mode(int mode, const void* wdev, const void* x, void* y, const fb_shape_t* s,
                 const Plan& pl, hipStream_t stream) {
-  if (mode == kFlat) return launch_gemv<FMT, XDT, kFlat>(wdev, x, y, s, pl, stream);
-  if (mode == kSliced) return launch_gemv<FMT, XDT, kSliced>(wdev, x, y, s, pl, stream);
-  return launch_gemv<FMT, XDT, kRotated>(wdev, x, y, s, pl, stream);
+  if (mode == kFlat) {
+    if (pl.nw == kWaves / 2)
+      return launch_gemv<FMT, XDT, kFlat, kWaves / 2>(wdev, x, y, s, pl, stream);
+    return launch_gemv<FMT, XDT, kFlat, kWaves>(wdev, x, y, s, pl, stream);
+  }
+  if (mode == kSliced) return launch_gemv<FMT, XDT, kSliced, kWaves>(wdev, x, y, s, pl, stream);
+  return launch_gemv<FMT, XDT, kRotated, kWaves>(wdev, x, y, s, pl, stream);
 }
 
 }  // namespace
