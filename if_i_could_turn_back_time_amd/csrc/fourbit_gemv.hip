@@ -9,7 +9,8 @@
 // LDS).  The VALU only decodes; the cross-lane reduction is the MFMA itself; batch 1..16
 // costs the same VALU work.
 //
-// Partition: workgroup g (16 waves, one per CU) owns the contiguous 16-row tiles [t0, t1).
+// Partition: workgroup g (16 waves, one per CU; for small batch-1 layers 8 waves, two per
+// CU) owns the contiguous 16-row tiles [t0, t1).
 // Its (tile, span) units are handed to its waves through an LDS counter: the SIMDs issue
 // the oldest wave first, so with a fixed split the youngest wave of each SIMD would finish
 // long after the others; taking units on demand keeps all waves busy to the end.  Each
@@ -87,7 +88,6 @@ __device__ __forceinline__ u32x4 gf4_decode8(unsigned q, const u32x4& tl, const 
   return w;
 }
 
-
 // Two independent 8-code decodes written stage by stage, so the scheduler sees twice the
 // instruction-level parallelism of one decode chain.
 __device__ __forceinline__ void gf4_decode16(unsigned q0, unsigned q1, const u32x4& tl,
@@ -112,6 +112,7 @@ __device__ __forceinline__ void gf4_decode16(unsigned q0, unsigned q1, const u32
   w0.z = perm(hiB0, loB0, 0x05010400u); w1.z = perm(hiB1, loB1, 0x05010400u);
   w0.w = perm(hiB0, loB0, 0x07030602u); w1.w = perm(hiB1, loB1, 0x07030602u);
 }
+
 // E2M1 decode of one 32-bit word (8 codes, canonical order) times `scale`.
 template <int XDT>
 __device__ __forceinline__ u32x4 e2m1_decode8(unsigned q, float scale) {
