@@ -57,6 +57,9 @@ def packed_linear(wdev: torch.Tensor, N: int, K: int, fmt: str, fwht_block: int,
     x may have any leading shape and dtype: it is cast to fp16 (GF4, or any rotation) or
     kept in fp16/bf16 (E2M1; fp32 becomes bf16) and zero-padded to ``packed_k(K)``; y
     has x's dtype (fp32 for other dtypes).  No CPU path: x must be on the GPU."""
+    if x.dim() == 0 or x.shape[-1] != K:
+        raise RuntimeError(f"packed linear: input of shape {tuple(x.shape)} does not end in "
+                           f"in_features={K}")
     if not x.is_cuda:
         raise RuntimeError("the packed 4-bit linear runs the HIP kernel: move the module and "
                            "input to a ROCm GPU")
@@ -77,7 +80,7 @@ def packed_linear(wdev: torch.Tensor, N: int, K: int, fmt: str, fwht_block: int,
         b1 = min(b0 + MAX_GEMV_BATCH, x2.shape[0])
         shape = C.make_shape(N, kp, b1 - b0, f, fwht_block, C.DTYPE_CODE[xk.dtype],
                              C.DTYPE_CODE[ydt])
-        C.gemv(wdev, xk[b0:b1], y[b0:b1], shape)
+        C.gemv(wdev, xk[b0:b1], y[b0:b1], shape, C.new_workspace(shape, x.device))
     if bias is not None:
         y = y + bias.to(ydt)
     return y.reshape(*lead, N)

@@ -208,6 +208,29 @@ def oracle_weight(q: QuantLinear) -> torch.Tensor:
     return O.dequant_f32(q.fmt, codes, meta)[:, :q.in_features]
 
 
+def test_quantlinear_batch_edges_gpu():
+    """Batch edges of the forward: an empty batch gives an empty output (no launch), 33
+    rows run as chunks of 16 + 16 + 1, and a 3-D input keeps its leading shape; every
+    row is checked against the oracle's decode + fp32 F.linear."""
+    say("batch edges")
+    g = torch.Generator().manual_seed(33)
+    lin = torch.nn.Linear(512, 80)
+    for fmt, xdt in (("gf4", torch.float16), ("e2m1", torch.bfloat16)):
+        q = QuantLinear(lin, fmt=fmt).to(DEV)
+        W = oracle_weight(q).float()
+        y0 = q(torch.empty(0, 512, device=DEV, dtype=xdt))
+        assert y0.shape == (0, 80) and y0.dtype == xdt
+        for shape in ((33, 512), (1, 1, 512), (2, 17, 512)):
+            x = torch.randn(*shape, generator=g).to(xdt)
+            y = q(x.to(DEV))
+            torch.cuda.synchronize()
+            assert y.shape == (*shape[:-1], 80)
+            yref = torch.nn.functional.linear(x.reshape(-1, 512).float(), W, lin.bias.detach())
+            extra = {torch.float16: 2.0 ** -11, torch.bfloat16: 2.0 ** -8}[xdt]
+            ok, emax, _ = within_tol(y.reshape(-1, 80), yref, extra)
+            assert ok, f"{fmt} {shape}: max abs err {emax}"
+
+
 def test_ragged_k_masked_forward_gpu():
     """in_features = 300 (x zero-padded to 384 for the kernel), 70% of weights masked."""
     say("ragged K / masked")

@@ -182,6 +182,11 @@ def test_quantlinear_api_on_cpu():
     assert q.codes.shape == (48, 128) and q.meta.shape == (48, 2, 16)
     with pytest.raises(RuntimeError, match="GPU"):
         q(torch.randn(2, 256))
+    # like F.linear, an input whose last dimension is not in_features is refused (here
+    # before the device check): [2, 512] would otherwise reshape to 4 rows of 256
+    for bad in (torch.randn(2, 512), torch.randn(256, 2), torch.tensor(1.0)):
+        with pytest.raises(RuntimeError, match="in_features=256"):
+            q(bad)
     with pytest.raises(ValueError):
         QuantLinear(lin, bitwidth=8)
     # commit(): weight becomes the exact decode of the packed codes
