@@ -34,8 +34,7 @@ typedef __bf16 bf168_t __attribute__((ext_vector_type(8)));
 typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
-constexpr int kWaves = 16;  // waves of a full-CU workgroup (the rotated path always uses it)
-constexpr int kThreads = kWaves * 64;
+constexpr int kWaves = 16;  // waves of a full-CU workgroup
 constexpr int kLdsLimit = 160 * 1024;
 constexpr int kSliceBytes = 272;  // 128 x 16-bit values + 16-byte pad (bank spread)
 
@@ -253,13 +252,14 @@ __device__ void stage_plain(uint8_t* lds, const XPre& xp, const uint16_t* __rest
 // Blockwise normalised FWHT (fp32 butterflies) of x[b, k0 : k0+kw] into the staged
 // layout (rounded to fp16); kw is a whole number of blocks of fb.
 //  - Stages 0..7 run in registers.  The B*kw values are cut into 256-value sub-blocks,
-//    taken by the waves in turn (sub-block i by wave i % kWaves); lane l holds values
+//    taken by the NW waves in turn (sub-block i by wave i % NW); lane l holds values
 //    4l..4l+3: stages 0-1 are in-lane, stages 2-7 pair lanes l and l ^ 2^(s-2) (lane_xor).
 //    The x of a wave's first kXPre sub-blocks is loaded by rot_preload before the slice's
 //    weight loads are issued.
 //  - Blocks larger than 256 go through LDS (F: B*kw floats) once: each 4096-value piece is
-//    read back with value e = (16w + l % 16) + 256 (r + 4 (l / 16)) in wave w, lane l,
-//    register r, so stages 8-9 are in-lane and stages 10-11 pair lanes l and l ^ 16, 32.
+//    read back in 16 column groups, taken by the waves in turn; group c holds value
+//    e = (16c + l % 16) + 256 (r + 4 (l / 16)) in lane l, register r, so stages 8-9 are
+//    in-lane and stages 10-11 pair lanes l and l ^ 16, 32.
 // Staged positions k >= kw (up to the slice width) are zero.
 struct XRot {
   uint2 v[kXPre];
@@ -268,6 +268,7 @@ struct XRot {
 // The loads are unconditional (lanes past kw, and waves past the last sub-block, read
 // values that stage_fwht does not use), so the four are issued back to back and nothing
 // waits for them before stage_fwht.
+template <int NW>
 __device__ __forceinline__ void rot_preload(XRot& xr, const uint16_t* __restrict__ x, int K,
                                             int B, int k0, int kw, int tid) {
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
@@ -276,7 +277,7 @@ __device__ __forceinline__ void rot_preload(XRot& xr, const uint16_t* __restrict
   for (int i = 0; i < kXPre; ++i) {
     // flat sub-block index over (row, sub-block), uniform; past the last one the wave
     // re-reads its first (the values are not used) so that no load is conditional
-    const int sb = wave + i * kWaves < B * nsb ? wave + i * kWaves : min(wave, B * nsb - 1);
+    const int sb = wave + i * NW < B * nsb ? wave + i * NW : min(wave, B * nsb - 1);
     const int b = sb / nsb;
     const int k = (sb - b * nsb) * 256 + lane * 4;
     xr.v[i] = *reinterpret_cast<const uint2*>(x + (int64_t)b * K + k0 + (k < kw ? k : 0));
@@ -313,6 +314,7 @@ __device__ __forceinline__ float lane_xor(float v, int m, int lane) {
 // so the four 1024-apart lane groups of a phase-2 read fall in different banks.
 __host__ __device__ __forceinline__ int fpad(int p) { return p + (p >> 10) * 16; }
 
+template <int NW>
 __device__ void stage_fwht(uint8_t* lds, float* F, const XRot& xr, const uint16_t* __restrict__ x,
                            int K, int B, int k0, int kw, int nsl, int RS, int fb, float sc,
                            int tid) {
@@ -329,7 +331,7 @@ __device__ void stage_fwht(uint8_t* lds, float* F, const XRot& xr, const uint16_
     hi = a - c;
   };
   int i = 0;
-  for (int sb = wave; sb < B * nsb; sb += kWaves, ++i) {
+  for (int sb = wave; sb < B * nsb; sb += NW, ++i) {
     const int b = sb / nsb;
     const int k = (sb - b * nsb) * 256 + lane * 4;
     const bool live = k < kw;  // kw is a multiple of 128: whole lanes are in or out
@@ -377,12 +379,14 @@ __device__ void stage_fwht(uint8_t* lds, float* F, const XRot& xr, const uint16_
     __syncthreads();
     const int total = B * kw;
     const float inv_kw = 1.0f / (float)kw;
-    for (int base = 0; base < total; base += 4096) {
+    const int npieces = ((total + 4095) >> 12) << 4;  // (4096-value piece, column group)
+    for (int piece = wave; piece < npieces; piece += NW) {
+      const int base = (piece >> 4) * 4096 + (piece & 15) * 16;
       float v[4];
       int e[4];
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        e[r] = base + (wave * 16 + (lane & 15)) + 256 * (r + 4 * (lane >> 4));
+        e[r] = base + (lane & 15) + 256 * (r + 4 * (lane >> 4));
         v[r] = e[r] < total ? F[fpad(e[r])] : 0.0f;
       }
       if (lg_fb > 8) {
@@ -419,7 +423,7 @@ __device__ void stage_fwht(uint8_t* lds, float* F, const XRot& xr, const uint16_
   }
   // zeros past the rotated width (the weight stream is zero there too)
   const int width = nsl * 128;
-  for (int t = tid; t < B * ((width - kw) >> 3); t += kThreads) {
+  for (int t = tid; t < B * ((width - kw) >> 3); t += NW * 64) {
     const int b = t / ((width - kw) >> 3);
     const int k = kw + (t - b * ((width - kw) >> 3)) * 8;
     *reinterpret_cast<u32x4*>(lds + b * RS + (k >> 7) * kSliceBytes + (k & 127) * 2) =
@@ -487,7 +491,6 @@ __global__ __launch_bounds__(NW * 64) void gemv_kernel(
   const float fwht_scale = MODE == kRotated ? 1.0f / __builtin_sqrtf((float)fwht_block) : 1.0f;
   constexpr int BB = FMT == FB_FMT_GF4 ? fb::kGf4BlockBytes : fb::kE2m1BlockBytes;
   constexpr int NT = NW * 64;
-  static_assert(MODE != kRotated || NW == kWaves, "the rotation staging assumes 16 waves");
   const int g = blockIdx.x;
   const int t0 = g * tq + min(g, tr);
   const int t1 = t0 + tq + (g < tr ? 1 : 0);
@@ -569,7 +572,7 @@ __global__ __launch_bounds__(NW * 64) void gemv_kernel(
     XPre xp;
     XRot xr;
     if constexpr (rot)
-      rot_preload(xr, xg, K, B, k0, kw, tid);
+      rot_preload<NW>(xr, xg, K, B, k0, kw, tid);
     else
       x_preload<NT>(xp, xg, K, k0, per_row, B * per_row, row_of, tid);
     int u0 = wave, u1 = wave + NW;
@@ -588,7 +591,7 @@ __global__ __launch_bounds__(NW * 64) void gemv_kernel(
       if (threadIdx.x < 16) reinterpret_cast<u32x4*>(zeros)[threadIdx.x] = u32x4{0u, 0u, 0u, 0u};
     }
     if constexpr (rot)
-      stage_fwht(xst, reinterpret_cast<float*>(xst + B * RS), xr, xg, K, B, k0, kw, nsl, RS,
+      stage_fwht<NW>(xst, reinterpret_cast<float*>(xst + B * RS), xr, xg, K, B, k0, kw, nsl, RS,
                  fwht_block, fwht_scale, tid);
     else
       stage_plain<NT>(xst, xp, xg, K, B, k0, nsl, RS, row_of, tid);
@@ -727,7 +730,8 @@ size_t plan_lds(const fb_shape_t* s, int tpw, int SPL) {
 // The fewest K-slices whose LDS fits.  One 16-wave workgroup per CU (up to the number of
 // row tiles), or, for unrotated batch-1 layers with few row tiles per CU (GF4 at most 3,
 // E2M1 at most 2) and LDS that fits twice in a CU, two 8-wave workgroups per CU (measured
-// 0.3-1.4 us faster there; no faster on large layers, slower at batch 2 and 4).
+// 0.3-1.4 us faster there; no faster on large layers, slower at batch 2 and 4, and slower
+// with a rotation, which each workgroup would then compute with half the waves).
 bool make_plan(const fb_shape_t* s, int cus, Plan& pl) {
   const int GS = (s->K / 128 + 3) / 4;
   const int T = (s->N + 15) / 16;

@@ -236,7 +236,8 @@ const char* fb_strerror(int code) {
     case FB_ERR_GROUP: return "fourbit: group size must be 128 for GF4 and 32 for E2M1";
     case FB_ERR_FORMAT: return "fourbit: unknown format";
     case FB_ERR_DTYPE: return "fourbit: unsupported dtype (GF4 needs fp16 x; E2M1 fp16/bf16 x; y fp16/bf16/fp32)";
-    case FB_ERR_FWHT: return "fourbit: fwht_block must be 0 or a power of two >= 2 dividing K";
+    case FB_ERR_FWHT:
+      return "fourbit: fwht_block must be 0 or a power of two in [2, 4096] dividing K";
     case FB_ERR_ALIGN: return "fourbit: device pointers must be 16-byte aligned";
     case FB_ERR_WORKSPACE: return "fourbit: workspace smaller than fb_workspace_bytes()";
     case FB_ERR_BATCH: return "fourbit: batch size not supported by this entry point";
@@ -257,8 +258,9 @@ int fb_validate(const fb_shape_t* s) {
   if ((int64_t)s->N * (s->K / 128) > INT32_MAX) return FB_ERR_SHAPE;  // < 2^31 groups
   if (s->fmt == FB_FMT_GF4 && s->group != 128) return FB_ERR_GROUP;
   if (s->fmt == FB_FMT_E2M1 && s->group != 32) return FB_ERR_GROUP;
+  // the kernel's rotation has stages up to 4096 (12 butterfly levels)
   if (s->fwht_block != 0 && (!is_pow2(s->fwht_block) || s->fwht_block < 2 ||
-                             s->K % s->fwht_block != 0))
+                             s->fwht_block > 4096 || s->K % s->fwht_block != 0))
     return FB_ERR_FWHT;
   if (s->fmt == FB_FMT_GF4 && s->x_dtype != FB_DT_F16) return FB_ERR_DTYPE;
   if (s->fmt == FB_FMT_E2M1 && s->x_dtype != FB_DT_F16 && s->x_dtype != FB_DT_BF16)

@@ -36,7 +36,7 @@ typedef enum {
   FB_ERR_GROUP = -3,         /* group size not supported for the format / K % group */
   FB_ERR_FORMAT = -4,        /* unknown fmt                                        */
   FB_ERR_DTYPE = -5,         /* unsupported x / y dtype for the format             */
-  FB_ERR_FWHT = -6,          /* fwht_block not a power of two dividing K           */
+  FB_ERR_FWHT = -6,          /* fwht_block not a power of two in [2,4096] | K      */
   FB_ERR_ALIGN = -7,         /* pointer not 16-byte aligned                        */
   FB_ERR_WORKSPACE = -8,     /* workspace too small                                */
   FB_ERR_BATCH = -9,         /* batch size not supported by this entry point       */
@@ -57,7 +57,8 @@ typedef struct {
   int32_t B;           /* batch rows of x / y                                        */
   int32_t group;       /* 128 for GF4, 32 for E2M1                                   */
   int32_t fmt;         /* fb_fmt                                                     */
-  int32_t fwht_block;  /* 0 = no rotation, else power of two dividing K (x' = H x/sqrt(b)) */
+  int32_t fwht_block;  /* 0 = no rotation, else power of two in [2, 4096] dividing K
+                          (x' = H x/sqrt(b)) */
   int32_t x_dtype;     /* fb_dtype of x: GF4 needs F16; E2M1 takes F16 or BF16       */
   int32_t y_dtype;     /* fb_dtype of y: F16, BF16 or F32                            */
 } fb_shape_t;

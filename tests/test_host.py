@@ -33,6 +33,7 @@ def test_abi_exports_every_declared_symbol():
     (dict(K=100), -2), (dict(K=0), -2), (dict(N=0), -2), (dict(B=0), -2),
     (dict(group=64), -3), (dict(fmt=7), -4), (dict(x_dtype=C.DT_BF16), -5),
     (dict(y_dtype=9), -5), (dict(fwht_block=3), -6), (dict(fwht_block=8192), -6),
+    (dict(K=8192, fwht_block=8192), -6),
 ])
 def test_validate_errors(kw, err):
     s = dict(N=64, K=1024, B=1, group=128, fmt=C.FMT_GF4, fwht_block=0, x_dtype=C.DT_F16,
