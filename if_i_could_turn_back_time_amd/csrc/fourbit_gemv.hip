@@ -198,11 +198,15 @@ __host__ __device__ inline int x_row_stride(int nsl) {
   return rs;
 }
 
-// x is read in chunks of 8 consecutive values (16 bytes), kXPre per thread ahead of the
+// x is read in chunks of 8 consecutive values (16 bytes), XP per thread ahead of the
 // slice's first weight loads, so that their wait does not queue behind the weight stream.
-constexpr int kXPre = 4;
+// XP chunks per thread (4 or 8, chosen by the host so that a slice's x fits whenever it
+// can: chunks past the preload are requested after the first weight unit, and loads
+// return in order, so they would wait for its weights).
+constexpr int kXPre = 4;  // x values of the rotation: 256-value sub-blocks per wave
+template <int XP>
 struct XPre {
-  u32x4 v[kXPre];
+  u32x4 v[XP];
 };
 
 __device__ __forceinline__ u32x4 x_load8(const uint16_t* __restrict__ x, int K, int b, int k) {
@@ -214,11 +218,11 @@ __device__ __forceinline__ u32x4 x_load8(const uint16_t* __restrict__ x, int K, 
 // Chunk t of a slice is batch row t / per_row, values k0 + 8 * (t % per_row) ...; thread
 // j * NT + threadIdx.x of an NT-thread workgroup takes chunk t in step j.
 // row_of(t) = t / per_row.
-template <int NT, typename RowOf>
-__device__ __forceinline__ void x_preload(XPre& xp, const uint16_t* __restrict__ x, int K, int k0,
+template <int NT, int XP, typename RowOf>
+__device__ __forceinline__ void x_preload(XPre<XP>& xp, const uint16_t* __restrict__ x, int K, int k0,
                                           int per_row, int nchunks, RowOf row_of, int tid) {
 #pragma unroll
-  for (int j = 0; j < kXPre; ++j) {
+  for (int j = 0; j < XP; ++j) {
     const int t = tid + j * NT;
     if (t < nchunks) {
       const int b = row_of(t);
@@ -228,8 +232,8 @@ __device__ __forceinline__ void x_preload(XPre& xp, const uint16_t* __restrict__
 }
 
 // Plain staging: chunk t lands in its 128-value group of the slice layout.
-template <int NT, typename RowOf>
-__device__ void stage_plain(uint8_t* lds, const XPre& xp, const uint16_t* __restrict__ x, int K,
+template <int NT, int XP, typename RowOf>
+__device__ void stage_plain(uint8_t* lds, const XPre<XP>& xp, const uint16_t* __restrict__ x, int K,
                             int B, int k0, int nsl, int RS, RowOf row_of, int tid) {
   const int per_row = nsl * 16;
   const int n = B * per_row;
@@ -239,11 +243,11 @@ __device__ void stage_plain(uint8_t* lds, const XPre& xp, const uint16_t* __rest
     *reinterpret_cast<u32x4*>(lds + b * RS + (c8 >> 4) * kSliceBytes + (c8 & 15) * 16) = v;
   };
 #pragma unroll
-  for (int j = 0; j < kXPre; ++j) {
+  for (int j = 0; j < XP; ++j) {
     const int t = tid + j * NT;
     if (t < n) put(t, xp.v[j]);
   }
-  for (int t = tid + kXPre * NT; t < n; t += NT) {
+  for (int t = tid + XP * NT; t < n; t += NT) {
     const int b = row_of(t);
     put(t, x_load8(x, K, b, k0 + (t - b * per_row) * 8));
   }
@@ -481,7 +485,7 @@ enum { kFlat = 0, kSliced = 1, kRotated = 2 };
 // NW: waves per workgroup.  16 (one workgroup per CU) in general; 8 (two per CU) for
 // layers with few row tiles per CU, where twice the workgroups, each with half the waves,
 // finish sooner.
-template <int FMT, int XDT, int MODE, int NW>
+template <int FMT, int XDT, int MODE, int NW, int XP>
 __global__ __launch_bounds__(NW * 64) void gemv_kernel(
     const uint8_t* __restrict__ w, const void* __restrict__ x, int K, int B, int SPL, int GS,
     int tq, int tr, unsigned spl_m, int S, int fwht_block, int RS, void* __restrict__ y, int N,
@@ -495,8 +499,14 @@ __global__ __launch_bounds__(NW * 64) void gemv_kernel(
   const int t0 = g * tq + min(g, tr);
   const int t1 = t0 + tq + (g < tr ? 1 : 0);
   const int nsl = SPL * 4;
-  const int nu = (t1 - t0) * SPL;  // units of this workgroup in one slice
-  auto span_of = [&](int u) { return u - fdiv(u, SPL, spl_m) * SPL; };
+  // Unit u of a slice is span u % sp of tile t0 + u / sp, with sp = SPL spans per slice;
+  // the last K-slice may hold fewer (spl_last), and then has fewer units.  A unit's slot
+  // is tile * SPL + span in every slice.
+  const int spl_last = GS - (S - 1) * SPL;
+  int sp = SPL;
+  unsigned sp_m = spl_m;
+  int nu = (t1 - t0) * SPL;  // units of this workgroup in the current slice
+  auto tile_of = [&](int u) { return fdiv(u, sp, sp_m); };
   // LDS: unit counter (16 B) | zero block (256 B) | staged x (xbytes) | partial-sum slots
   int* counter = reinterpret_cast<int*>(lds);
   uint8_t* zeros = lds + 16;
@@ -513,8 +523,7 @@ __global__ __launch_bounds__(NW * 64) void gemv_kernel(
   const uint8_t* xl = col < B ? xst + col * RS + q * kSliceBytes : zeros;
   const int xspan = col < B ? 4 * kSliceBytes : 0;  // x bytes per span for this lane
 
-  // Unit u of a slice is span u % SPL of tile t0 + u / SPL.  After two fixed units per
-  // wave, the waves take units from the workgroup's LDS counter, so a wave that the SIMD's
+  // After two fixed units per wave, the waves take units from the workgroup's LDS counter, so a wave that the SIMD's
   // issue order favours does more of them and all waves finish together.
   // lane 0 holds the fetched index; it is made uniform when it is used, a step later, so
   // the atomic's latency is hidden.
@@ -525,17 +534,19 @@ __global__ __launch_bounds__(NW * 64) void gemv_kernel(
     return u;
   };
   auto unit_off = [&](int s, int u) -> unsigned {
-    const int lt = fdiv(u, SPL, spl_m);
-    return (unsigned)(((int64_t)(t0 + lt) * GS + s * SPL + (u - lt * SPL)) * BB);
+    const int lt = tile_of(u);
+    return (unsigned)(((int64_t)(t0 + lt) * GS + s * SPL + (u - lt * sp)) * BB);
   };
 
   // Decode + MFMA of unit u (slice s) from record r; the unit's partial sums go to its own
   // LDS slot (added to the earlier slices' value), so the final sum has a fixed order
   // whichever wave did the unit.
   auto process = [&](const Rec<FMT>& r, int s, int u) {
-    const f32x4 acc = unit_partial<FMT, XDT>(r, xl + span_of(u) * xspan);
+    const int lt = tile_of(u);
+    const int span = u - lt * sp;
+    const f32x4 acc = unit_partial<FMT, XDT>(r, xl + span * xspan);
     if (col < B) {
-      f32x4* sl = slots + ((size_t)u * 4 + q) * B + col;
+      f32x4* sl = slots + ((size_t)(lt * SPL + span) * 4 + q) * B + col;
       if (s == 0)
         *sl = acc;
       else
@@ -569,12 +580,19 @@ __global__ __launch_bounds__(NW * 64) void gemv_kernel(
     // registers the decode needs, for the whole kernel).
     int tid = threadIdx.x;
     if constexpr (MODE != kFlat) asm volatile("" : "+v"(tid));
-    XPre xp;
+    XPre<XP> xp;
     XRot xr;
     if constexpr (rot)
       rot_preload<NW>(xr, xg, K, B, k0, kw, tid);
     else
-      x_preload<NT>(xp, xg, K, k0, per_row, B * per_row, row_of, tid);
+      x_preload<NT, XP>(xp, xg, K, k0, per_row, B * per_row, row_of, tid);
+    if constexpr (MODE != kFlat) {
+      if (s == nslices - 1 && spl_last != SPL) {  // a last slice with fewer spans
+        sp = spl_last;
+        sp_m = 0xFFFFFFFFu / (unsigned)spl_last;  // floor(2^32 / sp), or one less: fdiv fixes it
+        nu = (t1 - t0) * spl_last;
+      }
+    }
     int u0 = wave, u1 = wave + NW;
     // the rotation cannot start before its x has arrived, and x loads queued behind the
     // first weight unit arrive later: wait for x first
@@ -594,7 +612,7 @@ __global__ __launch_bounds__(NW * 64) void gemv_kernel(
       stage_fwht<NW>(xst, reinterpret_cast<float*>(xst + B * RS), xr, xg, K, B, k0, kw, nsl, RS,
                  fwht_block, fwht_scale, tid);
     else
-      stage_plain<NT>(xst, xp, xg, K, B, k0, nsl, RS, row_of, tid);
+      stage_plain<NT, XP>(xst, xp, xg, K, B, k0, nsl, RS, row_of, tid);
     __syncthreads();  // x staged, counter set
     issue(s, u1, ring[1]);
     __builtin_amdgcn_sched_barrier(0);  // keep the prefetch ahead of the compute
@@ -708,12 +726,13 @@ bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) ==
 
 struct Plan {
   int S = 0;     // K-slices staged one after the other
-  int SPL = 0;   // spans per slice
+  int SPL = 0;   // spans per slice (the last slice: GS - (S - 1) * SPL)
   int grid = 0;  // workgroups
   int GS = 0;    // spans per row
   int tq = 0;    // row tiles per workgroup (the first tr workgroups take one more)
   int tr = 0;
   int nw = 0;    // waves per workgroup: 16 (one workgroup per CU) or 8 (two per CU)
+  int xp = 4;    // x chunks each thread preloads per slice: 4, or 8 for larger slices
   size_t lds = 0;
 };
 
@@ -743,9 +762,9 @@ bool make_plan(const fb_shape_t* s, int cus, Plan& pl) {
     const int grid = std::max(1, std::min(T, pass == 0 ? 2 * cus : cus));
     const int tpw = (T + grid - 1) / grid;  // most tiles a workgroup owns
     for (int S = 1; S <= GS; ++S) {
-      if (GS % S) continue;
+      const int SPL = (GS + S - 1) / S;  // spans per slice; the last slice may have fewer
+      if ((S - 1) * SPL >= GS) continue;   // it would have none
       if (pass == 0 && S > 1) break;  // two workgroups per CU only with one K-slice
-      const int SPL = GS / S;
       if (s->fwht_block && S > 1 && (SPL * 512) % s->fwht_block) continue;
       const size_t lds = plan_lds(s, tpw, SPL);
       if (lds > limit) continue;
@@ -756,6 +775,7 @@ bool make_plan(const fb_shape_t* s, int cus, Plan& pl) {
       pl.tq = T / grid;
       pl.tr = T % grid;
       pl.nw = nw;
+      pl.xp = (s->B * SPL + nw - 1) / nw <= 4 ? 4 : 8;  // 16-byte chunks per thread
       pl.lds = lds;
       return true;
     }
@@ -769,10 +789,10 @@ int device_cus() {
   return cu_count(dev);
 }
 
-template <int FMT, int XDT, int MODE, int NW>
+template <int FMT, int XDT, int MODE, int NW, int XP>
 int launch_gemv(const void* wdev, const void* x, void* y, const fb_shape_t* s, const Plan& pl,
                 hipStream_t stream) {
-  auto kern = gemv_kernel<FMT, XDT, MODE, NW>;
+  auto kern = gemv_kernel<FMT, XDT, MODE, NW, XP>;
   static std::atomic<bool> attr_set{false};
   if (!attr_set.load(std::memory_order_acquire)) {
     if (hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
@@ -790,13 +810,28 @@ int launch_gemv(const void* wdev, const void* x, void* y, const fb_shape_t* s, c
 template <int FMT, int XDT>
 int launch_mode(int mode, const void* wdev, const void* x, void* y, const fb_shape_t* s,
                 const Plan& pl, hipStream_t stream) {
+  const bool deep = pl.xp == 8;
   if (mode == kFlat) {
     if (pl.nw == kWaves / 2)
-      return launch_gemv<FMT, XDT, kFlat, kWaves / 2>(wdev, x, y, s, pl, stream);
-    return launch_gemv<FMT, XDT, kFlat, kWaves>(wdev, x, y, s, pl, stream);
+      return deep ? launch_gemv<FMT, XDT, kFlat, kWaves / 2, 8>(wdev, x, y, s, pl, stream)
+                  : launch_gemv<FMT, XDT, kFlat, kWaves / 2, 4>(wdev, x, y, s, pl, stream);
+    return deep ? launch_gemv<FMT, XDT, kFlat, kWaves, 8>(wdev, x, y, s, pl, stream)
+                : launch_gemv<FMT, XDT, kFlat, kWaves, 4>(wdev, x, y, s, pl, stream);
   }
-  if (mode == kSliced) return launch_gemv<FMT, XDT, kSliced, kWaves>(wdev, x, y, s, pl, stream);
-  return launch_gemv<FMT, XDT, kRotated, kWaves>(wdev, x, y, s, pl, stream);
+  if (mode == kSliced)
+    return deep ? launch_gemv<FMT, XDT, kSliced, kWaves, 8>(wdev, x, y, s, pl, stream)
+                : launch_gemv<FMT, XDT, kSliced, kWaves, 4>(wdev, x, y, s, pl, stream);
+  // the rotation preloads kXPre 256-value sub-blocks per wave instead
+  return launch_gemv<FMT, XDT, kRotated, kWaves, 4>(wdev, x, y, s, pl, stream);
+}
+
+int launch_plan(const void* wdev, const void* x, void* y, const fb_shape_t* s, const Plan& pl,
+                hipStream_t hs) {
+  const int mode = s->fwht_block ? kRotated : pl.S > 1 ? kSliced : kFlat;
+  if (s->fmt == FB_FMT_GF4) return launch_mode<FB_FMT_GF4, FB_DT_F16>(mode, wdev, x, y, s, pl, hs);
+  if (s->x_dtype == FB_DT_BF16)
+    return launch_mode<FB_FMT_E2M1, FB_DT_BF16>(mode, wdev, x, y, s, pl, hs);
+  return launch_mode<FB_FMT_E2M1, FB_DT_F16>(mode, wdev, x, y, s, pl, hs);
 }
 
 }  // namespace
@@ -819,14 +854,28 @@ int fb_gemv(const void* wdev, const void* x, void* y, const fb_shape_t* s, void*
   if (!aligned16(wdev) || !aligned16(x) || (reinterpret_cast<uintptr_t>(y) & 3u))
     return FB_ERR_ALIGN;
   if (s->fwht_block && s->x_dtype != FB_DT_F16) return FB_ERR_DTYPE;
-  Plan pl;
-  if (!make_plan(s, device_cus(), pl)) return FB_ERR_LDS;
+  const int cus = device_cus();
   hipStream_t hs = static_cast<hipStream_t>(stream);
-  const int mode = s->fwht_block ? kRotated : pl.S > 1 ? kSliced : kFlat;
-  if (s->fmt == FB_FMT_GF4) return launch_mode<FB_FMT_GF4, FB_DT_F16>(mode, wdev, x, y, s, pl, hs);
-  if (s->x_dtype == FB_DT_BF16)
-    return launch_mode<FB_FMT_E2M1, FB_DT_BF16>(mode, wdev, x, y, s, pl, hs);
-  return launch_mode<FB_FMT_E2M1, FB_DT_F16>(mode, wdev, x, y, s, pl, hs);
+  Plan pl;
+  if (make_plan(s, cus, pl)) return launch_plan(wdev, x, y, s, pl, hs);
+  // No plan holds the whole batch in LDS (a 4096-wide rotation keeps an fp32 copy of every
+  // batch row): the rows run in the largest chunks that fit, each streaming the weights.
+  fb_shape_t sc = *s;
+  int bc = s->B - 1;
+  for (; bc >= 1; --bc) {
+    sc.B = bc;
+    if (make_plan(&sc, cus, pl)) break;
+  }
+  if (bc < 1) return FB_ERR_LDS;
+  const size_t ysize = s->y_dtype == FB_DT_F32 ? 4 : 2;
+  for (int b0 = 0; b0 < s->B; b0 += bc) {
+    sc.B = std::min(bc, s->B - b0);
+    if (!make_plan(&sc, cus, pl)) return FB_ERR_LDS;
+    const int st = launch_plan(wdev, static_cast<const uint8_t*>(x) + (size_t)b0 * s->K * 2,
+                               static_cast<uint8_t*>(y) + (size_t)b0 * s->N * ysize, &sc, pl, hs);
+    if (st != FB_OK) return st;
+  }
+  return FB_OK;
 }
 
 int fb_dequant(const void* wdev, void* w_out, int32_t out_dtype, const fb_shape_t* s,

@@ -146,7 +146,10 @@ int fb_dequant_host(const uint8_t* codes, const void* meta, float* w_out, const 
  * ws: device workspace of at least fb_workspace_bytes(s) bytes (16-byte aligned).  The
  * current kernels exchange nothing between workgroups through memory, so
  * fb_workspace_bytes is 0 for every valid shape and ws may be NULL; the argument is
- * kept so that a future split-K variant does not change the ABI. */
+ * kept so that a future split-K variant does not change the ABI.
+ * A batch whose staged activations do not fit LDS at once (a 4096-wide rotation keeps an
+ * fp32 copy of every batch row) runs as several launches over row chunks, each streaming
+ * the weights; FB_ERR_LDS only when a single row does not fit. */
 int fb_gemv(const void* wdev, const void* x, void* y, const fb_shape_t* s, void* ws,
             size_t ws_bytes, void* stream);
 

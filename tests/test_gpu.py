@@ -129,6 +129,25 @@ def test_gemv_fwht_vs_oracle(B, N, K, block):
     assert rel < 0.15
 
 
+@pytest.mark.parametrize("B", [5, 8, 16])
+@pytest.mark.parametrize("N,K,block", [(96, 11008, 256), (64, 4096, 4096), (40, 8192, 4096)])
+def test_gemv_fwht_large_batch_vs_oracle(B, N, K, block):
+    """Rotated layers at larger batches: K = 11008 (256-blocks) runs three K-slices, the
+    last one ragged; 4096-blocks keep an fp32 copy of each batch row in LDS, so batches
+    that do not fit run in row chunks inside fb_gemv."""
+    say("fwht large batch", B, N, K, block)
+    gen = torch.Generator().manual_seed(7 * N + K + B)
+    w = torch.randn(N, K, generator=gen) * 0.02
+    pw = PackedWeight.quantize(w, "gf4", fwht_block=block, device=DEV)
+    x = torch.randn(B, K, generator=gen).half()
+    yref = oracle_y(pw, x)
+    for ydt in (torch.float32, torch.float16):
+        y = pw.gemv(x.to(DEV), out_dtype=ydt)
+        torch.cuda.synchronize()
+        ok, emax, _ = within_tol(y, yref, 2.0 ** -11 if ydt == torch.float16 else 0.0)
+        assert ok, f"{ydt}: max abs err {emax}"
+
+
 @pytest.mark.parametrize("fmt", ["gf4", "e2m1"])
 def test_special_inputs(fmt):
     say("special", fmt)
@@ -230,6 +249,31 @@ def test_quantlinear_batch_edges_gpu():
             extra = {torch.float16: 2.0 ** -11, torch.bfloat16: 2.0 ** -8}[xdt]
             ok, emax, _ = within_tol(y.reshape(-1, 80), yref, extra)
             assert ok, f"{fmt} {shape}: max abs err {emax}"
+
+
+def test_quantlinear_hadamard_forward_gpu():
+    """QuantLinear(hadamard=True) on 24 rows (launches of 16 + 8 rows; the 4096-wide
+    rotation runs each in row chunks that fit LDS) against the oracle's rotated product
+    plus bias; commit() rotates the packed weight back, and F.linear with it agrees."""
+    say("quantlinear hadamard")
+    g = torch.Generator().manual_seed(4096)
+    lin = torch.nn.Linear(4096, 96)
+    q = QuantLinear(lin, hadamard=True).to(DEV)
+    assert q.fwht_block == 4096
+    x = torch.randn(2, 12, 4096, generator=g).half()
+    y = q(x.to(DEV))
+    torch.cuda.synchronize()
+    assert y.shape == (2, 12, 96) and y.dtype == torch.float16
+    codes = O.unpack_nibbles(q.codes.cpu().numpy())
+    meta = q.meta.cpu().numpy().view(np.uint16)
+    yref = O.y_ref("gf4", codes, meta, x.reshape(-1, 4096), 4096) + lin.bias.detach()
+    ok, emax, _ = within_tol(y.reshape(-1, 96), yref, 2.0 ** -10)
+    assert ok, f"max abs err {emax}"
+    q.commit()
+    ycommit = torch.nn.functional.linear(x.reshape(-1, 4096).float(), q.weight.detach().cpu(),
+                                         lin.bias.detach())
+    ok, emax, _ = within_tol(y.reshape(-1, 96), ycommit, 2.0 ** -9)
+    assert ok, f"vs committed weight: max abs err {emax}"
 
 
 def test_ragged_k_masked_forward_gpu():
