@@ -3,6 +3,8 @@ include/fourbit.h declares, argument validation, and the native packers / layout
 transform against the oracle and the golden fixtures (bit-exact)."""
 import ctypes
 import re
+import shutil
+import subprocess
 from pathlib import Path
 
 import numpy as np
@@ -391,3 +393,22 @@ def test_lenet300_fixture_packs_and_round_trips():
         assert fresh[i].fmt == "gf4"
         assert torch.equal(fresh[i].wdev, q[i].wdev)
         assert torch.equal(fresh[i].dequantized_weight(), q[i].dequantized_weight())
+
+
+@pytest.mark.skipif(shutil.which("gcc") is None, reason="gcc not on PATH")
+def test_c_abi_from_c(tmp_path):
+    """The host-side C ABI called from C, as a native binding would: tests/c/abi_host.c is
+    compiled with gcc against include/fourbit.h (-Wall -Wextra -Werror), linked to the
+    built libfourbit.so, and checks known answers of validation, both packers, integer
+    levels, the FWHT and the device-layout round trip."""
+    C.lib()  # the library is built
+    root = Path(__file__).resolve().parents[1]
+    exe = tmp_path / "abi_host"
+    libdir = C.LIB_PATH.parent
+    subprocess.run(["gcc", "-std=c99", "-O1", "-Wall", "-Wextra", "-Werror",
+                    f"-I{root / 'include'}", str(root / "tests" / "c" / "abi_host.c"),
+                    "-o", str(exe), f"-L{libdir}", "-l:libfourbit.so",
+                    f"-Wl,-rpath,{libdir}", "-lm"], check=True)
+    r = subprocess.run([str(exe)], capture_output=True, text=True, timeout=60)
+    assert r.returncode == 0, r.stderr
+    assert r.stdout.strip() == "ok"
