@@ -1,4 +1,5 @@
-"""Builds libfourbit.so in-tree: hipcc for the gfx950 kernels, g++ for the host packers.
+"""Builds libfourbit.so in-tree: hipcc for the gfx950 kernels, g++ for the host packers;
+then ``tests/c/abi_gpu``, the GPU tests' native caller of the library's C ABI.
 
 Run as ``python -m if_i_could_turn_back_time_amd.build_lib`` (``__graft_entry__.build()``
 calls :func:`build`).  Always recompiles.  Objects go to ``_build/`` at the repo root;
@@ -18,6 +19,7 @@ CSRC = PKG / "csrc"
 INCLUDE = ROOT / "include"
 BUILD = ROOT / "_build"
 LIB = PKG / "libfourbit.so"
+C_TESTS = ROOT / "tests" / "c"
 ARCH = "gfx950"
 
 # packed fp32 VALU ops are disabled for every HIP translation unit: a correctness
@@ -75,6 +77,14 @@ def build(verbose: bool = False) -> Path:
             print(" ".join(cmd), flush=True)
         _run(cmd)
     os.replace(tmp, LIB)
+    # the GPU test suite's native (no Python) caller of the C ABI, linked to the library
+    # through a path relative to itself, so that it runs wherever the tree is copied
+    caller = [_hipcc(), *HIP_FLAGS, f"-I{INCLUDE}", str(C_TESTS / "abi_gpu.cpp"), "-o",
+              str(C_TESTS / "abi_gpu"), f"-L{PKG}", "-l:libfourbit.so",
+              "-Wl,-rpath,$ORIGIN/../../if_i_could_turn_back_time_amd"]
+    if verbose:
+        print(" ".join(caller), flush=True)
+    _run(caller)
     return LIB
 
 

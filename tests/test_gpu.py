@@ -1,6 +1,7 @@
 """GPU parity: device decode bit-exact vs the oracle, fused GEMV within the north-star
 tolerance |y - y_ref| <= 1e-2 + 1e-3 |y_ref| (y_ref = oracle dequantize-then-F.linear in
 fp32 on the CPU), all through the C ABI of libfourbit.so."""
+import subprocess
 import sys
 from pathlib import Path
 
@@ -226,6 +227,20 @@ def oracle_weight(q: QuantLinear) -> torch.Tensor:
     codes = O.unpack_nibbles(q.codes.cpu().numpy())
     meta = q.meta.cpu().numpy().view(np.uint16) if q.fmt == "gf4" else q.meta.cpu().numpy()
     return O.dequant_f32(q.fmt, codes, meta)[:, :q.in_features]
+
+
+def test_c_abi_gpu_caller():
+    """The C ABI from a native C++ caller with no Python or torch (tests/c/abi_gpu.cpp,
+    built by build_lib): hipMalloc'd buffers, its own stream, weights packed by the host
+    packers, fb_gemv, and y checked against an fp64 host product of the exact decode
+    (GF4 fp16 x batch 3 with a partial row tile; E2M1 bf16 x batch 16)."""
+    say("native C++ caller")
+    exe = Path(__file__).resolve().parent / "c" / "abi_gpu"
+    assert exe.exists(), "tests/c/abi_gpu is built with the library (__graft_entry__.build())"
+    r = subprocess.run([str(exe)], capture_output=True, text=True, timeout=120)
+    print(r.stdout, flush=True)
+    assert r.returncode == 0, r.stdout + r.stderr
+    assert r.stdout.strip().endswith("ok")
 
 
 def test_quantlinear_batch_edges_gpu():
