@@ -25,6 +25,7 @@ FMT_BY_NAME = {"gf4": FMT_GF4, "e2m1": FMT_E2M1}
 GROUP_BY_FMT = {FMT_GF4: 128, FMT_E2M1: 32}
 DTYPE_CODE = {torch.float16: DT_F16, torch.bfloat16: DT_BF16, torch.float32: DT_F32}
 ABI_VERSION = 1
+ERR_VALUE = -10  # FB_ERR_VALUE: non-finite / non-integer / out-of-range packer input
 
 # every symbol include/fourbit.h declares
 EXPORTED = (
@@ -240,8 +241,9 @@ def gemv(wdev: torch.Tensor, x: torch.Tensor, y: torch.Tensor, shape: FbShape,
     if need and (workspace is None or workspace.numel() < need):
         workspace = new_workspace(shape, x.device)
     wp = _ptr(workspace) if need else None
-    check(lib().fb_gemv(_ptr(wdev), _ptr(x), _ptr(y), ctypes.byref(shape), wp, need,
-                        _stream(x.device)))
+    with torch.cuda.device(x.device):  # HIP launches on the current device
+        check(lib().fb_gemv(_ptr(wdev), _ptr(x), _ptr(y), ctypes.byref(shape), wp, need,
+                            _stream(x.device)))
     return y
 
 
@@ -251,8 +253,9 @@ def dequant_device(wdev: torch.Tensor, shape: FbShape, out_dtype=torch.float32) 
     if wdev.numel() < device_bytes(shape):
         raise ValueError("weight stream is smaller than fb_device_bytes(shape)")
     out = torch.empty(shape.N, shape.K, dtype=out_dtype, device=wdev.device)
-    check(lib().fb_dequant(_ptr(wdev), _ptr(out), DTYPE_CODE[out_dtype], ctypes.byref(shape),
-                           _stream(wdev.device)))
+    with torch.cuda.device(wdev.device):
+        check(lib().fb_dequant(_ptr(wdev), _ptr(out), DTYPE_CODE[out_dtype],
+                               ctypes.byref(shape), _stream(wdev.device)))
     return out
 
 
@@ -274,11 +277,12 @@ def quantize_gf4_gpu(w: torch.Tensor, keep: torch.Tensor | None = None):
     else:
         finite = torch.isfinite(w)
     if not bool(finite.all()):
-        raise RuntimeError(strerror(-10))
+        raise RuntimeError(strerror(ERR_VALUE))
     codes = torch.empty(N, K // 2, dtype=torch.uint8, device=w.device)
     book = torch.empty(N, max(K // 128, 1), 16, dtype=torch.int16, device=w.device)
-    check(lib().fb_quantize_gf4_gpu(_ptr(w), _ptr(kp) if kp is not None else None, N, K,
-                                    _ptr(codes), _ptr(book), _stream(w.device)))
+    with torch.cuda.device(w.device):
+        check(lib().fb_quantize_gf4_gpu(_ptr(w), _ptr(kp) if kp is not None else None, N, K,
+                                        _ptr(codes), _ptr(book), _stream(w.device)))
     return codes, book
 
 
@@ -291,9 +295,10 @@ def quantize_e2m1_gpu(w: torch.Tensor):
     w = w.detach().to(torch.float32).contiguous()
     N, K = w.shape
     if not bool(torch.isfinite(w).all()):
-        raise RuntimeError(strerror(-10))
+        raise RuntimeError(strerror(ERR_VALUE))
     codes = torch.empty(N, K // 2, dtype=torch.uint8, device=w.device)
     scales = torch.empty(N, max(K // 32, 1), dtype=torch.uint8, device=w.device)
-    check(lib().fb_quantize_e2m1_gpu(_ptr(w), N, K, _ptr(codes), _ptr(scales),
-                                     _stream(w.device)))
+    with torch.cuda.device(w.device):
+        check(lib().fb_quantize_e2m1_gpu(_ptr(w), N, K, _ptr(codes), _ptr(scales),
+                                         _stream(w.device)))
     return codes, scales

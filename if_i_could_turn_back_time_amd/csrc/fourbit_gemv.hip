@@ -793,12 +793,16 @@ template <int FMT, int XDT, int MODE, int NW, int XP>
 int launch_gemv(const void* wdev, const void* x, void* y, const fb_shape_t* s, const Plan& pl,
                 hipStream_t stream) {
   auto kern = gemv_kernel<FMT, XDT, MODE, NW, XP>;
-  static std::atomic<bool> attr_set{false};
-  if (!attr_set.load(std::memory_order_acquire)) {
+  // the LDS limit is a per-device attribute of the kernel: set once on each device
+  static std::atomic<uint64_t> attr_set{0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return FB_ERR_HIP;
+  const uint64_t bit = dev >= 0 && dev < 64 ? uint64_t{1} << dev : 0;
+  if (!bit || !(attr_set.load(std::memory_order_acquire) & bit)) {
     if (hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
                             hipFuncAttributeMaxDynamicSharedMemorySize, kLdsLimit) != hipSuccess)
       return FB_ERR_HIP;
-    attr_set.store(true, std::memory_order_release);
+    attr_set.fetch_or(bit, std::memory_order_release);
   }
   hipLaunchKernelGGL(kern, dim3(pl.grid), dim3(NW * 64), pl.lds, stream,
                      static_cast<const uint8_t*>(wdev), x, s->K, s->B, pl.SPL, pl.GS, pl.tq,

@@ -135,7 +135,8 @@ int fb_from_device(const void* wdev, uint8_t* codes, void* meta, const fb_shape_
 int fb_dequant_host(const uint8_t* codes, const void* meta, float* w_out, const fb_shape_t* s);
 
 /* ---------------------------------------------------------------------------------
- * GPU entry points (hipStream_t passed as void*).
+ * GPU entry points (hipStream_t passed as void*).  They launch on the calling thread's
+ * current HIP device; the stream and every device pointer must belong to it.
  * ------------------------------------------------------------------------------- */
 
 /* Fused dequant-GEMV, batch 1..16: y = x' . W^T with x' = FWHT_b(x) when fwht_block.
