@@ -82,7 +82,7 @@ def packed_linear(wdev: torch.Tensor, N: int, K: int, fmt: str, fwht_block: int,
                              C.DTYPE_CODE[ydt])
         C.gemv(wdev, xk[b0:b1], y[b0:b1], shape, C.new_workspace(shape, x.device))
     if bias is not None:
-        y = y + bias.to(ydt)
+        y.add_(bias.to(ydt))  # y is this call's own buffer
     return y.reshape(*lead, N)
 
 

@@ -149,6 +149,31 @@ def test_gemv_fwht_large_batch_vs_oracle(B, N, K, block):
         assert ok, f"{ydt}: max abs err {emax}"
 
 
+@pytest.mark.parametrize("B", [1, 4, 16])
+@pytest.mark.parametrize("N,K,block", [(64, 4096, 4096), (48, 11008, 256)])
+def test_gemv_e2m1_fwht_vs_oracle(B, N, K, block):
+    """E2M1 weights with a rotation (fp16 x): the same in-kernel rotation feeding the
+    E2M1 decode; also through QuantLinear(fmt='e2m1', hadamard=block)."""
+    say("e2m1 fwht", B, N, K, block)
+    gen = torch.Generator().manual_seed(3 * N + K + B)
+    w = torch.randn(N, K, generator=gen) * 0.02
+    pw = PackedWeight.quantize(w, "e2m1", fwht_block=block, device=DEV)
+    x = torch.randn(B, K, generator=gen).half()
+    yref = oracle_y(pw, x)
+    y = pw.gemv(x.to(DEV), out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    ok, emax, _ = within_tol(y, yref)
+    assert ok, f"max abs err {emax}"
+    lin = torch.nn.Linear(K, N, bias=False)
+    with torch.no_grad():
+        lin.weight.copy_(w)
+    q = QuantLinear(lin, fmt="e2m1", hadamard=block).to(DEV)
+    yq = q(x.to(DEV))
+    torch.cuda.synchronize()
+    ok, emax, _ = within_tol(yq, yref, 2.0 ** -11)
+    assert ok, f"QuantLinear: max abs err {emax}"
+
+
 @pytest.mark.parametrize("fmt", ["gf4", "e2m1"])
 def test_special_inputs(fmt):
     say("special", fmt)
