@@ -89,6 +89,8 @@ def synth(kind: str, N: int, K: int, B: int, xdtype):
 
 
 MALL_BYTES = 256 * 2**20  # MI355X Infinity Cache (memory-side, in front of HBM)
+MIN_WARM_S = 0.25  # least wall time of back-to-back warm-up calls before a timed region
+LAST_WARMUP_CALLS = 0  # warm-up calls the last time_gpu ran (>= the requested warm-up)
 
 
 def n_copies(nbytes: int, cold: bool) -> int:
@@ -115,9 +117,17 @@ def time_gpu(pw: PackedWeight, x: torch.Tensor, y: torch.Tensor, steps: int, war
     wsp, nws = (ws.data_ptr(), ws.numel()) if ws is not None else (None, 0)
     stream = torch.cuda.current_stream()
     sp = stream.cuda_stream
-    for i in range(warmup):
-        C.check(L.fb_gemv(wps[i % ncp], xp, yp, sref, wsp, nws, sp))
-    torch.cuda.synchronize()
+    # Warm-up: at least `warmup` calls and at least MIN_WARM_S of back-to-back calls.  After
+    # idle, MI355X runs the first ~20 ms of calls at lower clocks (~37 against ~30.5 us/call
+    # on the north-star layer), so a short warm-up would time the clock ramp, not the kernel.
+    done, t_end = 0, time.perf_counter() + MIN_WARM_S
+    while done < warmup or time.perf_counter() < t_end:
+        for _ in range(50):
+            C.check(L.fb_gemv(wps[done % ncp], xp, yp, sref, wsp, nws, sp))
+            done += 1
+        torch.cuda.synchronize()
+    global LAST_WARMUP_CALLS
+    LAST_WARMUP_CALLS = done
     t0 = torch.cuda.Event(enable_timing=True)
     t1 = torch.cuda.Event(enable_timing=True)
     t0.record(stream)
@@ -297,6 +307,7 @@ def run_workload(name: str, steps: int, warmup: int, want_cpu: bool, check: bool
     xd = x.to("cuda:0")
     y = torch.empty(B, N, dtype=xdt, device="cuda:0")
     ms, ncp = time_gpu(pw, xd, y, steps, warmup, cold=True)
+    warm_calls = LAST_WARMUP_CALLS
     ms_warm = time_gpu(pw, xd, y, steps, warmup, cold=False)[0] if warm else None
     ms_graph = time_gpu_graph(pw, xd, y, min(steps, 200)) if warm else None
     nbytes = pw.algorithmic_bytes(B)
@@ -305,7 +316,7 @@ def run_workload(name: str, steps: int, warmup: int, want_cpu: bool, check: bool
         "workload": name, "fmt": fmt, "K": K, "N": N, "B": B, "fwht_block": fb,
         "bytes_per_call": nbytes, "weight_stream_bytes": N * K // 2,
         "us_per_call": ms * 1e3, "GBps": gbs, "frac_of_8TBps": gbs / PEAK_GBS,
-        "weight_copies_cycled": ncp,
+        "weight_copies_cycled": ncp, "warmup_calls_run": warm_calls,
         "us_per_call_warm": None if ms_warm is None else ms_warm * 1e3,
         "GBps_warm": None if ms_warm is None else nbytes / (ms_warm * 1e-3) / 1e9,
         "us_per_call_graph": None if ms_graph is None else ms_graph * 1e3,
@@ -411,7 +422,9 @@ def main():
             "bytes_per_call": rec["bytes_per_call"],
             "weight_stream_bytes": rec["weight_stream_bytes"],
             "timing": (f"cold: {rec['weight_copies_cycled']} weight copies cycled so every "
-                       "call streams from HBM, not the 256 MiB Infinity Cache"),
+                       "call streams from HBM, not the 256 MiB Infinity Cache; warm-up of "
+                       f"{rec['warmup_calls_run']} calls (at least --warmup and "
+                       f"{MIN_WARM_S} s, past the GPU's clock ramp after idle)"),
             "us_per_call_warm_single_copy": rec["us_per_call_warm"],
             "GBps_warm_single_copy": rec["GBps_warm"],
             "us_per_call_hipgraph_warm": rec["us_per_call_graph"],
