@@ -203,7 +203,7 @@ __host__ __device__ inline int x_row_stride(int nsl) {
 // XP chunks per thread (4 or 8, chosen by the host so that a slice's x fits whenever it
 // can: chunks past the preload are requested after the first weight unit, and loads
 // return in order, so they would wait for its weights).
-constexpr int kXPre = 4;  // x values of the rotation: 256-value sub-blocks per wave
+constexpr int kXPre = 4;  // the rotation's x preload: 256-value sub-blocks per wave
 template <int XP>
 struct XPre {
   u32x4 v[XP];
