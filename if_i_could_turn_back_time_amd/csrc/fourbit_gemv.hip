@@ -198,11 +198,10 @@ __host__ __device__ inline int x_row_stride(int nsl) {
   return rs;
 }
 
-// x is read in chunks of 8 consecutive values (16 bytes), XP per thread ahead of the
-// slice's first weight loads, so that their wait does not queue behind the weight stream.
-// XP chunks per thread (4 or 8, chosen by the host so that a slice's x fits whenever it
-// can: chunks past the preload are requested after the first weight unit, and loads
-// return in order, so they would wait for its weights).
+// x is read in chunks of 8 consecutive values (16 bytes), XP per thread (4 or 8, chosen by
+// the host so that a slice's x fits whenever it can) ahead of the slice's first weight
+// loads.  Chunks past the preload are requested after the first weight unit, and loads
+// return in order, so they wait for its weights.
 constexpr int kXPre = 4;  // the rotation's x preload: 256-value sub-blocks per wave
 template <int XP>
 struct XPre {
