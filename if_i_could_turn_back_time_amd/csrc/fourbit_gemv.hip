@@ -761,10 +761,13 @@ bool make_plan(const fb_shape_t* s, int cus, Plan& pl) {
     const int grid = std::max(1, std::min(T, pass == 0 ? 2 * cus : cus));
     const int tpw = (T + grid - 1) / grid;  // most tiles a workgroup owns
     for (int S = 1; S <= GS; ++S) {
-      const int SPL = (GS + S - 1) / S;  // spans per slice; the last slice may have fewer
-      if ((S - 1) * SPL >= GS) continue;   // it would have none
+      int SPL = (GS + S - 1) / S;  // spans per slice; the last slice may have fewer
+      if (S > 1 && s->fwht_block > 512) {  // a slice holds whole rotation blocks
+        const int bs = s->fwht_block / 512;
+        SPL = (SPL + bs - 1) / bs * bs;
+      }
+      if ((S - 1) * SPL >= GS) continue;  // the last slice would have no span
       if (pass == 0 && S > 1) break;  // two workgroups per CU only with one K-slice
-      if (s->fwht_block && S > 1 && (SPL * 512) % s->fwht_block) continue;
       const size_t lds = plan_lds(s, tpw, SPL);
       if (lds > limit) continue;
       pl.S = S;

@@ -111,7 +111,7 @@ def test_gemv_vs_oracle(fmt, xdt, B, N, K):
 @pytest.mark.parametrize("B", [1, 2, 4])
 @pytest.mark.parametrize("N,K,block", [(64, 4096, 4096), (96, 11008, 256), (32, 1024, 256),
                                        (16, 512, 2), (24, 2048, 32), (40, 3072, 512),
-                                       (48, 2048, 1024), (20, 6144, 2048)])
+                                       (48, 2048, 1024), (20, 6144, 2048), (24, 28672, 4096)])
 def test_gemv_fwht_vs_oracle(B, N, K, block):
     say("fwht", B, N, K, block)
     gen = torch.Generator().manual_seed(N + K + block)
