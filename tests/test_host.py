@@ -5,6 +5,7 @@ import ctypes
 import re
 import shutil
 import subprocess
+import sys
 from pathlib import Path
 
 import numpy as np
@@ -412,3 +413,13 @@ def test_c_abi_from_c(tmp_path):
     r = subprocess.run([str(exe)], capture_output=True, text=True, timeout=60)
     assert r.returncode == 0, r.stderr
     assert r.stdout.strip() == "ok"
+
+
+def test_bench_refuses_several_gpus():
+    """bench.py runs on one GPU: --gpus N > 1 exits non-zero with a message, before any
+    GPU work (this runs without a GPU)."""
+    root = Path(__file__).resolve().parents[1]
+    r = subprocess.run([sys.executable, str(root / "bench.py"), "--gpus", "2"],
+                       capture_output=True, text=True, timeout=300)
+    assert r.returncode != 0
+    assert "one GPU" in (r.stdout + r.stderr)
