@@ -746,14 +746,14 @@ size_t plan_lds(const fb_shape_t* s, int tpw, int SPL) {
 }
 
 // The fewest K-slices whose LDS fits.  One 16-wave workgroup per CU (up to the number of
-// row tiles), or, for unrotated batch-1 layers with few row tiles per CU (GF4 at most 3,
+// row tiles), or, for unrotated batch-1 layers with few row tiles per CU (GF4 at most 4,
 // E2M1 at most 2) and LDS that fits twice in a CU, two 8-wave workgroups per CU (measured
-// 0.3-1.4 us faster there; no faster on large layers, slower at batch 2 and 4, and slower
-// with a rotation, which each workgroup would then compute with half the waves).
+// 0.3-1.4 us faster there; slower on larger layers, at batch 2 and 4, and with a rotation,
+// which each workgroup would then compute with half the waves).
 bool make_plan(const fb_shape_t* s, int cus, Plan& pl) {
   const int GS = (s->K / 128 + 3) / 4;
   const int T = (s->N + 15) / 16;
-  const int half_tiles = (s->fmt == FB_FMT_GF4 ? 3 : 2) * cus;
+  const int half_tiles = (s->fmt == FB_FMT_GF4 ? 4 : 2) * cus;
   const bool half = !s->fwht_block && s->B == 1 && T <= half_tiles;
   for (int pass = half ? 0 : 1; pass < 2; ++pass) {
     const int nw = pass == 0 ? kWaves / 2 : kWaves;
