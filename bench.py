@@ -30,67 +30,21 @@ sys.path.insert(0, str(ROOT))
 
 from if_i_could_turn_back_time_amd import PackedWeight, fwht_block_for  # noqa: E402
 from if_i_could_turn_back_time_amd import _capi as C  # noqa: E402
+from if_i_could_turn_back_time_amd import workloads  # noqa: E402
 
 PEAK_GBS = 8000.0
 METRIC = "achieved HBM GB/s (% of roofline) & µs/call, 4-bit dequant-GEMV at batch 1"
 
-# name -> (fmt, K, N, B, generator, fwht)
-WORKLOADS = {
-    "gf4_k8192_n28672_b1": ("gf4", 8192, 28672, 1, "cfg4", False),
-    "gf4_k28672_n8192_b1": ("gf4", 28672, 8192, 1, "cfg4", False),
-    "gf4_k8192_n28672_b2": ("gf4", 8192, 28672, 2, "cfg4", False),
-    "gf4_k8192_n28672_b4": ("gf4", 8192, 28672, 4, "cfg4", False),
-    "gf4_k28672_n8192_b2": ("gf4", 28672, 8192, 2, "cfg4", False),
-    "gf4_k4096_n4096_b1": ("gf4", 4096, 4096, 1, "cfg1", False),
-    "e2m1_k4096_n4096_b1": ("e2m1", 4096, 4096, 1, "cfg2", False),
-    "e2m1_k4096_n11008_b1": ("e2m1", 4096, 11008, 1, "cfg2", False),
-    "e2m1_k11008_n4096_b1": ("e2m1", 11008, 4096, 1, "cfg2", False),
-    "gf4fwht_k4096_n4096_b1": ("gf4", 4096, 4096, 1, "cfg1", True),
-    "gf4fwht_k4096_n11008_b1": ("gf4", 4096, 11008, 1, "cfg1", True),
-    "gf4fwht_k11008_n4096_b1": ("gf4", 11008, 4096, 1, "cfg1", True),
-    "gf4_k28672_n8192_b4": ("gf4", 28672, 8192, 4, "cfg4", False),
-    # small-batch dense contraction (batch 8 / 16): E2M1 as config 2, GF4 as config 1
-    "e2m1_k8192_n8192_b8": ("e2m1", 8192, 8192, 8, "cfg2", False),
-    "e2m1_k8192_n8192_b16": ("e2m1", 8192, 8192, 16, "cfg2", False),
-    "e2m1_k8192_n28672_b8": ("e2m1", 8192, 28672, 8, "cfg2", False),
-    "e2m1_k8192_n28672_b16": ("e2m1", 8192, 28672, 16, "cfg2", False),
-    "gf4_k8192_n8192_b8": ("gf4", 8192, 8192, 8, "cfg1", False),
-    "gf4_k8192_n8192_b16": ("gf4", 8192, 8192, 16, "cfg1", False),
-    "gf4_k8192_n28672_b8": ("gf4", 8192, 28672, 8, "cfg1", False),
-    "gf4_k8192_n28672_b16": ("gf4", 8192, 28672, 16, "cfg1", False),
-    # the reference's own 4-bit weight (QuantLinear.commit) as GF4 integer-level codebooks
-    "int4ref_k8192_n28672_b1": ("int4ref", 8192, 28672, 1, "cfg4", False),
-}
-DEFAULT = "gf4_k8192_n28672_b1"
-
-
-def synth(kind: str, N: int, K: int, B: int, xdtype):
-    """Seeded synthetic inputs (CPU generator, seed 0; order: weights, outlier masks,
-    activations), per the input-generation rules of the benchmark configs."""
-    g = torch.Generator().manual_seed(0)
-    if kind == "cfg4":
-        w = torch.randn(N, K, generator=g) * 0.015
-        m = torch.rand(N, K, generator=g) < 0.005
-        w[m] = torch.randn(int(m.sum()), generator=g) * (8 * 0.015)
-        x = torch.randn(B, K, generator=g)
-    elif kind == "cfg2":
-        nu = 5
-        z = torch.randn(N, K, generator=g)
-        chi = sum(torch.randn(N, K, generator=g) ** 2 for _ in range(nu))
-        w = z / torch.sqrt(chi / nu) * (0.02 / np.sqrt(nu / (nu - 2)))
-        x = torch.randn(B, K, generator=g)
-        n_out = max(1, round(0.001 * K))
-        pos = torch.randperm(K, generator=g)[:n_out]
-        x[:, pos] *= 20.0
-    else:  # cfg1 / cfg3
-        w = torch.randn(N, K, generator=g) * 0.02
-        x = torch.randn(B, K, generator=g)
-    return w.contiguous(), x.to(xdtype)
+# name -> (fmt, K, N, B, generator, rotated); generators per the benchmark configs
+WORKLOADS = workloads.WORKLOADS
+DEFAULT = workloads.DEFAULT
 
 
 MALL_BYTES = 256 * 2**20  # MI355X Infinity Cache (memory-side, in front of HBM)
 MIN_WARM_S = 0.25  # least wall time of back-to-back warm-up calls before a timed region
 LAST_WARMUP_CALLS = 0  # warm-up calls the last time_gpu ran (>= the requested warm-up)
+PRE_CALLS = 3  # untimed calls enqueued before each start event (busy GPU at the stamp)
+MEDIAN_WINDOWS = 9  # timed regions of --steps calls whose median is reported beside value
 
 
 def n_copies(nbytes: int, cold: bool) -> int:
@@ -102,10 +56,17 @@ def n_copies(nbytes: int, cold: bool) -> int:
 
 
 def time_gpu(pw: PackedWeight, x: torch.Tensor, y: torch.Tensor, steps: int, warmup: int,
-             cold: bool = True):
+             cold: bool = True, windows: int = 0):
     """Back-to-back launches on the current stream, timed with HIP events on that stream
     (the stream fb_gemv launches on).  cold: cycle through weight copies that together
-    exceed the Infinity Cache.  Returns mean ms per call."""
+    exceed the Infinity Cache.
+
+    The timed region is exactly ``steps`` calls, bracketed by device synchronisations.
+    Inside it, ``PRE_CALLS`` untimed calls are enqueued before the start event, so the
+    event is stamped on a busy GPU: the host's first launch latency (argument checks,
+    plan, ctypes) would otherwise land inside the region.  ``windows`` more regions of
+    the same length follow for the median.  Returns (mean ms per call of the first
+    region, number of weight copies, [ms per call of each extra region])."""
     L = C.lib()
     shape = pw.shape(x.shape[0], x.dtype, y.dtype)
     sref = ctypes.byref(shape)
@@ -128,15 +89,24 @@ def time_gpu(pw: PackedWeight, x: torch.Tensor, y: torch.Tensor, steps: int, war
         torch.cuda.synchronize()
     global LAST_WARMUP_CALLS
     LAST_WARMUP_CALLS = done
-    t0 = torch.cuda.Event(enable_timing=True)
-    t1 = torch.cuda.Event(enable_timing=True)
-    t0.record(stream)
-    for i in range(steps):
-        L.fb_gemv(wps[i % ncp], xp, yp, sref, wsp, nws, sp)
-    t1.record(stream)
-    torch.cuda.synchronize()
+
+    def region():
+        torch.cuda.synchronize()
+        for i in range(PRE_CALLS):
+            L.fb_gemv(wps[i % ncp], xp, yp, sref, wsp, nws, sp)
+        t0 = torch.cuda.Event(enable_timing=True)
+        t1 = torch.cuda.Event(enable_timing=True)
+        t0.record(stream)
+        for i in range(steps):
+            L.fb_gemv(wps[(PRE_CALLS + i) % ncp], xp, yp, sref, wsp, nws, sp)
+        t1.record(stream)
+        torch.cuda.synchronize()
+        return t0.elapsed_time(t1) / steps
+
+    first = region()
+    extra = [region() for _ in range(windows)]
     del copies
-    return t0.elapsed_time(t1) / steps, ncp
+    return first, ncp, extra
 
 
 def time_gpu_graph(pw, x, y, steps: int, reps: int = 5):
@@ -234,7 +204,7 @@ def cpu_baseline(pw: PackedWeight, x: torch.Tensor, budget_s: float = 12.0):
         "cores": torch.get_num_threads(),
         "kind": "port",
         "sample": (f"{rows} of {N} rows per call (dequantize packed->fp32 then F.linear, "
-                   f"median of {len(times)} calls); CPU: {platform.processor() or platform.machine()}, "
+                   f"median of {len(times)} calls); CPU: {cpu_model()}, "
                    f"os.cpu_count()={threads}"),
         "us_per_call_full_layer_est": med / frac * 1e6,
         "hard_quant_cached_fp32": {
@@ -277,12 +247,12 @@ def time_gpu_pack(w: torch.Tensor, pw: PackedWeight, reps: int = 3):
 
 def run_workload(name: str, steps: int, warmup: int, want_cpu: bool, check: bool = True,
                  warm: bool = False, cache: dict | None = None, pack_check: bool = False,
-                 packer: str = "host"):
+                 packer: str = "host", windows: int = 0, cpu_budget_s: float = 12.0):
     """cache: packed weights by (fmt, K, N, kind, rotation), reused across batch sizes (the
     weights are drawn before the activations, so they do not depend on the batch)."""
     fmt, K, N, B, kind, fwht = WORKLOADS[name]
     xdt = torch.float16 if fmt in ("gf4", "int4ref") else torch.bfloat16
-    w, x = synth(kind, N, K, B, xdt)
+    w, x = workloads.synth(kind, N, K, B, xdt)
     fb = fwht_block_for(K) if fwht else 0
     key = (fmt, K, N, kind, fb)
     t = time.perf_counter()
@@ -306,7 +276,7 @@ def run_workload(name: str, steps: int, warmup: int, want_cpu: bool, check: bool
     del w
     xd = x.to("cuda:0")
     y = torch.empty(B, N, dtype=xdt, device="cuda:0")
-    ms, ncp = time_gpu(pw, xd, y, steps, warmup, cold=True)
+    ms, ncp, extra = time_gpu(pw, xd, y, steps, warmup, cold=True, windows=windows)
     warm_calls = LAST_WARMUP_CALLS
     ms_warm = time_gpu(pw, xd, y, steps, warmup, cold=False)[0] if warm else None
     ms_graph = time_gpu_graph(pw, xd, y, min(steps, 200)) if warm else None
@@ -322,6 +292,8 @@ def run_workload(name: str, steps: int, warmup: int, want_cpu: bool, check: bool
         "us_per_call_graph": None if ms_graph is None else ms_graph * 1e3,
         "GBps_graph": None if ms_graph is None else nbytes / (ms_graph * 1e-3) / 1e9,
         "tokens_per_s_equiv": B / (ms * 1e-3), "pack_s": pack_s, "gpu_pack": gpu_pack,
+        "us_per_call_windows": [v * 1e3 for v in [ms] + extra],
+        "us_per_call_median": float(np.median([ms] + extra)) * 1e3,
     }
     if check:  # spot parity: sampled rows vs exact host decode + F.linear (fp32)
         yk = torch.empty(B, N, dtype=torch.float32, device="cuda:0")
@@ -337,8 +309,19 @@ def run_workload(name: str, steps: int, warmup: int, want_cpu: bool, check: bool
         rec["parity_ok"] = bool((err <= 1e-2 + 1e-3 * yref.abs()).all())
         rec["parity_max_abs_err"] = float(err.max())
     if want_cpu:
-        rec["cpu_baseline"] = cpu_baseline(pw, x)
+        rec["cpu_baseline"] = cpu_baseline(pw, x, cpu_budget_s)
     return rec, pw
+
+
+def cpu_model() -> str:
+    """The host CPU's model string (``/proc/cpuinfo``), for the CPU baseline record."""
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or platform.machine()
 
 
 def main():
@@ -397,7 +380,21 @@ def main():
                       f"parity {rec.get('parity_ok')}", file=sys.stderr, flush=True)
 
     rec, pw = run_workload(args.workload, args.steps, args.warmup, not args.no_cpu,
-                           warm=args.warm, pack_check=not args.no_pack_check, packer=args.packer)
+                           warm=args.warm, pack_check=not args.no_pack_check, packer=args.packer,
+                           windows=MEDIAN_WINDOWS)
+    del pw
+    torch.cuda.empty_cache()
+    cfg1 = None
+    if not args.no_cpu and args.workload != workloads.CPU_CONFIG:
+        # the configuration the reference's CPU path is quoted on, GPU and CPU side by side
+        r1, pw1 = run_workload(workloads.CPU_CONFIG, args.steps, args.warmup, True,
+                               windows=MEDIAN_WINDOWS, cpu_budget_s=8.0)
+        del pw1
+        cfg1 = {"workload": workloads.CPU_CONFIG, "gpu_us_per_call": r1["us_per_call"],
+                "gpu_us_per_call_median": r1["us_per_call_median"], "gpu_GBps": r1["GBps"],
+                "parity_ok": r1.get("parity_ok"),
+                "cpu": {k: v for k, v in r1["cpu_baseline"].items() if k != "hard_quant_cached_fp32"},
+                "cpu_hard_quant_cached_fp32": r1["cpu_baseline"]["hard_quant_cached_fp32"]}
     fmt, K, N, B = rec["fmt"], rec["K"], rec["N"], rec["B"]
     achieved = rec["GBps"]
     out = {
@@ -425,6 +422,10 @@ def main():
                        "call streams from HBM, not the 256 MiB Infinity Cache; warm-up of "
                        f"{rec['warmup_calls_run']} calls (at least --warmup and "
                        f"{MIN_WARM_S} s, past the GPU's clock ramp after idle)"),
+            "us_per_call_median": rec["us_per_call_median"],
+            "median_note": (f"median over {1 + MEDIAN_WINDOWS} timed regions of --steps calls "
+                            "(the first is the one value is computed from)"),
+            "us_per_call_regions": rec["us_per_call_windows"],
             "us_per_call_warm_single_copy": rec["us_per_call_warm"],
             "GBps_warm_single_copy": rec["GBps_warm"],
             "us_per_call_hipgraph_warm": rec["us_per_call_graph"],
@@ -433,10 +434,15 @@ def main():
             "pack_gpu": rec["gpu_pack"],
             "cpu_hard_quant_cached_fp32": (rec["cpu_baseline"] or {}).get("hard_quant_cached_fp32")
             if rec.get("cpu_baseline") else None,
+            "cpu_config1": cfg1,
         },
         "roofline": {
             "bound": "hbm", "achieved": achieved, "peak": PEAK_GBS, "unit": "GB/s",
             "frac": achieved / PEAK_GBS, "traffic": load_traffic(args.workload),
+            "traffic_source": (f"profiles/traffic_{args.workload}.json: rocprofv3 --pmc "
+                               "FETCH_SIZE + WRITE_SIZE per dispatch, each scaled by the same "
+                               "counter on a plain copy of known size; not measured in this run")
+            if load_traffic(args.workload) is not None else None,
         },
         "cpu_baseline": rec.get("cpu_baseline"),
     }

@@ -532,9 +532,12 @@ __global__ __launch_bounds__(NW * 64) void gemv_kernel(
       u = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
     return u;
   };
+  // Offsets are taken from this workgroup's first block, so a unit's offset stays below
+  // 2^31 (the host checks that a workgroup's blocks span less) whatever the layer's size.
+  const uint8_t* wbase = w + (int64_t)t0 * GS * BB;
   auto unit_off = [&](int s, int u) -> unsigned {
     const int lt = tile_of(u);
-    return (unsigned)(((int64_t)(t0 + lt) * GS + s * SPL + (u - lt * sp)) * BB);
+    return (unsigned)((lt * GS + s * SPL + (u - lt * sp)) * BB);
   };
 
   // Decode + MFMA of unit u (slice s) from record r; the unit's partial sums go to its own
@@ -559,7 +562,7 @@ __global__ __launch_bounds__(NW * 64) void gemv_kernel(
   Rec<FMT> ring[2];
   auto issue = [&](int s, int u, Rec<FMT>& r) {
     const bool real = u < nu;  // wave-uniform: only the range changes
-    const rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(w), (short)0,
+    const rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(wbase), (short)0,
                                                         real ? 0x7fffffff : 0, kRsrcWord3);
     load_rec<FMT>(rs, real ? unit_off(s, u) : 0u, lane, r);
   };
@@ -861,6 +864,15 @@ int fb_gemv(const void* wdev, const void* x, void* y, const fb_shape_t* s, void*
     return FB_ERR_ALIGN;
   if (s->fwht_block && s->x_dtype != FB_DT_F16) return FB_ERR_DTYPE;
   const int cus = device_cus();
+  {
+    // The kernel addresses a workgroup's blocks with 32-bit offsets from its first block,
+    // so the row tiles one workgroup owns (at most ceil(T / min(T, CUs))) must span less
+    // than 2^31 bytes.  Under fb_validate's limit of 2^31 groups (192 GiB of GF4 stream)
+    // this holds on every device with 128 CUs or more.
+    const int64_t T = (s->N + 15) / 16, GS = (s->K / 128 + 3) / 4;
+    const int64_t grid = std::min<int64_t>(T, cus);
+    if ((T + grid - 1) / grid * GS * fb::block_bytes(s->fmt) > INT32_MAX) return FB_ERR_SHAPE;
+  }
   hipStream_t hs = static_cast<hipStream_t>(stream);
   Plan pl;
   if (make_plan(s, cus, pl)) return launch_plan(wdev, x, y, s, pl, hs);

@@ -49,41 +49,146 @@ def fwht_block_for(K: int) -> int:
     return min(b, 4096)
 
 
+FP16_MAX = 65504.0
+# E8M0 scale bytes whose E2M1 products are all exact fp16 values: 0.5 * 2^(s-127) >= 2^-24
+# (the smallest fp16 subnormal) and 6 * 2^(s-127) <= 65504.
+E2M1_F16_SCALES = (104, 140)
+
+
+def e2m1_scales_fit_f16(meta: torch.Tensor) -> bool:
+    """Whether every E8M0 byte of an E2M1 weight lies in ``E2M1_F16_SCALES``, i.e. the
+    kernel's fp16 decode (fp16 activations) gives the exact weight values."""
+    if meta.numel() == 0:
+        return True
+    lo, hi = int(meta.min()), int(meta.max())
+    return E2M1_F16_SCALES[0] <= lo and hi <= E2M1_F16_SCALES[1]
+
+
+def _fwht_last_dim(t: torch.Tensor, block: int) -> torch.Tensor:
+    """Normalised blockwise Walsh-Hadamard transform along the last dim (fp32, on t's
+    device): every ``block``-wide slice becomes ``H_b v / sqrt(b)``, Sylvester order."""
+    lead = t.shape[:-1]
+    K = t.shape[-1]
+    v = t.reshape(-1, K // block, block).float()
+    h = 1
+    while h < block:
+        v = v.reshape(v.shape[0], v.shape[1], block // (2 * h), 2, h)
+        a, c = v[:, :, :, 0, :], v[:, :, :, 1, :]
+        v = torch.stack((a + c, a - c), dim=3)
+        h *= 2
+    return (v.reshape(*lead, K) / float(block) ** 0.5)
+
+
+def _gemv_chunks(wdev, N, kp, fmt, fwht_block, xk, y):
+    f = C.FMT_BY_NAME[fmt]
+    for b0 in range(0, xk.shape[0], MAX_GEMV_BATCH):
+        b1 = min(b0 + MAX_GEMV_BATCH, xk.shape[0])
+        shape = C.make_shape(N, kp, b1 - b0, f, fwht_block, C.DTYPE_CODE[xk.dtype],
+                             C.DTYPE_CODE[y.dtype])
+        C.gemv(wdev, xk[b0:b1], y[b0:b1], shape, C.new_workspace(shape, xk.device))
+
+
+def _kernel_input(x2: torch.Tensor, K: int, fmt: str, fwht_block: int, range_check: bool,
+                  f16_exact: bool) -> torch.Tensor:
+    """x [M, K] -> the kernel's activation: fp16 for GF4 and every rotation (E2M1 keeps
+    fp16 / bf16, fp32 becomes bf16), zero-padded to ``packed_k(K)``.  ``range_check``
+    raises where the fp16 staging would overflow: values beyond +-65504 in a wider x, and
+    for a rotation any block of L2 norm >= 65504 (a rotated value is at most its block's
+    norm).  It costs one reduction and a host sync per call."""
+    if fmt == "gf4" or fwht_block:
+        xk = x2.to(torch.float16)
+        if range_check and xk.numel():
+            if x2.dtype != torch.float16 and bool((torch.isfinite(x2) & ~torch.isfinite(xk)).any()):
+                raise ValueError("packed linear: activations beyond the fp16 range (+-65504); "
+                                 "the GF4 and rotated kernels take fp16 x")
+            if fwht_block:
+                nb = K // fwht_block
+                norm = xk.float().reshape(-1, nb, fwht_block).norm(dim=-1).max()
+                if bool(norm >= FP16_MAX):
+                    raise ValueError("packed linear: a rotation block of x has L2 norm >= 65504, "
+                                     "so its rotated values may overflow fp16")
+    else:
+        xk = x2 if x2.dtype in (torch.float16, torch.bfloat16) else x2.to(torch.bfloat16)
+    if fmt == "e2m1" and xk.dtype == torch.float16 and not f16_exact:
+        raise ValueError(f"packed linear: E2M1 scale bytes outside {E2M1_F16_SCALES} do not "
+                         "decode exactly to fp16; pass bfloat16 activations (without a "
+                         "rotation) for this weight")
+    kp = packed_k(K)
+    if kp != K:
+        xk = F.pad(xk, (0, kp - K))
+    return xk.contiguous()
+
+
+class _PackedLinearFn(torch.autograd.Function):
+    """``x -> x W^T`` through the fused kernel, differentiable in x (as ``F.linear`` with
+    the reference's frozen committed weight is, ``layers.py:34-35``).  Backward:
+    ``grad_x = grad_y W``, with W decoded on the device (fb_dequant, fp32) and, for a
+    rotated weight W' = W H, rotated back: ``grad_x = (grad_y W') H``."""
+
+    @staticmethod
+    def forward(ctx, x2, wdev, N, K, fmt, fwht_block, range_check, f16_exact):
+        xk = _kernel_input(x2, K, fmt, fwht_block, range_check, f16_exact)
+        ydt = x2.dtype if x2.dtype in C.DTYPE_CODE else torch.float32
+        y = torch.empty(x2.shape[0], N, dtype=ydt, device=x2.device)
+        _gemv_chunks(wdev, N, packed_k(K), fmt, fwht_block, xk, y)
+        ctx.save_for_backward(wdev)
+        ctx.cfg = (N, K, fmt, fwht_block, x2.dtype)
+        return y
+
+    @staticmethod
+    def backward(ctx, gy):
+        (wdev,) = ctx.saved_tensors
+        N, K, fmt, fwht_block, xdt = ctx.cfg
+        shape = C.make_shape(N, packed_k(K), 1, C.FMT_BY_NAME[fmt], fwht_block)
+        W = C.dequant_device(wdev, shape, torch.float32)
+        gx = gy.float() @ W
+        if fwht_block:
+            gx = _fwht_last_dim(gx, fwht_block)
+        return gx[:, :K].to(xdt), None, None, None, None, None, None, None
+
+
 def packed_linear(wdev: torch.Tensor, N: int, K: int, fmt: str, fwht_block: int,
-                  x: torch.Tensor, bias: torch.Tensor | None = None) -> torch.Tensor:
+                  x: torch.Tensor, bias: torch.Tensor | None = None, *,
+                  range_check: bool = True, f16_exact: bool = True) -> torch.Tensor:
     """``F.linear(x, W, bias)`` for a packed 4-bit ``W [N, K]`` (device stream ``wdev``
     of a ``packed_k(K)``-wide weight), through fb_gemv in chunks of 16 rows of x.
 
     x may have any leading shape and dtype: it is cast to fp16 (GF4, or any rotation) or
     kept in fp16/bf16 (E2M1; fp32 becomes bf16) and zero-padded to ``packed_k(K)``; y
-    has x's dtype (fp32 for other dtypes).  No CPU path: x must be on the GPU."""
+    has x's dtype (fp32 for other dtypes).  Differentiable in x (and bias): the weight is
+    frozen, as the reference's committed weight is.  ``range_check`` (see
+    ``_kernel_input``) raises instead of letting fp16 staging overflow; ``f16_exact``
+    (E2M1 only) says whether the weight's scales decode exactly to fp16.  No CPU path: x
+    must be on the GPU."""
     if x.dim() == 0 or x.shape[-1] != K:
         raise RuntimeError(f"packed linear: input of shape {tuple(x.shape)} does not end in "
                            f"in_features={K}")
     if not x.is_cuda:
         raise RuntimeError("the packed 4-bit linear runs the HIP kernel: move the module and "
                            "input to a ROCm GPU")
-    kp = packed_k(K)
     lead = x.shape[:-1]
     x2 = x.reshape(-1, K)
-    if fmt == "gf4" or fwht_block:
-        xk = x2.to(torch.float16)
-    else:
-        xk = x2 if x2.dtype in (torch.float16, torch.bfloat16) else x2.to(torch.bfloat16)
-    if kp != K:
-        xk = F.pad(xk, (0, kp - K))
-    xk = xk.contiguous()
-    ydt = x.dtype if x.dtype in C.DTYPE_CODE else torch.float32
-    y = torch.empty(x2.shape[0], N, dtype=ydt, device=x.device)
-    f = C.FMT_BY_NAME[fmt]
-    for b0 in range(0, x2.shape[0], MAX_GEMV_BATCH):
-        b1 = min(b0 + MAX_GEMV_BATCH, x2.shape[0])
-        shape = C.make_shape(N, kp, b1 - b0, f, fwht_block, C.DTYPE_CODE[xk.dtype],
-                             C.DTYPE_CODE[ydt])
-        C.gemv(wdev, xk[b0:b1], y[b0:b1], shape, C.new_workspace(shape, x.device))
+    if torch.is_grad_enabled() and x.requires_grad:
+        y = _PackedLinearFn.apply(x2, wdev, N, K, fmt, fwht_block, range_check, f16_exact)
+        if bias is not None:
+            y = y + bias.to(y.dtype)
+        return y.reshape(*lead, N)
+    with torch.no_grad():
+        y = _PackedLinearFn.forward(_NoCtx(), x2, wdev, N, K, fmt, fwht_block, range_check,
+                                    f16_exact)
     if bias is not None:
-        y.add_(bias.to(ydt))  # y is this call's own buffer
+        if torch.is_grad_enabled() and bias.requires_grad:
+            y = y + bias.to(y.dtype)
+        else:
+            y.add_(bias.to(y.dtype))  # y is this call's own buffer
     return y.reshape(*lead, N)
+
+
+class _NoCtx:
+    """Stand-in for the autograd context when no graph is built."""
+
+    def save_for_backward(self, *a):
+        pass
 
 
 class PackedWeight:
@@ -95,6 +200,7 @@ class PackedWeight:
         self.fmt_name = fmt
         self.N, self.K, self.fwht_block = N, K, fwht_block
         self.codes, self.meta = codes, meta
+        self.f16_exact = self.fmt != C.FMT_E2M1 or e2m1_scales_fit_f16(meta)
         self._ws = {}
         shape = C.make_shape(N, K, 1, self.fmt, fwht_block)
         self.wdev = C.to_device_layout(codes, meta, shape)
@@ -162,6 +268,9 @@ class PackedWeight:
              out_dtype: torch.dtype | None = None) -> torch.Tensor:
         """x [B,K] (B <= 16) on the GPU -> y [B,N]."""
         B = x.shape[0]
+        if x.dtype == torch.float16 and not self.f16_exact:
+            raise ValueError(f"E2M1 scale bytes outside {E2M1_F16_SCALES} do not decode "
+                             "exactly to fp16: use bfloat16 activations for this weight")
         ydt = out.dtype if out is not None else (out_dtype or x.dtype)
         if out is None:
             out = torch.empty(B, self.N, dtype=ydt, device=x.device)
@@ -216,6 +325,10 @@ class QuantLinear(nn.Linear):
              self.fwht_block], dtype=torch.int32))
         self.register_buffer("wdev", torch.empty(0, dtype=torch.uint8), persistent=False)
         self.hard_quant = False
+        # raise instead of letting fp16 activation staging overflow (one host sync per
+        # call for bf16 / fp32 inputs and for rotated layers); set False to skip
+        self.range_check = True
+        self._f16_exact = True
         self.register_load_state_dict_post_hook(QuantLinear._rebuild_after_load)
         if pack:
             self.quantize()
@@ -278,6 +391,7 @@ class QuantLinear(nn.Linear):
         self.codes = pw.codes.to(dev)
         self.meta = pw.meta.to(dev)
         self.wdev = pw.wdev.to(dev)
+        self._f16_exact = self.fmt != "e2m1" or e2m1_scales_fit_f16(pw.meta)
 
     def _shape(self, B=1, x_dtype=torch.float16, y_dtype=torch.float16) -> C.FbShape:
         return C.make_shape(self.out_features, self.k_pack, B, C.FMT_BY_NAME[self.fmt],
@@ -308,6 +422,7 @@ class QuantLinear(nn.Linear):
         shape = self._shape()
         self.wdev = C.to_device_layout(self.codes.cpu(), self.meta.cpu(), shape).to(
             self.codes.device)
+        self._f16_exact = self.fmt != "e2m1" or e2m1_scales_fit_f16(self.meta.cpu())
 
     # -- reference API ------------------------------------------------------------
     def dequantized_weight(self) -> torch.Tensor:
@@ -329,7 +444,8 @@ class QuantLinear(nn.Linear):
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         return packed_linear(self.wdev, self.out_features, self.in_features, self.fmt,
-                             self.fwht_block, x, self.bias)
+                             self.fwht_block, x, self.bias, range_check=self.range_check,
+                             f16_exact=self._f16_exact)
 
     def extra_repr(self) -> str:
         return (f"in_features={self.in_features}, out_features={self.out_features}, "

@@ -423,3 +423,58 @@ def test_bench_refuses_several_gpus():
                        capture_output=True, text=True, timeout=300)
     assert r.returncode != 0
     assert "one GPU" in (r.stdout + r.stderr)
+
+
+# ----------------------------------------------------------------------------- contract edges
+def test_workgroup_offsets_fit_32_bits():
+    """The GEMV addresses a workgroup's blocks with 32-bit offsets from its first block.
+    fb_validate caps a layer at 2^31 - 1 groups of 128 (96 bytes each in GF4, at most
+    192 GiB), so with one workgroup per CU a workgroup spans at most 192 GiB / CUs plus one
+    row tile (<= 192 MiB): less than 2^31 bytes on any device with 128 CUs or more (MI355X
+    has 256), whatever the layer's total size.  fb_gemv returns FB_ERR_SHAPE otherwise."""
+    groups = 2 ** 31 - 1
+    for K in (1 << 24, 1 << 20, 1 << 14, 128 * 3):
+        N = min(groups // (K // 128), 1 << 26)
+        sh = C.make_shape(N, K, 1)
+        assert C.lib().fb_validate(ctypes.byref(sh)) == 0
+        if N < (1 << 26):
+            sh_over = C.make_shape(N + 1, K, 1)
+            assert C.lib().fb_validate(ctypes.byref(sh_over)) == -2
+        for cus in (128, 256, 304):
+            T = (N + 15) // 16
+            GS = (K // 128 + 3) // 4
+            grid = min(T, cus)
+            assert -(-T // grid) * GS * 6144 < 2 ** 31, (K, cus)
+    # a stream past 2 GiB is a valid shape (the GPU test runs one)
+    big = C.make_shape(49152, 65536, 1)
+    assert C.device_bytes(big) > 2 ** 31
+
+
+def test_e2m1_fp16_exact_scale_range():
+    """E2M1 decodes to fp16 exactly when 0.5 * 2^(s-127) >= 2^-24 and 6 * 2^(s-127) <= 65504,
+    i.e. E8M0 bytes 104..140; PackedWeight records it from the packed scales."""
+    from if_i_could_turn_back_time_amd.linear import E2M1_F16_SCALES, e2m1_scales_fit_f16
+    lo, hi = E2M1_F16_SCALES
+    assert 0.5 * 2.0 ** (lo - 127) == 2.0 ** -24 and 0.5 * 2.0 ** (lo - 1 - 127) < 2.0 ** -24
+    assert 6 * 2.0 ** (hi - 127) <= 65504 < 6 * 2.0 ** (hi + 1 - 127)
+    for s, ok in ((0, False), (103, False), (104, True), (127, True), (140, True),
+                  (141, False), (255, False)):
+        meta = torch.full((2, 4), 127, dtype=torch.uint8)
+        meta[1, 2] = s
+        assert e2m1_scales_fit_f16(meta) == ok, s
+    w = torch.randn(16, 256) * 0.02
+    assert PackedWeight.quantize(w, "e2m1").f16_exact
+    w[3, :32] *= 2.0 ** 23                                  # amax ~ 2^18: byte >= 141
+    assert not PackedWeight.quantize(w, "e2m1").f16_exact
+
+
+@pytest.mark.parametrize("block", [2, 16, 256, 4096])
+def test_backward_fwht_matches_oracle(block):
+    """The device-side FWHT of the packed linear's backward (torch ops, any device) is
+    the oracle's normalised Sylvester transform."""
+    from if_i_could_turn_back_time_amd.linear import _fwht_last_dim
+    K = max(2 * block, 512)
+    t = torch.from_numpy(RNG.standard_normal((3, K)).astype(np.float32))
+    got = _fwht_last_dim(t, block)
+    ref = torch.from_numpy(O.fwht_rows(t.double().numpy(), block)).float()
+    assert torch.allclose(got, ref, atol=1e-5, rtol=1e-5)
