@@ -67,6 +67,17 @@ __device__ __forceinline__ int fdiv(int n, int d, unsigned m) {
   return (q + 1) * d <= n ? q + 1 : q;
 }
 
+// n / d for 0 <= n < 2^20 and 1 <= d < 2^20 through the fp32 reciprocal: the truncated
+// product is within one of the quotient, and two compares fix it.  Prologue code uses it
+// instead of integer division, which is a long scalar sequence that every wave of a
+// workgroup would run on the CU's one scalar unit.
+__device__ __forceinline__ int small_div(int n, int d) {
+  int q = (int)((float)n * __builtin_amdgcn_rcpf((float)d));
+  q -= q * d > n ? 1 : 0;
+  q += (q + 1) * d <= n ? 1 : 0;
+  return q;
+}
+
 // GF4 decode of one 32-bit word (8 codes, layout order) into 4 fp16 pairs in element
 // order (e0,e1) (e2,e3) (e4,e5) (e6,e7).  tl/th: lo/hi byte-plane tables
 // {A'[0..3], A'[4..7], B'[0..3], B'[4..7]}.
@@ -263,33 +274,39 @@ __device__ void stage_plain(uint8_t* lds, const XPre<XP>& xp, const uint16_t* __
 //    read back in 16 column groups, taken by the waves in turn; group c holds value
 //    e = (16c + l % 16) + 256 (r + 4 (l / 16)) in lane l, register r, so stages 8-9 are
 //    in-lane and stages 10-11 pair lanes l and l ^ 16, 32.
+//  - A lane-pair butterfly is one fma: v' = s v + o with o the partner's value and
+//    s = +1 in the lower lane (v + o), -1 in the upper one (o - v), the same roundings as
+//    the add and the subtract.
 // Staged positions k >= kw (up to the slice width) are zero.
 struct XRot {
   uint2 v[kXPre];
 };
 
-// The loads are unconditional (lanes past kw, and waves past the last sub-block, read
-// values that stage_fwht does not use), so the four are issued back to back and nothing
-// waits for them before stage_fwht.
+// Each wave loads its first kXPre sub-blocks through a buffer resource over x; a sub-block
+// past the last one, and lanes past kw, get an out-of-range offset, which returns zeros and
+// moves no data.  The loads are issued back to back with no branch, and nothing waits for
+// them before stage_fwht.
+constexpr unsigned kXOutOfRange = 0x7FFFFFF0u;
 template <int NW>
-__device__ __forceinline__ void rot_preload(XRot& xr, const uint16_t* __restrict__ x, int K,
-                                            int B, int k0, int kw, int tid) {
+__device__ __forceinline__ void rot_preload(XRot& xr, rsrc_t xrs, int K, int B, int k0, int kw,
+                                            int tid) {
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
   const int nsb = (kw + 255) >> 8;
 #pragma unroll
   for (int i = 0; i < kXPre; ++i) {
-    // flat sub-block index over (row, sub-block), uniform; past the last one the wave
-    // re-reads its first (the values are not used) so that no load is conditional
-    const int sb = wave + i * NW < B * nsb ? wave + i * NW : min(wave, B * nsb - 1);
-    const int b = sb / nsb;
+    const int sb = wave + i * NW;  // flat sub-block index over (row, sub-block), uniform
+    const int b = B == 1 ? 0 : small_div(sb, nsb);
     const int k = (sb - b * nsb) * 256 + lane * 4;
-    xr.v[i] = *reinterpret_cast<const uint2*>(x + (int64_t)b * K + k0 + (k < kw ? k : 0));
+    const unsigned off = sb < B * nsb && k < kw ? (unsigned)(b * K + k0 + k) * 2u : kXOutOfRange;
+    const auto v = __builtin_amdgcn_raw_buffer_load_b64(xrs, off, 0, 0);
+    xr.v[i] = uint2{(unsigned)v[0], (unsigned)v[1]};
   }
 }
 
-// v of lane ^ m for a compile-time m (after unrolling): m = 1, 2 by DPP quad permutes and
-// m = 4, 8 by DPP row shifts (one per direction, selected by the lane bit), all on the VALU;
-// m = 16 by ds_swizzle (xor within 32 lanes); m = 32 by ds_bpermute.
+// v of lane ^ m for a compile-time m (after unrolling), on the VALU for m <= 8: m = 1, 2 by a
+// DPP quad permute; m = 4 by a half-row mirror (l ^ 7) then a quad reversal (^ 3); m = 8 by a
+// row mirror (l ^ 15) then a half-row mirror (^ 7).  m = 16 by ds_swizzle (xor within 32
+// lanes); m = 32 by ds_bpermute.
 __device__ __forceinline__ float lane_xor(float v, int m, int lane) {
   const int iv = __builtin_bit_cast(int, v);
   int r;
@@ -298,13 +315,11 @@ __device__ __forceinline__ float lane_xor(float v, int m, int lane) {
   } else if (m == 2) {
     r = __builtin_amdgcn_update_dpp(0, iv, 0x4E, 0xF, 0xF, false);  // quad_perm [2,3,0,1]
   } else if (m == 4) {
-    const int up = __builtin_amdgcn_update_dpp(0, iv, 0x104, 0xF, 0xF, false);  // from lane + 4
-    const int dn = __builtin_amdgcn_update_dpp(0, iv, 0x114, 0xF, 0xF, false);  // from lane - 4
-    r = (lane & 4) ? dn : up;
+    r = __builtin_amdgcn_update_dpp(0, iv, 0x141, 0xF, 0xF, false);  // row_half_mirror
+    r = __builtin_amdgcn_update_dpp(0, r, 0x1B, 0xF, 0xF, false);    // quad_perm [3,2,1,0]
   } else if (m == 8) {
-    const int up = __builtin_amdgcn_update_dpp(0, iv, 0x108, 0xF, 0xF, false);  // from lane + 8
-    const int dn = __builtin_amdgcn_update_dpp(0, iv, 0x118, 0xF, 0xF, false);  // from lane - 8
-    r = (lane & 8) ? dn : up;
+    r = __builtin_amdgcn_update_dpp(0, iv, 0x140, 0xF, 0xF, false);  // row_mirror
+    r = __builtin_amdgcn_update_dpp(0, r, 0x141, 0xF, 0xF, false);   // row_half_mirror
   } else if (m == 16) {
     r = __builtin_amdgcn_ds_swizzle(iv, 0x401F);  // bitmask mode: xor 16 within 32 lanes
   } else {
@@ -318,24 +333,23 @@ __device__ __forceinline__ float lane_xor(float v, int m, int lane) {
 __host__ __device__ __forceinline__ int fpad(int p) { return p + (p >> 10) * 16; }
 
 template <int NW>
-__device__ void stage_fwht(uint8_t* lds, float* F, const XRot& xr, const uint16_t* __restrict__ x,
-                           int K, int B, int k0, int kw, int nsl, int RS, int fb, float sc,
-                           int tid) {
+__device__ void stage_fwht(uint8_t* lds, float* F, const XRot& xr, rsrc_t xrs, int K, int B,
+                           int k0, int kw, int nsl, int RS, int fb, float sc, int tid) {
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
   const int lg_fb = 31 - __builtin_clz(fb);
   const int nsb = (kw + 255) >> 8;  // 256-value sub-blocks per batch row
-  auto store_x = [&](int b, int k, float v) {
-    *(reinterpret_cast<_Float16*>(lds + b * RS + (k >> 7) * kSliceBytes) + (k & 127)) =
-        (_Float16)(v * sc);
-  };
   auto bfly = [&](float& lo, float& hi) {
     const float a = lo, c = hi;
     lo = a + c;
     hi = a - c;
   };
+  // per-stage butterfly signs: +1 in the lower lane of a pair, -1 in the upper one
+  float sgn[6];
+#pragma unroll
+  for (int st = 0; st < 6; ++st) sgn[st] = (lane & (1 << st)) ? -1.0f : 1.0f;
   int i = 0;
   for (int sb = wave; sb < B * nsb; sb += NW, ++i) {
-    const int b = sb / nsb;
+    const int b = B == 1 ? 0 : small_div(sb, nsb);
     const int k = (sb - b * nsb) * 256 + lane * 4;
     const bool live = k < kw;  // kw is a multiple of 128: whole lanes are in or out
     uint2 raw = {0u, 0u};
@@ -343,9 +357,10 @@ __device__ void stage_fwht(uint8_t* lds, float* F, const XRot& xr, const uint16_
 #pragma unroll
       for (int j = 0; j < kXPre; ++j)
         if (j == i) raw = xr.v[j];
-      if (!live) raw = uint2{0u, 0u};
-    } else if (live) {
-      raw = *reinterpret_cast<const uint2*>(x + (int64_t)b * K + k0 + k);
+    } else {
+      const auto v = __builtin_amdgcn_raw_buffer_load_b64(
+          xrs, live ? (unsigned)(b * K + k0 + k) * 2u : kXOutOfRange, 0, 0);
+      raw = uint2{(unsigned)v[0], (unsigned)v[1]};
     }
     const _Float16* h = reinterpret_cast<const _Float16*>(&raw);
     float v[4] = {(float)h[0], (float)h[1], (float)h[2], (float)h[3]};
@@ -360,19 +375,17 @@ __device__ void stage_fwht(uint8_t* lds, float* F, const XRot& xr, const uint16_
 #pragma unroll
     for (int st = 0; st < 6; ++st) {
       if (st + 2 < lg_fb) {  // uniform
-        const int m = 1 << st;
-        const bool upper = (lane & m) != 0;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const float o = lane_xor(v[e], m, lane);
-          v[e] = upper ? o - v[e] : v[e] + o;
-        }
+        for (int e = 0; e < 4; ++e) v[e] = __builtin_fmaf(sgn[st], v[e], lane_xor(v[e], 1 << st, lane));
       }
     }
     if (!live) continue;
     if (lg_fb <= 8) {
-#pragma unroll
-      for (int e = 0; e < 4; ++e) store_x(b, k + e, v[e]);
+      // four consecutive values of one 128-group: one 8-byte store
+      typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
+      const half4_t hv = {(_Float16)(v[0] * sc), (_Float16)(v[1] * sc), (_Float16)(v[2] * sc),
+                          (_Float16)(v[3] * sc)};
+      *reinterpret_cast<half4_t*>(lds + b * RS + (k >> 7) * kSliceBytes + (k & 127) * 2) = hv;
     } else {
       const int p = b * kw + k;
       *reinterpret_cast<f32x4*>(F + fpad(p)) = f32x4{v[0], v[1], v[2], v[3]};
@@ -383,6 +396,8 @@ __device__ void stage_fwht(uint8_t* lds, float* F, const XRot& xr, const uint16_
     const int total = B * kw;
     const float inv_kw = 1.0f / (float)kw;
     const int npieces = ((total + 4095) >> 12) << 4;  // (4096-value piece, column group)
+    // With kw a multiple of 4096 a piece lies in one batch row, found once per piece.
+    const bool whole = (kw & 4095) == 0;
     for (int piece = wave; piece < npieces; piece += NW) {
       const int base = (piece >> 4) * 4096 + (piece & 15) * 16;
       float v[4];
@@ -403,23 +418,29 @@ __device__ void stage_fwht(uint8_t* lds, float* F, const XRot& xr, const uint16_
 #pragma unroll
       for (int st = 0; st < 2; ++st) {
         if (st + 10 < lg_fb) {  // uniform
-          const int m = 16 << st;
-          const bool upper = (lane & m) != 0;
 #pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const float o = lane_xor(v[r], m, lane);
-            v[r] = upper ? o - v[r] : v[r] + o;
-          }
+          for (int r = 0; r < 4; ++r) v[r] = __builtin_fmaf(sgn[4 + st], v[r], lane_xor(v[r], 16 << st, lane));
         }
       }
+      auto store_x = [&](int bb, int k, float val) {
+        *(reinterpret_cast<_Float16*>(lds + bb * RS + (k >> 7) * kSliceBytes) + (k & 127)) =
+            (_Float16)(val * sc);
+      };
+      if (whole) {
+        const int bb = ((piece >> 4) * 4096) / kw;  // uniform
+        const int kofs = bb * kw;
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        if (e[r] < total) {
-          // e < 16 * kw < 2^24: the float quotient is within one of e / kw
-          int b = (int)((float)e[r] * inv_kw);
-          b -= b * kw > e[r] ? 1 : 0;
-          b += (b + 1) * kw <= e[r] ? 1 : 0;
-          store_x(b, e[r] - b * kw, v[r]);
+        for (int r = 0; r < 4; ++r) store_x(bb, e[r] - kofs, v[r]);  // total: whole pieces
+      } else {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          if (e[r] < total) {
+            // e < 16 * kw < 2^24: the float quotient is within one of e / kw
+            int bb = (int)((float)e[r] * inv_kw);
+            bb -= bb * kw > e[r] ? 1 : 0;
+            bb += (bb + 1) * kw <= e[r] ? 1 : 0;
+            store_x(bb, e[r] - bb * kw, v[r]);
+          }
         }
       }
     }
@@ -471,10 +492,10 @@ __device__ __forceinline__ f32x4 unit_partial(const Rec<FMT>& r, const uint8_t* 
 // ---------------------------------------------------------------------------------
 // The GEMV kernel
 // ---------------------------------------------------------------------------------
-// The first 14 argument dwords arrive preloaded in SGPRs and hold everything but the
+// The first 15 argument dwords arrive preloaded in SGPRs and hold everything but the
 // output; y, N and ydt come through a scalar load that completes long before the epilogue
-// needs them (the LDS size of staged x and the rotation scale are derived in the kernel, so
-// nothing early waits for that load).  tq, tr: row tiles per workgroup = tq (+1 for the
+// needs them (the LDS size of staged x is derived in the kernel, and the rotation scale is
+// an argument, so nothing early waits for that load).  tq, tr: row tiles per workgroup = tq (+1 for the
 // first tr workgroups); GS: 512-element spans per row; RS: LDS bytes per staged x row;
 // spl_m: div_magic(SPL).
 // MODE: kFlat = one K-slice, no rotation (the common case); kSliced = several K-slices, no
@@ -487,11 +508,10 @@ enum { kFlat = 0, kSliced = 1, kRotated = 2 };
 template <int FMT, int XDT, int MODE, int NW, int XP>
 __global__ __launch_bounds__(NW * 64) void gemv_kernel(
     const uint8_t* __restrict__ w, const void* __restrict__ x, int K, int B, int SPL, int GS,
-    int tq, int tr, unsigned spl_m, int S, int fwht_block, int RS, void* __restrict__ y, int N,
-    int ydt) {
+    int tq, int tr, unsigned spl_m, int S, int fwht_block, int RS, float fwht_scale,
+    void* __restrict__ y, int N, int ydt) {
   extern __shared__ __align__(16) uint8_t lds[];
   const int xbytes = x_lds_bytes(B, K, SPL, fwht_block);  // staged x; the slots follow
-  const float fwht_scale = MODE == kRotated ? 1.0f / __builtin_sqrtf((float)fwht_block) : 1.0f;
   constexpr int BB = FMT == FB_FMT_GF4 ? fb::kGf4BlockBytes : fb::kE2m1BlockBytes;
   constexpr int NT = NW * 64;
   const int g = blockIdx.x;
@@ -567,6 +587,9 @@ __global__ __launch_bounds__(NW * 64) void gemv_kernel(
     load_rec<FMT>(rs, real ? unit_off(s, u) : 0u, lane, r);
   };
   const uint16_t* xg = static_cast<const uint16_t*>(x);
+  // x through a buffer resource for the rotation's loads (out-of-range offsets read zeros)
+  const rsrc_t xrs = __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(x), (short)0, B * K * 2,
+                                                       kRsrcWord3);
   // Each wave's first two units are static (wave, wave + NW); the counter hands out
   // the rest.
   constexpr bool rot = MODE == kRotated;
@@ -585,7 +608,7 @@ __global__ __launch_bounds__(NW * 64) void gemv_kernel(
     XPre<XP> xp;
     XRot xr;
     if constexpr (rot)
-      rot_preload<NW>(xr, xg, K, B, k0, kw, tid);
+      rot_preload<NW>(xr, xrs, K, B, k0, kw, tid);
     else
       x_preload<NT, XP>(xp, xg, K, k0, per_row, B * per_row, row_of, tid);
     if constexpr (MODE != kFlat) {
@@ -611,7 +634,7 @@ __global__ __launch_bounds__(NW * 64) void gemv_kernel(
       if (threadIdx.x < 16) reinterpret_cast<u32x4*>(zeros)[threadIdx.x] = u32x4{0u, 0u, 0u, 0u};
     }
     if constexpr (rot)
-      stage_fwht<NW>(xst, reinterpret_cast<float*>(xst + B * RS), xr, xg, K, B, k0, kw, nsl, RS,
+      stage_fwht<NW>(xst, reinterpret_cast<float*>(xst + B * RS), xr, xrs, K, B, k0, kw, nsl, RS,
                  fwht_block, fwht_scale, tid);
     else
       stage_plain<NT, XP>(xst, xp, xg, K, B, k0, nsl, RS, row_of, tid);
@@ -738,6 +761,10 @@ struct Plan {
   size_t lds = 0;
 };
 
+// The rotation's normalisation 1 / sqrt(b), rounded as fp32 (correctly rounded sqrt and
+// division, so the same value the device would compute).
+float fwht_scale(int fb) { return fb ? 1.0f / std::sqrt((float)fb) : 1.0f; }
+
 // Multiplier of fdiv: floor(2^32 / d), or 2^32 - 1 for d = 1.
 unsigned div_magic(int d) { return d == 1 ? 0xFFFFFFFFu : (unsigned)((1ull << 32) / (unsigned)d); }
 
@@ -811,7 +838,8 @@ int launch_gemv(const void* wdev, const void* x, void* y, const fb_shape_t* s, c
   }
   hipLaunchKernelGGL(kern, dim3(pl.grid), dim3(NW * 64), pl.lds, stream,
                      static_cast<const uint8_t*>(wdev), x, s->K, s->B, pl.SPL, pl.GS, pl.tq,
-                     pl.tr, div_magic(pl.SPL), pl.S, s->fwht_block, x_row_stride(pl.SPL * 4), y,
+                     pl.tr, div_magic(pl.SPL), pl.S, s->fwht_block, x_row_stride(pl.SPL * 4),
+                     fwht_scale(s->fwht_block), y,
                      s->N, s->y_dtype);
   return hipGetLastError() == hipSuccess ? FB_OK : FB_ERR_HIP;
 }
