@@ -7,7 +7,9 @@ C ABI of ``libfourbit.so`` (``include/fourbit.h``).
 from .linear import (PackedWeight, QuantLinear, fwht_block_for, packed_k,  # noqa: F401
                      packed_linear, quantize_module)
 from .brecq import adaround_levels, pack_quantized_linears, replace_forward  # noqa: F401
+from .jenks import bias_mask, jenks2, linear_mask  # noqa: F401
 from . import _capi  # noqa: F401
 
 __all__ = ["PackedWeight", "QuantLinear", "fwht_block_for", "packed_k", "packed_linear",
-           "quantize_module", "adaround_levels", "pack_quantized_linears", "replace_forward"]
+           "quantize_module", "adaround_levels", "pack_quantized_linears", "replace_forward",
+           "jenks2", "linear_mask", "bias_mask"]

@@ -33,7 +33,7 @@ EXPORTED = (
     "fb_quantize_gf4", "fb_quantize_gf4_masked", "fb_pack_levels_gf4", "fb_quantize_e2m1",
     "fb_fwht_rows_f32", "fb_to_device",
     "fb_from_device", "fb_dequant_host", "fb_gemv", "fb_dequant", "fb_quantize_gf4_gpu",
-    "fb_quantize_e2m1_gpu",
+    "fb_quantize_e2m1_gpu", "fb_jenks2_host", "fb_jenks2_workspace", "fb_jenks2_gpu",
 )
 
 
@@ -75,6 +75,9 @@ def lib() -> ctypes.CDLL:
         "fb_dequant": (ctypes.c_int, [vp, vp, i32, sp, vp]),
         "fb_quantize_gf4_gpu": (ctypes.c_int, [vp, vp, i32, i32, vp, vp, vp]),
         "fb_quantize_e2m1_gpu": (ctypes.c_int, [vp, i32, i32, vp, vp, vp]),
+        "fb_jenks2_host": (ctypes.c_int, [vp, ctypes.c_int64, vp, vp, vp]),
+        "fb_jenks2_workspace": (ctypes.c_int, [ctypes.c_int64, ctypes.POINTER(sz)]),
+        "fb_jenks2_gpu": (ctypes.c_int, [vp, ctypes.c_int64, vp, vp, vp, vp, sz, vp]),
     }
     for name, (res, args) in sigs.items():
         fn = getattr(L, name)
@@ -302,3 +305,39 @@ def quantize_e2m1_gpu(w: torch.Tensor):
         check(lib().fb_quantize_e2m1_gpu(_ptr(w), N, K, _ptr(codes), _ptr(scales),
                                          _stream(w.device)))
     return codes, scales
+
+
+# ------------------------------------------------------------------ two-class Jenks
+def jenks2_host(w: torch.Tensor):
+    """fb_jenks2_host over the flattened fp32 values: (keep bool [n], split, gvf)."""
+    w = _host_contig(w.reshape(-1), torch.float32)
+    n = w.numel()
+    keep = torch.empty(n, dtype=torch.uint8)
+    split = ctypes.c_int64(0)
+    gvf = ctypes.c_double(0.0)
+    check(lib().fb_jenks2_host(_ptr(w), n, _ptr(keep), ctypes.byref(split), ctypes.byref(gvf)))
+    return keep.bool(), split.value, gvf.value
+
+
+def jenks2_gpu(w: torch.Tensor):
+    """fb_jenks2_gpu over the flattened fp32 values of a device tensor: (keep bool [n] on
+    the device, split, gvf).  Raises on non-finite values (one torch reduction first)."""
+    if not w.is_cuda:
+        raise RuntimeError("fb_jenks2_gpu needs a device tensor (ROCm GPU)")
+    w = w.detach().reshape(-1).to(torch.float32).contiguous()
+    n = w.numel()
+    if not bool(torch.isfinite(w).all()):
+        raise RuntimeError(strerror(ERR_VALUE))
+    with torch.cuda.device(w.device):
+        need = ctypes.c_size_t(0)
+        check(lib().fb_jenks2_workspace(n, ctypes.byref(need)))
+        ws = torch.empty(need.value + 256, dtype=torch.uint8, device=w.device)
+        off = (-ws.data_ptr()) % 256
+        keep = torch.empty(n, dtype=torch.uint8, device=w.device)
+        out = torch.empty(2, dtype=torch.float64, device=w.device)   # [split (int64 bits), gvf]
+        split_p = out.data_ptr()
+        check(lib().fb_jenks2_gpu(_ptr(w), n, _ptr(keep), split_p, split_p + 8,
+                                  ws.data_ptr() + off, need.value, _stream(w.device)))
+        host = out.cpu()
+    split = int(host[:1].view(torch.int64).item())
+    return keep.bool(), split, float(host[1].item())

@@ -62,16 +62,20 @@ def build(verbose: bool = False) -> Path:
     host_o = BUILD / "fourbit_host.o"
     gemv_o = BUILD / "fourbit_gemv.o"
     pack_o = BUILD / "fourbit_pack.o"
+    jenks2_o = BUILD / "fourbit_jenks2.o"
     steps = [
         ["g++", *HOST_FLAGS, *inc, "-c", str(CSRC / "fourbit_host.cpp"), "-o", str(host_o)],
         [_hipcc(), *HIP_FLAGS, *inc, "-c", str(CSRC / "fourbit_gemv.hip"), "-o", str(gemv_o)],
         # the GPU packer must round every fp64 operation as the host packer does
         [_hipcc(), *HIP_FLAGS, "-ffp-contract=off", *inc, "-c", str(CSRC / "fourbit_pack.hip"),
          "-o", str(pack_o)],
+        # the two-class Jenks rounds every fp64 operation as its host twin does
+        [_hipcc(), *HIP_FLAGS, "-ffp-contract=off", *inc, "-c", str(CSRC / "fourbit_jenks2.hip"),
+         "-o", str(jenks2_o)],
     ]
     tmp = LIB.with_suffix(".so.tmp")
     steps.append([_hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", str(host_o), str(gemv_o),
-                  str(pack_o), "-o", str(tmp), "-lpthread"])
+                  str(pack_o), str(jenks2_o), "-o", str(tmp), "-lpthread"])
     for cmd in steps:
         if verbose:
             print(" ".join(cmd), flush=True)

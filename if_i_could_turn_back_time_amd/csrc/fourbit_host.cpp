@@ -496,4 +496,85 @@ int fb_dequant_host(const uint8_t* codes, const void* meta, float* w_out, const 
   return FB_OK;
 }
 
+// Two-class natural breaks over a whole array (the reference's Linear_Mask / Bias_Mask,
+// cuda_helpers.py:378-411): the same arithmetic, in the same association order, as
+// fb_jenks2_gpu (fourbit_jenks2.hip), so the two give the same split, GVF and mask bits.
+int fb_jenks2_host(const float* w, int64_t n, uint8_t* keep, int64_t* split, double* gvf) {
+  if (!w || !keep || !split || !gvf) return FB_ERR_NULL;
+  if (n < 1 || n > INT32_MAX) return FB_ERR_SHAPE;
+  for (int64_t t = 0; t < n; ++t)
+    if (!std::isfinite(w[t])) return FB_ERR_VALUE;
+  constexpr int64_t kBlk = 256, kSup = 256;
+  std::vector<int> order((size_t)n);
+  std::iota(order.begin(), order.end(), 0);
+  // ascending, stable by index; -0.0 == +0.0 under <
+  std::stable_sort(order.begin(), order.end(), [&](int a, int b) { return w[a] < w[b]; });
+  std::vector<float> srt((size_t)n);
+  for (int64_t t = 0; t < n; ++t) srt[t] = w[order[t]];
+  const double c = (double)srt[n / 2];
+  const int64_t nblk = (n + kBlk - 1) / kBlk, nsup = (nblk + kSup - 1) / kSup;
+  std::vector<double> t1(nblk), t2(nblk), bx1(nblk), bx2(nblk), sx1(nsup + 1), sx2(nsup + 1);
+  for (int64_t b = 0; b < nblk; ++b) {
+    double a1 = 0.0, a2 = 0.0;
+    for (int64_t i = b * kBlk; i < std::min(n, b * kBlk + kBlk); ++i) {
+      const double d = (double)srt[i] - c;
+      const double q = d * d;
+      a1 = a1 + d;
+      a2 = a2 + q;
+    }
+    t1[b] = a1;
+    t2[b] = a2;
+  }
+  std::vector<double> u1(nsup), u2(nsup);
+  for (int64_t s = 0; s < nsup; ++s) {
+    double a1 = 0.0, a2 = 0.0;
+    for (int64_t b = s * kSup; b < std::min(nblk, s * kSup + kSup); ++b) {
+      bx1[b] = a1;
+      bx2[b] = a2;
+      a1 = a1 + t1[b];
+      a2 = a2 + t2[b];
+    }
+    u1[s] = a1;
+    u2[s] = a2;
+  }
+  {
+    double a1 = 0.0, a2 = 0.0;
+    for (int64_t s = 0; s < nsup; ++s) {
+      sx1[s] = a1;
+      sx2[s] = a2;
+      a1 = a1 + u1[s];
+      a2 = a2 + u2[s];
+    }
+    sx1[nsup] = a1;
+    sx2[nsup] = a2;
+  }
+  const double pt = sx1[nsup], qt = sx2[nsup];
+  double best = 0.0, ssd0 = 0.0;
+  int64_t arg = -1;
+  for (int64_t b = 0; b < nblk; ++b) {
+    const double base1 = sx1[b / kSup] + bx1[b], base2 = sx2[b / kSup] + bx2[b];
+    double l1 = 0.0, l2 = 0.0;
+    for (int64_t i = b * kBlk; i < std::min(n, b * kBlk + kBlk); ++i) {
+      const double p = base1 + l1, q = base2 + l2;
+      const double left = i == 0 ? 0.0 : q - (p * p) / (double)i;
+      const double rp = pt - p;
+      const double right = (qt - q) - (rp * rp) / (double)(n - i);
+      const double v = left + right;
+      if (arg < 0 || v < best) {
+        best = v;
+        arg = i;
+      }
+      if (i == 0) ssd0 = v;
+      const double d = (double)srt[i] - c;
+      const double dq = d * d;
+      l1 = l1 + d;
+      l2 = l2 + dq;
+    }
+  }
+  for (int64_t t = 0; t < n; ++t) keep[order[t]] = t >= arg ? 1 : 0;
+  *split = arg;
+  *gvf = (ssd0 - best) / (ssd0 + 1e-8);
+  return FB_OK;
+}
+
 }  // extern "C"

@@ -1,0 +1,289 @@
+// Two-class natural breaks (k = 2 Jenks) over a whole array on the GPU, in O(n) after the
+// sort: the reference's weight/bias pruning rule (Linear_Mask / Bias_Mask,
+// Python_Jenks_Test/Jenks_Tests/cuda_helpers.py:378-411, kernels :85-118 and :151-184,
+// also CUDA_C_Code/include/layers.h:2424-2560).  The reference launches one thread per split
+// index, each summing both classes serially (O(n^2)); here the classes' sums come from
+// prefix sums, so every split costs a few operations.
+//
+// Rule (shared with fb_jenks2_host, which computes the same bits on the CPU):
+//  1. Sort the values ascending, stable by index (-0.0 and +0.0 are equal).
+//  2. c = sorted[n / 2]; d_t = sorted[t] - c and q_t = d_t * d_t in fp64 (the SSD is
+//     invariant to the shift; centering keeps the prefix sums free of cancellation).
+//  3. Prefix sums of d and q in a fixed association order: sequential within blocks of
+//     256 elements (Lx, exclusive), block totals sequential within superblocks of 256
+//     blocks (Bx, exclusive), superblock totals sequential (Sx, exclusive, Sx[S] = total);
+//     P(i) = (Sx[s] + Bx[b]) + Lx(i).
+//  4. For every split i in [0, n): ssd(i) = [i ? Q(i) - P(i)^2 / i : 0]
+//     + [(Qt - Q(i)) - (Pt - P(i))^2 / (n - i)]; split 0 is "no split".
+//  5. split = the first index of the minimum; the elements at sorted positions >= split
+//     are kept; GVF = (ssd(0) - ssd(split)) / (ssd(0) + 1e-8).
+// The file is compiled with -ffp-contract=off so no multiply-add is fused: every fp64
+// operation rounds as the host's does.
+#include <hip/hip_runtime.h>
+#include <hipcub/hipcub.hpp>
+
+#include <cstdint>
+
+#include "fourbit.h"
+
+namespace {
+
+constexpr int kBlk = 256;  // elements per block (sequential local sums)
+constexpr int kSup = 256;  // blocks per superblock
+
+struct J2Layout {
+  int64_t n, nblk, nsup;
+  size_t sort_bytes;
+  size_t off_keys_in, off_keys_out, off_vals_in, off_vals_out, off_sort;
+  size_t off_t1, off_t2, off_bx1, off_bx2, off_u1, off_u2, off_sx1, off_sx2;
+  size_t off_bmin, off_bidx, off_smin, off_sidx, off_ssd0, total;
+};
+
+size_t align256(size_t v) { return (v + 255) & ~size_t(255); }
+
+int j2_layout(int64_t n, J2Layout& L) {
+  L.n = n;
+  L.nblk = (n + kBlk - 1) / kBlk;
+  L.nsup = (L.nblk + kSup - 1) / kSup;
+  size_t sort_bytes = 0;
+  if (hipcub::DeviceRadixSort::SortPairs(nullptr, sort_bytes, (const float*)nullptr,
+                                         (float*)nullptr, (const int*)nullptr, (int*)nullptr,
+                                         (int)n, 0, 32, (hipStream_t)0) != hipSuccess)
+    return FB_ERR_HIP;
+  L.sort_bytes = sort_bytes;
+  size_t o = 0;
+  auto take = [&](size_t bytes) {
+    const size_t at = o;
+    o = align256(o + bytes);
+    return at;
+  };
+  L.off_keys_in = take(4 * (size_t)n);
+  L.off_keys_out = take(4 * (size_t)n);
+  L.off_vals_in = take(4 * (size_t)n);
+  L.off_vals_out = take(4 * (size_t)n);
+  L.off_sort = take(sort_bytes);
+  L.off_t1 = take(8 * (size_t)L.nblk);
+  L.off_t2 = take(8 * (size_t)L.nblk);
+  L.off_bx1 = take(8 * (size_t)L.nblk);
+  L.off_bx2 = take(8 * (size_t)L.nblk);
+  L.off_u1 = take(8 * (size_t)L.nsup);
+  L.off_u2 = take(8 * (size_t)L.nsup);
+  L.off_sx1 = take(8 * (size_t)(L.nsup + 1));
+  L.off_sx2 = take(8 * (size_t)(L.nsup + 1));
+  L.off_bmin = take(8 * (size_t)L.nblk);
+  L.off_bidx = take(4 * (size_t)L.nblk);
+  L.off_smin = take(8 * (size_t)L.nsup);
+  L.off_sidx = take(4 * (size_t)L.nsup);
+  L.off_ssd0 = take(8);
+  L.total = o;
+  return FB_OK;
+}
+
+// keys: the values with -0.0 made +0.0 (so the radix order treats them as equal and the
+// sort keeps their index order); payload: the index.
+__global__ void j2_prep(const float* __restrict__ w, float* __restrict__ keys,
+                        int* __restrict__ vals, int n) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) {
+    const float v = w[i];
+    keys[i] = v == 0.0f ? 0.0f : v;
+    vals[i] = i;
+  }
+}
+
+__device__ __forceinline__ double centre(const float* __restrict__ s, int n) {
+  return (double)s[n / 2];
+}
+
+// Block totals of d and q: one thread per block of kBlk sorted values.
+__global__ void j2_block_totals(const float* __restrict__ s, int n, int nblk,
+                                double* __restrict__ t1, double* __restrict__ t2) {
+  const int b = blockIdx.x * blockDim.x + threadIdx.x;
+  if (b >= nblk) return;
+  const double c = centre(s, n);
+  const int i0 = b * kBlk, i1 = min(n, i0 + kBlk);
+  double a1 = 0.0, a2 = 0.0;
+  for (int i = i0; i < i1; ++i) {
+    const double d = (double)s[i] - c;
+    const double q = d * d;
+    a1 = a1 + d;
+    a2 = a2 + q;
+  }
+  t1[b] = a1;
+  t2[b] = a2;
+}
+
+// Exclusive block prefixes within each superblock and the superblock totals.
+__global__ void j2_super(const double* __restrict__ t1, const double* __restrict__ t2, int nblk,
+                         int nsup, double* __restrict__ bx1, double* __restrict__ bx2,
+                         double* __restrict__ u1, double* __restrict__ u2) {
+  const int s = blockIdx.x * blockDim.x + threadIdx.x;
+  if (s >= nsup) return;
+  const int b0 = s * kSup, b1 = min(nblk, b0 + kSup);
+  double a1 = 0.0, a2 = 0.0;
+  for (int b = b0; b < b1; ++b) {
+    bx1[b] = a1;
+    bx2[b] = a2;
+    a1 = a1 + t1[b];
+    a2 = a2 + t2[b];
+  }
+  u1[s] = a1;
+  u2[s] = a2;
+}
+
+// Exclusive superblock prefixes; sx[nsup] is the total.  One thread.
+__global__ void j2_top(const double* __restrict__ u1, const double* __restrict__ u2, int nsup,
+                       double* __restrict__ sx1, double* __restrict__ sx2) {
+  if (blockIdx.x != 0 || threadIdx.x != 0) return;
+  double a1 = 0.0, a2 = 0.0;
+  for (int s = 0; s < nsup; ++s) {
+    sx1[s] = a1;
+    sx2[s] = a2;
+    a1 = a1 + u1[s];
+    a2 = a2 + u2[s];
+  }
+  sx1[nsup] = a1;
+  sx2[nsup] = a2;
+}
+
+// The SSD of every split of one block, and the block's first minimum.
+__global__ void j2_ssd(const float* __restrict__ s, int n, int nblk, int nsup,
+                       const double* __restrict__ bx1, const double* __restrict__ bx2,
+                       const double* __restrict__ sx1, const double* __restrict__ sx2,
+                       double* __restrict__ bmin, int* __restrict__ bidx,
+                       double* __restrict__ ssd0) {
+  const int b = blockIdx.x * blockDim.x + threadIdx.x;
+  if (b >= nblk) return;
+  const double c = centre(s, n);
+  const int sup = b / kSup;
+  const double base1 = sx1[sup] + bx1[b], base2 = sx2[sup] + bx2[b];
+  const double pt = sx1[nsup], qt = sx2[nsup];
+  const int i0 = b * kBlk, i1 = min(n, i0 + kBlk);
+  double l1 = 0.0, l2 = 0.0;
+  double best = 0.0;
+  int arg = -1;
+  for (int i = i0; i < i1; ++i) {
+    const double p = base1 + l1, q = base2 + l2;
+    const double left = i == 0 ? 0.0 : q - (p * p) / (double)i;
+    const double rp = pt - p;
+    const double right = (qt - q) - (rp * rp) / (double)(n - i);
+    const double v = left + right;
+    if (arg < 0 || v < best) {
+      best = v;
+      arg = i;
+    }
+    if (i == 0) *ssd0 = v;
+    const double d = (double)s[i] - c;
+    const double dq = d * d;
+    l1 = l1 + d;
+    l2 = l2 + dq;
+  }
+  bmin[b] = best;
+  bidx[b] = arg;
+}
+
+// First minimum over the blocks of each superblock.
+__global__ void j2_min_super(const double* __restrict__ bmin, const int* __restrict__ bidx,
+                             int nblk, int nsup, double* __restrict__ smin,
+                             int* __restrict__ sidx) {
+  const int s = blockIdx.x * blockDim.x + threadIdx.x;
+  if (s >= nsup) return;
+  const int b0 = s * kSup, b1 = min(nblk, b0 + kSup);
+  double best = bmin[b0];
+  int arg = bidx[b0];
+  for (int b = b0 + 1; b < b1; ++b)
+    if (bmin[b] < best) {
+      best = bmin[b];
+      arg = bidx[b];
+    }
+  smin[s] = best;
+  sidx[s] = arg;
+}
+
+__global__ void j2_final(const double* __restrict__ smin, const int* __restrict__ sidx, int nsup,
+                         const double* __restrict__ ssd0, int64_t* __restrict__ split,
+                         double* __restrict__ gvf) {
+  if (blockIdx.x != 0 || threadIdx.x != 0) return;
+  double best = smin[0];
+  int arg = sidx[0];
+  for (int s = 1; s < nsup; ++s)
+    if (smin[s] < best) {
+      best = smin[s];
+      arg = sidx[s];
+    }
+  *split = arg;
+  const double t = *ssd0;
+  *gvf = (t - best) / (t + 1e-8);
+}
+
+// keep[index of sorted position t] = t >= split
+__global__ void j2_mask(const int* __restrict__ order, int n, const int64_t* __restrict__ split,
+                        uint8_t* __restrict__ keep) {
+  const int t = blockIdx.x * blockDim.x + threadIdx.x;
+  if (t < n) keep[order[t]] = (int64_t)t >= *split ? 1 : 0;
+}
+
+int grid_of(int64_t items, int threads) { return (int)((items + threads - 1) / threads); }
+
+}  // namespace
+
+extern "C" {
+
+int fb_jenks2_workspace(int64_t n, size_t* bytes) {
+  if (!bytes) return FB_ERR_NULL;
+  if (n < 1 || n > INT32_MAX) return FB_ERR_SHAPE;
+  J2Layout L;
+  const int st = j2_layout(n, L);
+  if (st != FB_OK) return st;
+  *bytes = L.total;
+  return FB_OK;
+}
+
+int fb_jenks2_gpu(const float* w, int64_t n, uint8_t* keep, int64_t* split, double* gvf,
+                  void* ws, size_t ws_bytes, void* stream) {
+  if (!w || !keep || !split || !gvf || !ws) return FB_ERR_NULL;
+  if (n < 1 || n > INT32_MAX) return FB_ERR_SHAPE;
+  if ((reinterpret_cast<uintptr_t>(ws) & 255u) || (reinterpret_cast<uintptr_t>(split) & 7u) ||
+      (reinterpret_cast<uintptr_t>(gvf) & 7u) || (reinterpret_cast<uintptr_t>(w) & 3u))
+    return FB_ERR_ALIGN;
+  J2Layout L;
+  int st = j2_layout(n, L);
+  if (st != FB_OK) return st;
+  if (ws_bytes < L.total) return FB_ERR_WORKSPACE;
+  hipStream_t hs = static_cast<hipStream_t>(stream);
+  uint8_t* base = static_cast<uint8_t*>(ws);
+  auto at = [&](size_t off) { return static_cast<void*>(base + off); };
+  float* keys_in = static_cast<float*>(at(L.off_keys_in));
+  float* keys_out = static_cast<float*>(at(L.off_keys_out));
+  int* vals_in = static_cast<int*>(at(L.off_vals_in));
+  int* vals_out = static_cast<int*>(at(L.off_vals_out));
+  double *t1 = static_cast<double*>(at(L.off_t1)), *t2 = static_cast<double*>(at(L.off_t2));
+  double *bx1 = static_cast<double*>(at(L.off_bx1)), *bx2 = static_cast<double*>(at(L.off_bx2));
+  double *u1 = static_cast<double*>(at(L.off_u1)), *u2 = static_cast<double*>(at(L.off_u2));
+  double *sx1 = static_cast<double*>(at(L.off_sx1)), *sx2 = static_cast<double*>(at(L.off_sx2));
+  double* bmin = static_cast<double*>(at(L.off_bmin));
+  int* bidx = static_cast<int*>(at(L.off_bidx));
+  double* smin = static_cast<double*>(at(L.off_smin));
+  int* sidx = static_cast<int*>(at(L.off_sidx));
+  double* ssd0 = static_cast<double*>(at(L.off_ssd0));
+  const int ni = (int)n, nblk = (int)L.nblk, nsup = (int)L.nsup;
+  hipLaunchKernelGGL(j2_prep, dim3(grid_of(n, 256)), dim3(256), 0, hs, w, keys_in, vals_in, ni);
+  size_t sb = L.sort_bytes;
+  if (hipcub::DeviceRadixSort::SortPairs(at(L.off_sort), sb, keys_in, keys_out, vals_in, vals_out,
+                                         ni, 0, 32, hs) != hipSuccess)
+    return FB_ERR_HIP;
+  hipLaunchKernelGGL(j2_block_totals, dim3(grid_of(nblk, 64)), dim3(64), 0, hs, keys_out, ni, nblk,
+                     t1, t2);
+  hipLaunchKernelGGL(j2_super, dim3(grid_of(nsup, 64)), dim3(64), 0, hs, t1, t2, nblk, nsup, bx1,
+                     bx2, u1, u2);
+  hipLaunchKernelGGL(j2_top, dim3(1), dim3(1), 0, hs, u1, u2, nsup, sx1, sx2);
+  hipLaunchKernelGGL(j2_ssd, dim3(grid_of(nblk, 64)), dim3(64), 0, hs, keys_out, ni, nblk, nsup,
+                     bx1, bx2, sx1, sx2, bmin, bidx, ssd0);
+  hipLaunchKernelGGL(j2_min_super, dim3(grid_of(nsup, 64)), dim3(64), 0, hs, bmin, bidx, nblk, nsup,
+                     smin, sidx);
+  hipLaunchKernelGGL(j2_final, dim3(1), dim3(1), 0, hs, smin, sidx, nsup, ssd0, split, gvf);
+  hipLaunchKernelGGL(j2_mask, dim3(grid_of(n, 256)), dim3(256), 0, hs, vals_out, ni, split, keep);
+  return hipGetLastError() == hipSuccess ? FB_OK : FB_ERR_HIP;
+}
+
+}  // extern "C"

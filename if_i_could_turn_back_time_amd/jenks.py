@@ -1,0 +1,40 @@
+"""Two-class natural-breaks pruning masks over whole weight arrays, the reference's
+``Linear_Mask`` / ``Bias_Mask`` (``Python_Jenks_Test/Jenks_Tests/cuda_helpers.py:378-411``).
+
+The reference sorts the flattened weights, launches one CUDA thread per split index that
+sums both classes serially (``jenks_optimization_cuda``, ``:151-211``; O(n^2) overall),
+takes the first argmin of the within-class SSD and keeps the weights at sorted positions
+from the split on.  Here the same rule runs natively in O(n) after the sort
+(``fb_jenks2_gpu`` on a ROCm tensor, ``fb_jenks2_host`` on a CPU one; the two give the
+same bits).  The return values have the reference's types: a float32 CPU mask of the
+input's shape (1 = kept) and the goodness of variance fit as a Python float.
+"""
+from __future__ import annotations
+
+import torch
+
+from . import _capi as C
+
+
+def jenks2(weights: torch.Tensor):
+    """(keep bool tensor of ``weights``' shape, on its device; split index; GVF)."""
+    if weights.is_cuda:
+        keep, split, gvf = C.jenks2_gpu(weights)
+    else:
+        keep, split, gvf = C.jenks2_host(weights)
+    return keep.reshape(weights.shape), split, gvf
+
+
+def linear_mask(weights_cuda: torch.Tensor):
+    """``Linear_Mask`` (``cuda_helpers.py:378-395``): mask over the flattened weights,
+    reshaped to their shape, and GVF."""
+    keep, _, gvf = jenks2(weights_cuda)
+    return keep.to(device="cpu", dtype=torch.float32), gvf
+
+
+def bias_mask(weights_cuda: torch.Tensor):
+    """``Bias_Mask`` (``cuda_helpers.py:397-411``): the same rule on a 1-D tensor."""
+    if weights_cuda.dim() != 1:
+        raise ValueError("bias_mask takes a 1-D tensor (Linear_Mask flattens any shape)")
+    keep, _, gvf = jenks2(weights_cuda)
+    return keep.to(device="cpu", dtype=torch.float32), gvf

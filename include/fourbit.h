@@ -179,6 +179,40 @@ int fb_quantize_e2m1_gpu(const float* w, int32_t N, int32_t K, uint8_t* codes, u
 int fb_dequant(const void* wdev, void* w_out, int32_t out_dtype, const fb_shape_t* s,
                void* stream);
 
+/* ---------------------------------------------------------------------------------
+ * Two-class natural breaks over a whole array (k = 2 Jenks): the reference's weight and
+ * bias pruning masks, Linear_Mask / Bias_Mask (cuda_helpers.py:378-411), which call
+ * jenks_optimization_cuda / jenks_optimization_biases_cuda (cuda_helpers.py:151-211,
+ * :85-140; also CUDA_C_Code/include/layers.h:2424-2560).  The reference computes, for every
+ * split index idx of the ascending-sorted values, the SSD of [0, idx) about its mean plus the
+ * SSD of [idx, n) about its own (idx = 0: one class, "no split"), one O(n) thread per split,
+ * then takes the first argmin and keeps the values at sorted positions >= idx.  Here the
+ * class sums come from fp64 prefix sums: O(n) after the sort.
+ *   w      fp32 [n] (any shape, flattened), finite
+ *   keep   uint8 [n]: 1 where w[i] sits at a sorted position >= split (the reference's
+ *          `arr[indices[var_min:]] = 1`), else 0
+ *   split  int64: the first argmin over idx in [0, n)
+ *   gvf    double: (ssd(0) - ssd(split)) / (ssd(0) + 1e-8), the reference's GVF
+ * Arithmetic (fixed so host and GPU agree bit for bit): stable ascending sort (-0.0 ==
+ * +0.0), c = sorted[n/2], d = sorted - c and d*d in fp64, prefix sums sequential within
+ * blocks of 256, block totals sequential within superblocks of 256 blocks, superblock totals
+ * sequential, ssd(i) = [i ? Q(i) - P(i)^2/i : 0] + [(Qt - Q(i)) - (Pt - P(i))^2/(n - i)].
+ * The reference's own fp32 serial sums round differently: splits whose SSDs differ by less
+ * than that rounding may be chosen differently.  1 <= n <= 2^31 - 1.
+ * ------------------------------------------------------------------------------- */
+int fb_jenks2_host(const float* w, int64_t n, uint8_t* keep, int64_t* split, double* gvf);
+
+/* Device workspace bytes fb_jenks2_gpu needs for n values.  Queries the radix sort of the
+ * current HIP device, so it needs a GPU (FB_ERR_HIP without one). */
+int fb_jenks2_workspace(int64_t n, size_t* bytes);
+
+/* GPU version of fb_jenks2_host, bit-identical outputs.  w, keep, split, gvf and ws are
+ * device pointers (ws 256-byte aligned, at least fb_jenks2_workspace(n) bytes); asynchronous
+ * on the stream.  Non-finite values are not detected here (fb_jenks2_host rejects them with
+ * FB_ERR_VALUE), so callers check first. */
+int fb_jenks2_gpu(const float* w, int64_t n, uint8_t* keep, int64_t* split, double* gvf,
+                  void* ws, size_t ws_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

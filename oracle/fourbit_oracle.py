@@ -100,6 +100,65 @@ def jenks_breaks(v_sorted: np.ndarray, k: int):
     return bounds, D[:, n]
 
 
+def jenks2(values: np.ndarray):
+    """Two-class natural breaks over a whole array, the reference's pruning rule
+    (``Linear_Mask`` / ``Bias_Mask``, ``cuda_helpers.py:378-411``, over the kernels at
+    ``:85-118`` and ``:151-184``): for every split ``idx`` in ``[0, n)`` of the ascending
+    values, the SSD of ``[0, idx)`` about its mean plus the SSD of ``[idx, n)`` about its
+    own (``idx = 0`` is one class: "no split"); the first argmin is the split; the values at
+    sorted positions ``>= split`` are kept; ``GVF = (ssd(0) - ssd(split)) / (ssd(0) + 1e-8)``.
+
+    Unlike ``jenks_breaks(v, 2)``, whose DP forces two non-empty classes, split 0 is a
+    candidate here, as in the reference (its argmin runs over every idx); a constant array
+    therefore keeps everything.  The sums follow the build's fixed fp64 order (stable
+    ascending sort with -0.0 == +0.0; centre c = sorted[n // 2]; prefix sums sequential in
+    blocks of 256, block totals sequential in superblocks of 256 blocks, superblock totals
+    sequential), so that the native versions can be compared bit for bit.  Returns
+    ``(keep bool [n], split, gvf, ssd [n])``."""
+    w = np.asarray(values, dtype=np.float32).reshape(-1)
+    n = w.size
+    if n < 1 or not np.isfinite(w).all():
+        raise ValueError("need a non-empty finite array")
+    order = np.argsort(w, kind="stable")          # -0.0 == +0.0 under <
+    srt = w[order]
+    c = np.float64(srt[n // 2])
+    d = srt.astype(np.float64) - c
+    q = d * d
+    blk, sup = 256, 256
+    nblk = -(-n // blk)
+    nsup = -(-nblk // sup)
+
+    def blocked(v):
+        pad = np.zeros(nblk * blk)
+        pad[:n] = v
+        loc = np.cumsum(pad.reshape(nblk, blk), axis=1)       # sequential within a block
+        lx = np.concatenate([np.zeros((nblk, 1)), loc[:, :-1]], axis=1).reshape(-1)[:n]
+        tot = loc[:, -1]                                      # block totals
+        tpad = np.zeros(nsup * sup)
+        tpad[:nblk] = tot
+        bl = np.cumsum(tpad.reshape(nsup, sup), axis=1)
+        bx = np.concatenate([np.zeros((nsup, 1)), bl[:, :-1]], axis=1).reshape(-1)[:nblk]
+        u = bl[:, -1]
+        sx = np.concatenate([[0.0], np.cumsum(u)])           # sx[nsup] = total
+        i = np.arange(n)
+        b = i // blk
+        return (sx[b // sup] + bx[b]) + lx, sx[nsup]
+
+    P, Pt = blocked(d)
+    Q, Qt = blocked(q)
+    i = np.arange(n, dtype=np.float64)
+    with np.errstate(divide="ignore", invalid="ignore"):
+        left = np.where(i == 0, 0.0, Q - (P * P) / i)
+    rp = Pt - P
+    right = (Qt - Q) - (rp * rp) / (n - i)
+    ssd = left + right
+    split = int(np.argmin(ssd))                               # first minimum
+    keep = np.zeros(n, bool)
+    keep[order[split:]] = True
+    gvf = (ssd[0] - ssd[split]) / (ssd[0] + 1e-8)
+    return keep, split, float(gvf), ssd
+
+
 def f64_to_f16_bits(x: np.ndarray) -> np.ndarray:
     """fp64 -> fp32 -> fp16, each step round-to-nearest-even; returns uint16 bits."""
     return np.asarray(x, np.float64).astype(np.float32).astype(np.float16).view(np.uint16)

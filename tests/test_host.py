@@ -478,3 +478,52 @@ def test_backward_fwht_matches_oracle(block):
     got = _fwht_last_dim(t, block)
     ref = torch.from_numpy(O.fwht_rows(t.double().numpy(), block)).float()
     assert torch.allclose(got, ref, atol=1e-5, rtol=1e-5)
+
+
+# ----------------------------------------------------------------------------- two-class Jenks
+def _jenks2_inputs():
+    from model_fixtures import lenet300_from_fixture
+    net = lenet300_from_fixture()
+    yield "lenet300.1.weight", net[1].weight.detach().numpy()      # 300 x 784, ~98% zeros
+    yield "lenet300.3.weight", net[3].weight.detach().numpy()
+    yield "lenet300.5.bias", net[5].bias.detach().numpy()
+    for n in (1, 2, 3, 255, 256, 257, 4096, 65535, 65536, 65537, 131073):
+        w = (RNG.standard_normal(n) * 0.02).astype(np.float32)
+        if n > 8:
+            w[RNG.integers(0, n, n // 4)] = 0.0
+            w[RNG.integers(0, n, n // 8)] = -0.0
+        yield f"random{n}", w
+    yield "constant", np.full(1000, 0.5, np.float32)
+
+
+def test_jenks2_host_bit_exact_vs_oracle():
+    """fb_jenks2_host gives the oracle's split, GVF bits and mask (its arithmetic and
+    association order are the oracle's), on the reference's pruned LeNet300 weights and
+    on random arrays across the 256-element block and 65536-element superblock edges."""
+    for name, w in _jenks2_inputs():
+        keep_o, split_o, gvf_o, _ = O.jenks2(w)
+        keep_h, split_h, gvf_h = C.jenks2_host(torch.from_numpy(np.ascontiguousarray(w)))
+        assert split_h == split_o, name
+        assert np.float64(gvf_h).view(np.int64) == np.float64(gvf_o).view(np.int64), name
+        assert np.array_equal(keep_h.numpy(), keep_o.reshape(-1)), name
+
+
+def test_jenks2_host_errors_and_mask_api():
+    L = C.lib()
+    k = ctypes.c_char_p(b"x" * 8)
+    sp, gv = ctypes.c_int64(0), ctypes.c_double(0)
+    w = torch.tensor([1.0, float("nan")])
+    assert L.fb_jenks2_host(w.data_ptr(), 2, k, ctypes.byref(sp), ctypes.byref(gv)) == -10
+    assert L.fb_jenks2_host(w.data_ptr(), 0, k, ctypes.byref(sp), ctypes.byref(gv)) == -2
+    assert L.fb_jenks2_host(None, 2, k, ctypes.byref(sp), ctypes.byref(gv)) == -1
+    from if_i_could_turn_back_time_amd import bias_mask, linear_mask
+    W = torch.randn(30, 20) * 0.02
+    m, gvf = linear_mask(W)                         # cuda_helpers.py:378-395 return types
+    assert m.shape == W.shape and m.dtype == torch.float32 and m.device.type == "cpu"
+    assert isinstance(gvf, float) and 0.0 <= gvf <= 1.0
+    keep, split, _, _ = O.jenks2(W.numpy())
+    assert torch.equal(m.reshape(-1).bool(), torch.from_numpy(keep))
+    mb, _ = bias_mask(torch.randn(10))
+    assert mb.shape == (10,)
+    with pytest.raises(ValueError):
+        bias_mask(W)

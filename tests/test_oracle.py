@@ -386,3 +386,101 @@ def test_adaround_hard_equals_soft_where_saturated():
     assert bool(((soft_h == 0) | (soft_h == 1)).all())
     soft = torch.clamp(mask * (W_floor + soft_h), -8, 7)
     assert torch.equal(O.adaround_hard_levels(W_floor, alpha, mask, -8, 7), soft)
+
+
+# ----------------------------------------------------------------------------- k = 2 over arrays
+def _reference_k2_split_fp32(v):
+    """The reference kernel's own arithmetic (cuda_helpers.py:151-184) in float32: each
+    split's class means from serial float sums, then the serial float SSD; argmin over
+    every idx (cuda_helpers.py:386), split 0 included."""
+    v = np.asarray(v, np.float32)
+    n = v.size
+    var = np.zeros(n, np.float32)
+    for idx in range(n):
+        m1 = np.float32(0)
+        for t in range(idx):
+            m1 = np.float32(m1 + v[t])
+        if idx:
+            m1 = np.float32(m1 / np.float32(idx))
+        m2 = np.float32(0)
+        for t in range(idx, n):
+            m2 = np.float32(m2 + v[t])
+        m2 = np.float32(m2 / np.float32(n - idx))
+        acc = np.float32(0)
+        for t in range(idx):
+            acc = np.float32(acc + np.float32(v[t] - m1) * np.float32(v[t] - m1))
+        for t in range(idx, n):
+            acc = np.float32(acc + np.float32(v[t] - m2) * np.float32(v[t] - m2))
+        var[idx] = acc
+    return int(np.argmin(var)), var
+
+
+def test_jenks2_known_answer_jenks_test():
+    """jenks_test.py:4-60's score array: the two-class split of its sorted values is 22
+    (the reference kernel's rule, restated above)."""
+    arr = np.array([[0.4175, 0.2946, -0.2116, -0.2154], [0.3566, 0.4245, 0.2321, -0.4188],
+                    [-0.4813, 0.3807, -0.4328, -0.3908], [-0.0824, -0.0291, 0.1397, 0.0277],
+                    [-0.1358, -0.4866, 0.1868, -0.4537], [-0.0392, -0.2796, 0.2498, 0.3536],
+                    [-0.4195, -0.3004, 0.1421, 0.1625], [0.0492, -0.3681, -0.3715, -0.0706]])
+    arr_1 = np.repeat(np.array([-0.0615, 0.0, 0.0, 0.0277, 0.0, -0.0377, -0.0516, 0.0])[:, None],
+                      4, axis=1)
+    score = np.abs(arr * arr_1).reshape(-1).astype(np.float32)
+    keep, split, gvf, _ = O.jenks2(score)
+    assert split == 22 == _reference_k2_split_fp32(np.sort(score, kind="stable"))[0]
+    order = np.argsort(score, kind="stable")
+    assert keep.sum() == 32 - 22 and keep[order[22:]].all() and not keep[order[:22]].any()
+    assert 0 < gvf < 1
+
+
+def test_jenks2_matches_reference_kernel_arithmetic():
+    """Against the reference kernel's float32 arithmetic and the float64 two-pass rule on
+    random arrays (near-ties, where float32 rounding decides, are skipped)."""
+    for _ in range(25):
+        n = int(RNG.integers(2, 90))
+        w = (RNG.standard_t(3, size=n) * 0.05).astype(np.float32)
+        keep, split, gvf, ssd = O.jenks2(w)
+        v = np.sort(w, kind="stable")
+        s64, var64 = _reference_k2_split(v.astype(np.float64))
+        s32, var32 = _reference_k2_split_fp32(v)
+        srt = np.sort(var64)
+        if srt[1] - srt[0] > 1e-5 * srt[0]:
+            assert split == s64 == s32
+        assert np.isclose(ssd[split], var64.min(), rtol=1e-9, atol=1e-15)
+        assert np.isclose(gvf, (var64[0] - var64.min()) / (var64[0] + 1e-8), rtol=1e-9)
+
+
+def test_jenks2_brute_force_over_all_two_way_partitions():
+    """For n <= 10, every partition of the values into two sets (one may be empty): the
+    minimum within-class SSD is the one at the chosen split, so the optimum is contiguous
+    in sorted order and 'no split' competes."""
+    from itertools import product
+    for n in range(1, 10):
+        for _ in range(4):
+            w = np.round(RNG.normal(size=n) * 4) / 4        # ties on purpose
+            w = w.astype(np.float32)
+            _, split, _, ssd = O.jenks2(w)
+            best = np.inf
+            for bits in product((0, 1), repeat=n):
+                m = np.array(bits, bool)
+                cost = 0.0
+                for part in (w[m].astype(np.float64), w[~m].astype(np.float64)):
+                    if part.size:
+                        cost += ((part - part.mean()) ** 2).sum()
+                best = min(best, cost)
+            assert abs(ssd[split] - best) <= 1e-12 + 1e-9 * best, (n, w)
+
+
+def test_jenks2_degenerate_inputs():
+    """A constant array is 'no split' (split 0, everything kept, GVF 0); two constant runs
+    split exactly between them; -0.0 and +0.0 are equal and keep their index order."""
+    keep, split, gvf, _ = O.jenks2(np.full(17, 0.25, np.float32))
+    assert split == 0 and keep.all() and gvf == 0.0
+    w = np.array([3.0] * 5 + [-1.0] * 7, np.float32)
+    keep, split, gvf, _ = O.jenks2(w)
+    assert split == 7 and keep.tolist() == [True] * 5 + [False] * 7
+    assert np.isclose(gvf, 1.0, atol=1e-6)
+    w = np.array([0.0, -0.0, 0.0, -0.0, 1.0, 1.0, 1.0, 1.0, 1.0, 1.0], np.float32)
+    keep, split, _, _ = O.jenks2(w)
+    assert split == 4 and not keep[:4].any() and keep[4:].all()
+    keep, split, gvf, _ = O.jenks2(np.array([2.5], np.float32))
+    assert split == 0 and keep.all()
