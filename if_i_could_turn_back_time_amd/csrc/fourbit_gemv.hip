@@ -730,6 +730,46 @@ __global__ __launch_bounds__(256) void dequant_kernel(const uint8_t* __restrict_
 }
 
 // ---------------------------------------------------------------------------------
+// Rotation of x once per call, for batches where every workgroup rotating all of x in its
+// prologue would cost more than a launch: workgroup (c, b) rotates row b's values
+// [4096c, 4096c + 4096) with stage_fwht (the same arithmetic as the GEMV's own prologue, so
+// the fp16 values are the ones the GEMV would stage) and writes them to xo [B, K].
+// ---------------------------------------------------------------------------------
+constexpr int kRotPiece = 4096;
+constexpr int kRotWaves = 4;
+
+__host__ __device__ inline int rot_lds_bytes(int kw) {
+  return ((x_row_stride(kw / 128) + 15) & ~15) + fpad(kw) * 4 + 64;
+}
+
+template <int NW>
+__global__ __launch_bounds__(NW * 64) void rotate_kernel(const uint16_t* __restrict__ x,
+                                                         uint16_t* __restrict__ xo, int K,
+                                                         int fb, float sc) {
+  extern __shared__ __align__(16) uint8_t lds[];
+  const int c = blockIdx.x, b = blockIdx.y;
+  const int k0 = c * kRotPiece;
+  const int kw = min(kRotPiece, K - k0);  // a multiple of fb and of 128
+  const int nsl = kw / 128;
+  const int RS = x_row_stride(nsl);
+  float* F = reinterpret_cast<float*>(lds + ((RS + 15) & ~15));
+  const int tid = threadIdx.x;
+  const uint16_t* xrow = x + (int64_t)b * K;
+  const rsrc_t xrs = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(xrow), (short)0,
+                                                       K * 2, kRsrcWord3);
+  XRot xr;
+  rot_preload<NW>(xr, xrs, K, 1, k0, kw, tid);
+  stage_fwht<NW>(lds, F, xr, xrs, K, 1, k0, kw, nsl, RS, fb, sc, tid);
+  __syncthreads();
+  uint16_t* orow = xo + (int64_t)b * K + k0;
+  for (int t = tid; t < kw / 8; t += NW * 64) {
+    const int g = t >> 4, e = (t & 15) * 8;
+    *reinterpret_cast<u32x4*>(orow + g * 128 + e) =
+        *reinterpret_cast<const u32x4*>(lds + g * kSliceBytes + e * 2);
+  }
+}
+
+// ---------------------------------------------------------------------------------
 // host side
 // ---------------------------------------------------------------------------------
 constexpr int kMaxDevices = 64;
@@ -871,37 +911,31 @@ int launch_plan(const void* wdev, const void* x, void* y, const fb_shape_t* s, c
   return launch_mode<FB_FMT_E2M1, FB_DT_F16>(mode, wdev, x, y, s, pl, hs);
 }
 
-}  // namespace
+// Rotated calls with at least this many activation values (B * K) rotate x once
+// (rotate_kernel, into the workspace) instead of in the prologue of every workgroup, which
+// redoes the whole batch's rotation on every CU.  Measured on MI355X (median us, in-kernel
+// against once): 4096x4096 b=4096 B=3 10.8 / 11.6, B=4 12.3 / 11.6, B=16 42.5 / 12.9;
+// K=11008 b=256 B=1 11.4 / 12.5, B=2 14.5 / 14.0, B=16 54.3 / 21.0; 8192->28672 b=4096 B=1
+// 32.7 / 36.4, B=4 44.9 / 35.8, B=16 176.6 / 43.5.
+constexpr int64_t kRotOnceValues = 16384;
 
-extern "C" {
-
-size_t fb_workspace_bytes(const fb_shape_t* s) {
-  (void)s;
-  return 0;  // the GEMV needs no device workspace
+size_t rot_once_bytes(const fb_shape_t* s) {
+  if (!s->fwht_block || (int64_t)s->B * s->K < kRotOnceValues) return 0;
+  return ((size_t)s->B * s->K * 2 + 255) & ~size_t(255);
 }
 
-int fb_gemv(const void* wdev, const void* x, void* y, const fb_shape_t* s, void* ws,
-            size_t ws_bytes, void* stream) {
-  (void)ws;
-  (void)ws_bytes;
-  if (!s || !wdev || !x || !y) return FB_ERR_NULL;
-  int st = fb_validate(s);
-  if (st != FB_OK) return st;
-  if (s->B > 16) return FB_ERR_BATCH;
-  if (!aligned16(wdev) || !aligned16(x) || (reinterpret_cast<uintptr_t>(y) & 3u))
-    return FB_ERR_ALIGN;
-  if (s->fwht_block && s->x_dtype != FB_DT_F16) return FB_ERR_DTYPE;
-  const int cus = device_cus();
-  {
-    // The kernel addresses a workgroup's blocks with 32-bit offsets from its first block,
-    // so the row tiles one workgroup owns (at most ceil(T / min(T, CUs))) must span less
-    // than 2^31 bytes.  Under fb_validate's limit of 2^31 groups (192 GiB of GF4 stream)
-    // this holds on every device with 128 CUs or more.
-    const int64_t T = (s->N + 15) / 16, GS = (s->K / 128 + 3) / 4;
-    const int64_t grid = std::min<int64_t>(T, cus);
-    if ((T + grid - 1) / grid * GS * fb::block_bytes(s->fmt) > INT32_MAX) return FB_ERR_SHAPE;
-  }
-  hipStream_t hs = static_cast<hipStream_t>(stream);
+int launch_rotate(const void* x, void* xo, const fb_shape_t* s, hipStream_t hs) {
+  const int pieces = (s->K + kRotPiece - 1) / kRotPiece;
+  hipLaunchKernelGGL(rotate_kernel<kRotWaves>, dim3(pieces, s->B), dim3(kRotWaves * 64),
+                     rot_lds_bytes(std::min(s->K, kRotPiece)), hs,
+                     static_cast<const uint16_t*>(x), static_cast<uint16_t*>(xo), s->K,
+                     s->fwht_block, fwht_scale(s->fwht_block));
+  return hipGetLastError() == hipSuccess ? FB_OK : FB_ERR_HIP;
+}
+
+// The GEMV of a validated shape: one launch when a plan fits LDS, else row chunks.
+int gemv_planned(const void* wdev, const void* x, void* y, const fb_shape_t* s, int cus,
+                 hipStream_t hs) {
   Plan pl;
   if (make_plan(s, cus, pl)) return launch_plan(wdev, x, y, s, pl, hs);
   // No plan holds the whole batch in LDS (a 4096-wide rotation keeps an fp32 copy of every
@@ -922,6 +956,52 @@ int fb_gemv(const void* wdev, const void* x, void* y, const fb_shape_t* s, void*
     if (st != FB_OK) return st;
   }
   return FB_OK;
+}
+
+// fb_gemv behind the ABI.  ws (ws_bytes) is the scratch for the once-per-call rotation of
+// larger batches; without enough of it the rotation runs in every workgroup's prologue.
+int gemv_impl(const void* wdev, const void* x, void* y, const fb_shape_t* s, void* ws,
+              size_t ws_bytes, hipStream_t hs) {
+  if (!s || !wdev || !x || !y) return FB_ERR_NULL;
+  int st = fb_validate(s);
+  if (st != FB_OK) return st;
+  if (s->B > 16) return FB_ERR_BATCH;
+  if (!aligned16(wdev) || !aligned16(x) || (reinterpret_cast<uintptr_t>(y) & 3u))
+    return FB_ERR_ALIGN;
+  if (s->fwht_block && s->x_dtype != FB_DT_F16) return FB_ERR_DTYPE;
+  const int cus = device_cus();
+  {
+    // The kernel addresses a workgroup's blocks with 32-bit offsets from its first block,
+    // so the row tiles one workgroup owns (at most ceil(T / min(T, CUs))) must span less
+    // than 2^31 bytes.  Under fb_validate's limit of 2^31 groups (192 GiB of GF4 stream)
+    // this holds on every device with 128 CUs or more.
+    const int64_t T = (s->N + 15) / 16, GS = (s->K / 128 + 3) / 4;
+    const int64_t grid = std::min<int64_t>(T, cus);
+    if ((T + grid - 1) / grid * GS * fb::block_bytes(s->fmt) > INT32_MAX) return FB_ERR_SHAPE;
+  }
+  const size_t need = rot_once_bytes(s);
+  if (need && ws && ws_bytes >= need && (reinterpret_cast<uintptr_t>(ws) & 255u) == 0) {
+    st = launch_rotate(x, ws, s, hs);
+    if (st != FB_OK) return st;
+    fb_shape_t u = *s;
+    u.fwht_block = 0;  // x' is rotated
+    return gemv_planned(wdev, ws, y, &u, cus, hs);
+  }
+  return gemv_planned(wdev, x, y, s, cus, hs);
+}
+
+}  // namespace
+
+extern "C" {
+
+size_t fb_workspace_bytes(const fb_shape_t* s) {
+  if (fb_validate(s) != FB_OK) return 0;
+  return rot_once_bytes(s);
+}
+
+int fb_gemv(const void* wdev, const void* x, void* y, const fb_shape_t* s, void* ws,
+            size_t ws_bytes, void* stream) {
+  return gemv_impl(wdev, x, y, s, ws, ws_bytes, static_cast<hipStream_t>(stream));
 }
 
 int fb_dequant(const void* wdev, void* w_out, int32_t out_dtype, const fb_shape_t* s,

@@ -74,7 +74,9 @@ int fb_validate(const fb_shape_t* s);
  * fb_gemv. */
 size_t fb_device_bytes(const fb_shape_t* s);
 
-/* Workspace bytes fb_gemv needs for this shape (currently 0 for every shape). */
+/* Workspace bytes fb_gemv can use for this shape: B*K*2 (rounded up to 256) for rotated
+ * shapes with B*K >= 16384, where x is rotated once into the workspace by its own small
+ * kernel before the GEMV; 0 otherwise (and for invalid shapes). */
 size_t fb_workspace_bytes(const fb_shape_t* s);
 
 /* ---------------------------------------------------------------------------------
@@ -144,13 +146,14 @@ int fb_dequant_host(const uint8_t* codes, const void* meta, float* w_out, const 
  * brecq.py:323-329 new_forward) and the reference's native linear_kernel_batch
  * (CUDA_C_Code/include/layers.h:9828-9839).  wdev is the fb_to_device stream in
  * device memory; x is [B,K] of x_dtype, y is [B,N] of y_dtype.
- * ws: device workspace of at least fb_workspace_bytes(s) bytes (16-byte aligned).  The
- * current kernels exchange nothing between workgroups through memory, so
- * fb_workspace_bytes is 0 for every valid shape and ws may be NULL; the argument is
- * kept so that a future split-K variant does not change the ABI.
- * A batch whose staged activations do not fit LDS at once (a 4096-wide rotation keeps an
- * fp32 copy of every batch row) runs as several launches over row chunks, each streaming
- * the weights; FB_ERR_LDS only when a single row does not fit. */
+ * ws: device workspace (256-byte aligned) of fb_workspace_bytes(s) bytes, or NULL.  With it,
+ * a rotated call of B*K >= 16384 values rotates x once into ws (one extra small kernel)
+ * and runs the unrotated GEMV on it; without it (NULL, too small or misaligned) every
+ * workgroup rotates x in its prologue, which gives the same results within the tolerance
+ * and is slower for such batches.  Calls that share a workspace must not overlap.
+ * A batch whose staged activations do not fit LDS at once (a 4096-wide rotation done in
+ * the prologue keeps an fp32 copy of every batch row) runs as several launches over row
+ * chunks, each streaming the weights; FB_ERR_LDS only when a single row does not fit. */
 int fb_gemv(const void* wdev, const void* x, void* y, const fb_shape_t* s, void* ws,
             size_t ws_bytes, void* stream);
 

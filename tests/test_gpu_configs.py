@@ -253,3 +253,37 @@ def test_backward_matches_linear_with_decoded_weight(fmt, K, hadamard):
     gb_ref = gy.float().reshape(-1, N).sum(0)
     ok, emax = within_tol(q.bias.grad, gb_ref, 2.0 ** -8)
     assert ok, f"grad_bias: {emax}"
+
+
+@pytest.mark.parametrize("N,K,B,block", [(4096, 4096, 8, 4096), (96, 11008, 16, 256),
+                                         (520, 8192, 4, 4096), (64, 4096, 4, 2048)])
+def test_rotated_batch_with_and_without_workspace(N, K, B, block):
+    """Rotated batches of B*K >= 16384 values rotate x once into the workspace (an extra
+    small kernel), else (no workspace passed) in every workgroup's prologue: both within
+    tolerance of the oracle's rotated product, and of each other."""
+    import ctypes
+    say("rotate once", N, K, B, block)
+    g = torch.Generator().manual_seed(N + K + B)
+    w = torch.randn(N, K, generator=g) * 0.02
+    pw = PackedWeight.quantize(w, "gf4", fwht_block=block, device=DEV)
+    x = torch.randn(B, K, generator=g).half()
+    codes = O.unpack_nibbles(pw.codes.numpy())
+    yref = O.y_ref("gf4", codes, pw.meta.numpy().view(np.uint16), x, block)
+    shape = pw.shape(B, torch.float16, torch.float32)
+    need = C.workspace_bytes(shape)
+    assert need == B * K * 2
+    xd = x.to(DEV)
+    ys = {}
+    for mode in ("workspace", "none"):
+        y = torch.full((B, N), float("nan"), device=DEV)
+        ws = torch.zeros(need, dtype=torch.uint8, device=DEV) if mode == "workspace" else None
+        rc = C.lib().fb_gemv(pw.wdev.data_ptr(), xd.data_ptr(), y.data_ptr(), ctypes.byref(shape),
+                             None if ws is None else ws.data_ptr(), need if ws is not None else 0,
+                             torch.cuda.current_stream().cuda_stream)
+        assert rc == 0
+        torch.cuda.synchronize()
+        ok, emax = within_tol(y, yref)
+        assert ok, f"{mode}: max abs err {emax}"
+        ys[mode] = y.cpu()
+    ok, emax = within_tol(ys["workspace"], ys["none"])
+    assert ok, emax

@@ -222,10 +222,16 @@ def test_quantize_module_swaps_linears_and_keeps_masks():
 
 
 def test_workspace_contract():
-    """The GEMV needs no device workspace (workgroups never exchange partial sums), so
-    fb_gemv accepts NULL; the argument stays in the ABI for callers that pass one."""
+    """fb_gemv's workspace is only for rotating x once per call: 0 bytes for unrotated
+    shapes and for rotated ones under 16384 activation values (B*K), else B*K*2 rounded
+    up to 256; invalid shapes report 0 and are still rejected by fb_gemv."""
     for B in (1, 4, 16):
         assert C.workspace_bytes(C.make_shape(8192, 28672, B)) == 0
+    assert C.workspace_bytes(C.make_shape(4096, 4096, 3, C.FMT_GF4, 4096)) == 0
+    assert C.workspace_bytes(C.make_shape(4096, 4096, 4, C.FMT_GF4, 4096)) == 4 * 4096 * 2
+    assert C.workspace_bytes(C.make_shape(4096, 11008, 2, C.FMT_GF4, 256)) == 44032
+    assert C.workspace_bytes(C.make_shape(4096, 11008, 1, C.FMT_GF4, 256)) == 0
+    assert C.workspace_bytes(C.make_shape(64, 100, 4, C.FMT_GF4, 4096)) == 0   # invalid K
     buf = ctypes.c_char_p(b"x" * 64)
     big = C.make_shape(8192, 28672, 17)
     assert C.lib().fb_gemv(buf, buf, buf, ctypes.byref(big), None, 0, None) == -9
