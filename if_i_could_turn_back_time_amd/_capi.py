@@ -34,6 +34,7 @@ EXPORTED = (
     "fb_fwht_rows_f32", "fb_to_device",
     "fb_from_device", "fb_dequant_host", "fb_gemv", "fb_dequant", "fb_quantize_gf4_gpu",
     "fb_quantize_e2m1_gpu", "fb_jenks2_host", "fb_jenks2_workspace", "fb_jenks2_gpu",
+    "fb_gemv_noalloc",
 )
 
 
@@ -78,6 +79,7 @@ def lib() -> ctypes.CDLL:
         "fb_jenks2_host": (ctypes.c_int, [vp, ctypes.c_int64, vp, vp, vp]),
         "fb_jenks2_workspace": (ctypes.c_int, [ctypes.c_int64, ctypes.POINTER(sz)]),
         "fb_jenks2_gpu": (ctypes.c_int, [vp, ctypes.c_int64, vp, vp, vp, vp, sz, vp]),
+        "fb_gemv_noalloc": (ctypes.c_int, [vp, vp, vp, sp, vp]),
     }
     for name, (res, args) in sigs.items():
         fn = getattr(L, name)

@@ -990,9 +990,44 @@ int gemv_impl(const void* wdev, const void* x, void* y, const fb_shape_t* s, voi
   return gemv_planned(wdev, x, y, s, cus, hs);
 }
 
+// Scratch of the allocation-free entry point: a file-scope device array (one per GPU the
+// library runs on, alive until the process ends).  Host code never uses the array's name as
+// an address: the device address comes from hipGetSymbolAddress, once per device.
+constexpr size_t kScratchBytes = size_t(1) << 20;
+__device__ __align__(256) uint8_t scratch[kScratchBytes];
+std::atomic<void*> g_scratch[kMaxDevices];
+
+// The scratch's device address on the current device (nullptr on failure).
+void* scratch_ptr(int dev) {
+  if (dev < 0 || dev >= kMaxDevices) return nullptr;
+  void* p = g_scratch[dev].load(std::memory_order_acquire);
+  if (p) return p;
+  void* q = nullptr;
+  if (hipGetSymbolAddress(&q, HIP_SYMBOL(scratch)) != hipSuccess || !q) return nullptr;
+  g_scratch[dev].store(q, std::memory_order_release);
+  return q;
+}
+
 }  // namespace
 
 extern "C" {
+
+int fb_gemv_noalloc(const void* wdev, const void* x, void* y, const fb_shape_t* s,
+                    void* stream) {
+  if (!s) return FB_ERR_NULL;
+  const int st = fb_validate(s);
+  if (st != FB_OK) return st;
+  const size_t need = rot_once_bytes(s);
+  if (need > kScratchBytes) return FB_ERR_SCRATCH;
+  void* ws = nullptr;
+  if (need) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return FB_ERR_HIP;
+    ws = scratch_ptr(dev);
+    if (!ws) return FB_ERR_HIP;
+  }
+  return gemv_impl(wdev, x, y, s, ws, need ? kScratchBytes : 0, static_cast<hipStream_t>(stream));
+}
 
 size_t fb_workspace_bytes(const fb_shape_t* s) {
   if (fb_validate(s) != FB_OK) return 0;

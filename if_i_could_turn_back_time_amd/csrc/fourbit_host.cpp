@@ -246,6 +246,9 @@ const char* fb_strerror(int code) {
     case FB_ERR_THREADS: return "fourbit: nthreads must be >= 1";
     case FB_ERR_LDS: return "fourbit: activation vector does not fit the kernel's LDS budget";
     case FB_ERR_LEVELS: return "fourbit: the integer levels of a 128-group span more than 16 values";
+    case FB_ERR_SCRATCH:
+      return "fourbit: the shape needs more scratch than fb_gemv_noalloc's fixed 1 MiB device "
+             "array (a rotated call of B*K > 524288 values); use fb_gemv with a workspace";
     default: return "fourbit: unknown error";
   }
 }

@@ -44,7 +44,8 @@ typedef enum {
   FB_ERR_HIP = -11,          /* a HIP runtime call failed                          */
   FB_ERR_THREADS = -12,      /* nthreads < 1                                       */
   FB_ERR_LDS = -13,          /* activation does not fit the kernel's LDS budget    */
-  FB_ERR_LEVELS = -14        /* integer levels of one 128-group span > 16 values    */
+  FB_ERR_LEVELS = -14,       /* integer levels of one 128-group span > 16 values    */
+  FB_ERR_SCRATCH = -15       /* shape needs more than fb_gemv_noalloc's fixed scratch */
 } fb_status;
 
 typedef enum { FB_FMT_GF4 = 0, FB_FMT_E2M1 = 1 } fb_fmt;
@@ -156,6 +157,18 @@ int fb_dequant_host(const uint8_t* codes, const void* meta, float* w_out, const 
  * chunks, each streaming the weights; FB_ERR_LDS only when a single row does not fit. */
 int fb_gemv(const void* wdev, const void* x, void* y, const fb_shape_t* s, void* ws,
             size_t ws_bytes, void* stream);
+
+/* fb_gemv that allocates nothing and takes no workspace.  No counterpart in the reference:
+ * it is for callers that cannot allocate device memory around a call (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc).  The once-per-call
+ * rotation's scratch is a file-scope device array of 1 MiB per GPU (its address is looked
+ * up once per device on the first call there, and the array lives until the process
+ * ends): rotated calls of B*K > 524288 values return FB_ERR_SCRATCH.  No hipMalloc, hipFree
+ * or allocating library call is made.  Every call on a GPU shares that GPU's array, so
+ * calls that overlap on one GPU (several streams or host threads) race; serialise them.
+ * Results equal fb_gemv's with a workspace. */
+int fb_gemv_noalloc(const void* wdev, const void* x, void* y, const fb_shape_t* s,
+                    void* stream);
 
 /* GF4 packer on the GPU: the same arithmetic as fb_quantize_gf4 (keep == NULL) and
  * fb_quantize_gf4_masked, one wavefront per (row, 128-group), fp64; the outputs are

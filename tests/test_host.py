@@ -533,3 +533,16 @@ def test_jenks2_host_errors_and_mask_api():
     assert mb.shape == (10,)
     with pytest.raises(ValueError):
         bias_mask(W)
+
+
+def test_gemv_noalloc_validation_needs_no_gpu():
+    """fb_gemv_noalloc checks the shape and its scratch need before any device call: a
+    rotated call of more than 524288 activation values (1 MiB of fp16) is FB_ERR_SCRATCH."""
+    L = C.lib()
+    buf = ctypes.c_char_p(b"x" * 64)
+    big = C.make_shape(64, 65536, 16, C.FMT_GF4, 4096)
+    assert L.fb_gemv_noalloc(buf, buf, buf, ctypes.byref(big), None) == -15
+    assert "scratch" in C.strerror(-15)
+    assert L.fb_gemv_noalloc(buf, buf, buf, None, None) == -1
+    bad = C.make_shape(64, 100, 1)
+    assert L.fb_gemv_noalloc(buf, buf, buf, ctypes.byref(bad), None) == -2
