@@ -287,16 +287,24 @@ struct XRot {
 // moves no data.  The loads are issued back to back with no branch, and nothing waits for
 // them before stage_fwht.
 constexpr unsigned kXOutOfRange = 0x7FFFFFF0u;
+// Position of lane l's four values inside a 256-value sub-block: 4l for the butterflies;
+// 16 (l % 16) + 4 (l / 16) for the matrix-core transform (blocks of 256 or more), where they
+// are row l % 16, columns 4 (l / 16) .. + 3 of the sub-block as a 16 x 16 matrix.
+__device__ __forceinline__ int rot_lane_pos(int lane, int fb) {
+  return fb >= 256 ? 16 * (lane & 15) + 4 * (lane >> 4) : 4 * lane;
+}
+
 template <int NW>
 __device__ __forceinline__ void rot_preload(XRot& xr, rsrc_t xrs, int K, int B, int k0, int kw,
-                                            int tid) {
+                                            int fb, int tid) {
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
   const int nsb = (kw + 255) >> 8;
+  const int lpos = rot_lane_pos(lane, fb);
 #pragma unroll
   for (int i = 0; i < kXPre; ++i) {
     const int sb = wave + i * NW;  // flat sub-block index over (row, sub-block), uniform
     const int b = B == 1 ? 0 : small_div(sb, nsb);
-    const int k = (sb - b * nsb) * 256 + lane * 4;
+    const int k = (sb - b * nsb) * 256 + lpos;
     const unsigned off = sb < B * nsb && k < kw ? (unsigned)(b * K + k0 + k) * 2u : kXOutOfRange;
     const auto v = __builtin_amdgcn_raw_buffer_load_b64(xrs, off, 0, 0);
     xr.v[i] = uint2{(unsigned)v[0], (unsigned)v[1]};
@@ -332,6 +340,50 @@ __device__ __forceinline__ float lane_xor(float v, int m, int lane) {
 // so the four 1024-apart lane groups of a phase-2 read fall in different banks.
 __host__ __device__ __forceinline__ int fpad(int p) { return p + (p >> 10) * 16; }
 
+typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
+typedef short bf16x4_t __attribute__((ext_vector_type(4)));
+
+// H16 operand values of lane l: H16[4 (l / 16) + r][l % 16] = (-1)^popcount(.. & ..), as fp16
+// (for the first product) and as bf16 (for the second).
+struct H16Ops {
+  half4_t f;
+  bf16x4_t b;
+};
+__device__ __forceinline__ H16Ops h16_ops(int lane) {
+  H16Ops h;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const bool neg = __builtin_popcount((4 * (lane >> 4) + r) & (lane & 15)) & 1;
+    h.f[r] = neg ? (_Float16)-1.0f : (_Float16)1.0f;
+    h.b[r] = neg ? (short)0xBF80 : (short)0x3F80;
+  }
+  return h;
+}
+
+// Unnormalised 256-point Walsh-Hadamard transform of one sub-block on the matrix cores.  The
+// sub-block is a 16 x 16 matrix X (value 16 i + j at row i, column j); H256 x = H16 X H16.
+//  1. D1 = X H16: X is the A operand as loaded (lane l: row l % 16, columns 4 (l / 16) ..),
+//     fp16 values times +-1 summed in fp32.
+//  2. The accumulator of D1 fed back as an A operand is D1 transposed, so D2 = D1^T H16 =
+//     (H16 X H16)^T, which lands in lane l as the values 16 (l % 16) + 4 (l / 16) + r: the
+//     positions the lane loaded.  D1 goes in as bf16 hi + lo (hi = bf16(d), lo = bf16(d - hi),
+//     together within 2^-18 of d), two bf16 products summed in fp32.
+__device__ __forceinline__ f32x4 fwht256_mfma(uint2 raw, const H16Ops& h) {
+  const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
+  const f32x4 d1 =
+      __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(half4_t, raw), h.f, zero, 0, 0, 0);
+  bf16x4_t hi, lo;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const __bf16 a = (__bf16)d1[r];
+    hi[r] = __builtin_bit_cast(short, a);
+    lo[r] = __builtin_bit_cast(short, (__bf16)(d1[r] - (float)a));
+  }
+  f32x4 d2 = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(hi, h.b, zero, 0, 0, 0);
+  d2 = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(lo, h.b, d2, 0, 0, 0);
+  return d2;
+}
+
 template <int NW>
 __device__ void stage_fwht(uint8_t* lds, float* F, const XRot& xr, rsrc_t xrs, int K, int B,
                            int k0, int kw, int nsl, int RS, int fb, float sc, int tid) {
@@ -347,10 +399,13 @@ __device__ void stage_fwht(uint8_t* lds, float* F, const XRot& xr, rsrc_t xrs, i
   float sgn[6];
 #pragma unroll
   for (int st = 0; st < 6; ++st) sgn[st] = (lane & (1 << st)) ? -1.0f : 1.0f;
+  const bool mfma = lg_fb >= 8;  // uniform: whole 256-value sub-blocks on the matrix cores
+  const H16Ops hops = h16_ops(lane);
+  const int lpos = rot_lane_pos(lane, fb);
   int i = 0;
   for (int sb = wave; sb < B * nsb; sb += NW, ++i) {
     const int b = B == 1 ? 0 : small_div(sb, nsb);
-    const int k = (sb - b * nsb) * 256 + lane * 4;
+    const int k = (sb - b * nsb) * 256 + lpos;
     const bool live = k < kw;  // kw is a multiple of 128: whole lanes are in or out
     uint2 raw = {0u, 0u};
     if (i < kXPre) {
@@ -362,27 +417,39 @@ __device__ void stage_fwht(uint8_t* lds, float* F, const XRot& xr, rsrc_t xrs, i
           xrs, live ? (unsigned)(b * K + k0 + k) * 2u : kXOutOfRange, 0, 0);
       raw = uint2{(unsigned)v[0], (unsigned)v[1]};
     }
-    const _Float16* h = reinterpret_cast<const _Float16*>(&raw);
-    float v[4] = {(float)h[0], (float)h[1], (float)h[2], (float)h[3]};
-    if (lg_fb > 0) {
-      bfly(v[0], v[1]);
-      bfly(v[2], v[3]);
-    }
-    if (lg_fb > 1) {
-      bfly(v[0], v[2]);
-      bfly(v[1], v[3]);
-    }
+    float v[4];
+    if (mfma) {
+      const f32x4 d = fwht256_mfma(raw, hops);
+      v[0] = d[0];
+      v[1] = d[1];
+      v[2] = d[2];
+      v[3] = d[3];
+    } else {
+      const _Float16* h = reinterpret_cast<const _Float16*>(&raw);
+      v[0] = (float)h[0];
+      v[1] = (float)h[1];
+      v[2] = (float)h[2];
+      v[3] = (float)h[3];
+      if (lg_fb > 0) {
+        bfly(v[0], v[1]);
+        bfly(v[2], v[3]);
+      }
+      if (lg_fb > 1) {
+        bfly(v[0], v[2]);
+        bfly(v[1], v[3]);
+      }
 #pragma unroll
-    for (int st = 0; st < 6; ++st) {
-      if (st + 2 < lg_fb) {  // uniform
+      for (int st = 0; st < 6; ++st) {
+        if (st + 2 < lg_fb) {  // uniform
 #pragma unroll
-        for (int e = 0; e < 4; ++e) v[e] = __builtin_fmaf(sgn[st], v[e], lane_xor(v[e], 1 << st, lane));
+          for (int e = 0; e < 4; ++e)
+            v[e] = __builtin_fmaf(sgn[st], v[e], lane_xor(v[e], 1 << st, lane));
+        }
       }
     }
     if (!live) continue;
     if (lg_fb <= 8) {
       // four consecutive values of one 128-group: one 8-byte store
-      typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
       const half4_t hv = {(_Float16)(v[0] * sc), (_Float16)(v[1] * sc), (_Float16)(v[2] * sc),
                           (_Float16)(v[3] * sc)};
       *reinterpret_cast<half4_t*>(lds + b * RS + (k >> 7) * kSliceBytes + (k & 127) * 2) = hv;
@@ -608,7 +675,7 @@ __global__ __launch_bounds__(NW * 64) void gemv_kernel(
     XPre<XP> xp;
     XRot xr;
     if constexpr (rot)
-      rot_preload<NW>(xr, xrs, K, B, k0, kw, tid);
+      rot_preload<NW>(xr, xrs, K, B, k0, kw, fwht_block, tid);
     else
       x_preload<NT, XP>(xp, xg, K, k0, per_row, B * per_row, row_of, tid);
     if constexpr (MODE != kFlat) {
@@ -758,7 +825,7 @@ __global__ __launch_bounds__(NW * 64) void rotate_kernel(const uint16_t* __restr
   const rsrc_t xrs = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(xrow), (short)0,
                                                        K * 2, kRsrcWord3);
   XRot xr;
-  rot_preload<NW>(xr, xrs, K, 1, k0, kw, tid);
+  rot_preload<NW>(xr, xrs, K, 1, k0, kw, fb, tid);
   stage_fwht<NW>(lds, F, xr, xrs, K, 1, k0, kw, nsl, RS, fb, sc, tid);
   __syncthreads();
   uint16_t* orow = xo + (int64_t)b * K + k0;
