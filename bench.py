@@ -324,6 +324,174 @@ def cpu_model() -> str:
     return platform.processor() or platform.machine()
 
 
+PHASES = {  # lane index in the diagnostic build's per-wave record -> phase
+    1: "x loads issued", 2: "x arrived", 3: "first unit issued", 4: "first 256 points done",
+    5: "phase barrier", 6: "rotation done", 7: "x staged (barrier)", 12: "slice 1 staged",
+    13: "slice 2 staged", 8: "first unit done", 14: "slice 0 loop end",
+    15: "slice 1 loop end", 9: "last loop end", 10: "final barrier", 11: "end",
+}
+
+
+def phase_trace(name: str, calls: int, packer: str) -> dict:
+    """Per-wave phase timestamps of the GEMV on workload ``name``, from the diagnostic copy
+    of the library (``libfourbit_trace.so``, built with FB_PHASE_TRACE: each wave records a
+    100 MHz chip-wide clock at fixed points of the kernel).  ``calls`` traced calls run back
+    to back after the usual warm-up, on cold weight copies; times are relative to the
+    call's first wave start.  Also: each workgroup's end (its last wave's), grouped by the
+    XCD it ran on, and the gap between one call's last end and the next call's first
+    start."""
+    tl = ctypes.CDLL(str(ROOT / "if_i_could_turn_back_time_amd" / "libfourbit_trace.so"))
+    vp = ctypes.c_void_p
+    tl.fb_gemv.restype = ctypes.c_int
+    tl.fb_gemv.argtypes = [vp, vp, vp, ctypes.POINTER(C.FbShape), vp, ctypes.c_size_t, vp]
+    tl.fb_phase_trace_set.argtypes = [vp, ctypes.c_size_t]
+    ip = ctypes.POINTER(ctypes.c_int)
+    tl.fb_phase_plan.argtypes = [ctypes.POINTER(C.FbShape), ip, ip, ip, ip, ip]
+    fmt, K, N, B, kind, fwht = WORKLOADS[name]
+    xdt = torch.float16 if fmt in ("gf4", "int4ref") else torch.bfloat16
+    w, x = workloads.synth(kind, N, K, B, xdt)
+    fb = fwht_block_for(K) if fwht else 0
+    if fmt == "int4ref":
+        sc = w.abs().amax(dim=1, keepdim=True) / 7 + 1e-12
+        pw = PackedWeight.from_levels(torch.floor(w / sc), sc.reshape(-1), device="cuda:0")
+    else:
+        pw = PackedWeight.quantize(w, fmt, fwht_block=fb, device="cuda:0", packer=packer)
+    xd = x.to("cuda:0")
+    y = torch.empty(B, N, dtype=xdt, device="cuda:0")
+    shape = pw.shape(B, xd.dtype, y.dtype)
+    ws = C.new_workspace(shape, xd.device)
+    wsp, nws = (ws.data_ptr(), ws.numel()) if ws is not None else (None, 0)
+    # with a workspace the GEMV runs unrotated on the rotated x: that is the plan traced
+    launched = C.make_shape(N, K, B, pw.fmt, 0 if ws is not None else fb,
+                            C.DTYPE_CODE[xd.dtype], C.DTYPE_CODE[y.dtype])
+    plan = [ctypes.c_int() for _ in range(5)]
+    C.check(tl.fb_phase_plan(ctypes.byref(launched), *[ctypes.byref(v) for v in plan]))
+    grid, nw, S, tq, tr = (v.value for v in plan)
+    ncp = n_copies(pw.wdev.numel(), True)
+    copies = [pw.wdev] + [pw.wdev.clone() for _ in range(ncp - 1)]
+    sref = ctypes.byref(shape)
+    sp = torch.cuda.current_stream().cuda_stream
+    per_call = grid * nw * 64
+    bufs = torch.zeros(calls, per_call, dtype=torch.int64, device="cuda:0")
+
+    def run(f, n, traced=False):
+        for i in range(n):
+            if traced:
+                tl.fb_phase_trace_set(bufs[i].data_ptr(), per_call)
+            C.check(f(copies[i % ncp].data_ptr(), xd.data_ptr(), y.data_ptr(), sref, wsp, nws, sp))
+        if traced:
+            tl.fb_phase_trace_set(None, 0)
+
+    def timed(f, n=200):
+        run(f, PRE_CALLS)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        run(f, n)
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / n * 1e3
+
+    t_end = time.perf_counter() + MIN_WARM_S
+    while time.perf_counter() < t_end:
+        run(tl.fb_gemv, 50)
+        torch.cuda.synchronize()
+    run(tl.fb_gemv, PRE_CALLS)
+    run(tl.fb_gemv, calls, traced=True)
+    torch.cuda.synchronize()
+    us_traced_lib = timed(tl.fb_gemv)
+    us_product = timed(C.lib().fb_gemv)
+    t = bufs.cpu().numpy().astype(np.int64).reshape(calls, grid, nw, 64)
+    del bufs, copies
+    start = t[..., 0]
+    g0 = start.reshape(calls, -1).min(axis=1)[:, None, None]
+    us = lambda v: v / 100.0  # 100 MHz ticks -> us
+
+    def stats(v):
+        return {"median": round(float(np.median(v)), 3), "p90": round(float(np.percentile(v, 90)), 3),
+                "max": round(float(v.max()), 3)}
+
+    phases = {"wave start": stats(us(start - g0))}
+    for i, label in PHASES.items():
+        v = t[..., i]
+        ok = v != 0
+        if not ok.any():
+            continue
+        phases[label] = dict(stats(us((v - g0)[ok])),
+                             from_own_start_median=round(float(np.median(us((v - start)[ok]))), 3))
+    wg_end = us(t[..., 11].max(axis=2) - g0[:, :, 0])            # [calls, grid]
+    xcc = t[:, :, 0, 16] & 0xF                                    # [calls, grid]
+    xcd_med = np.array([[np.median(wg_end[c][xcc[c] == k]) if (xcc[c] == k).any() else np.nan
+                         for k in range(8)] for c in range(calls)])
+    span = wg_end.max(axis=1)
+    gaps = [us(start[c + 1].min() - t[c, ..., 11].max()) for c in range(calls - 1)]
+    period = [us(start[c + 1].min() - start[c].min()) for c in range(calls - 1)]
+    return {
+        "phase_trace": name, "calls": calls, "plan": {"grid": grid, "waves": nw, "slices": S,
+                                                      "tiles_per_wg": tq, "wgs_with_one_more": tr},
+        "rotate_once": ws is not None,
+        "us_per_call_untraced": round(us_product, 3), "us_per_call_trace_build": round(us_traced_lib, 3),
+        "phases_us_from_call_start": phases,
+        "workgroup_end_us": dict(stats(wg_end), p10=round(float(np.percentile(wg_end, 10)), 3),
+                                 min=round(float(wg_end.min()), 3)),
+        "first_start_to_last_end_us_median": round(float(np.median(span)), 3),
+        "xcd_median_end_us_per_call": [[round(float(v), 2) for v in row] for row in xcd_med],
+        "slowest_xcd_per_call": [int(np.nanargmax(row)) for row in xcd_med],
+        "xcd_spread_us_median": round(float(np.median(np.nanmax(xcd_med, 1) - np.nanmin(xcd_med, 1))), 3),
+        "gap_last_end_to_next_start_us": stats(np.array(gaps)) if gaps else None,
+        "start_to_next_start_us": stats(np.array(period)) if period else None,
+    }
+
+
+def jenks2_bench(n: int, steps: int) -> dict:
+    """Two-class natural breaks (fb_jenks2_gpu) over n resident fp32 values: sort, blocked
+    fp64 prefix sums, SSD per split, first argmin, mask.  Timed with HIP events over
+    back-to-back calls on one preallocated workspace; the host twin (fb_jenks2_host, one
+    thread) runs once on the same values and must give the same split, GVF and mask."""
+    L = C.lib()
+    g = torch.Generator().manual_seed(7)
+    w = (torch.randn(n, generator=g) * 0.05)
+    wd = w.to("cuda:0")
+    need = ctypes.c_size_t(0)
+    C.check(L.fb_jenks2_workspace(n, ctypes.byref(need)))
+    ws = torch.empty(need.value + 256, dtype=torch.uint8, device="cuda:0")
+    wsp = ws.data_ptr() + (-ws.data_ptr()) % 256
+    keep = torch.empty(n, dtype=torch.uint8, device="cuda:0")
+    out = torch.empty(2, dtype=torch.float64, device="cuda:0")
+    sp = torch.cuda.current_stream().cuda_stream
+
+    def call():
+        C.check(L.fb_jenks2_gpu(wd.data_ptr(), n, keep.data_ptr(), out.data_ptr(),
+                                out.data_ptr() + 8, wsp, need.value, sp))
+
+    t_end = time.perf_counter() + MIN_WARM_S
+    while time.perf_counter() < t_end:
+        for _ in range(5):
+            call()
+        torch.cuda.synchronize()
+    regions = []
+    for _ in range(5):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        call()
+        e0.record()
+        for _ in range(steps):
+            call()
+        e1.record()
+        torch.cuda.synchronize()
+        regions.append(e0.elapsed_time(e1) / steps * 1e3)
+    host = out.cpu()
+    split = int(host[:1].view(torch.int64).item())
+    t = time.perf_counter()
+    hk, hsplit, hgvf = C.jenks2_host(w)
+    host_s = time.perf_counter() - t
+    same = (hsplit == split and hgvf == float(host[1].item())
+            and torch.equal(hk, keep.cpu().bool()))
+    us = float(np.median(regions))
+    return {"jenks2_values": n, "us_per_call_median": us, "us_per_call_regions": regions,
+            "values_per_s": n / (us * 1e-6), "workspace_bytes": need.value,
+            "split": split, "gvf": float(host[1].item()), "host_twin_s": host_s,
+            "host_twin_threads": 1, "identical_to_host": bool(same)}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -342,6 +510,11 @@ def main():
                     help="also time one weight copy (Infinity-Cache warm) and a HIP graph")
     ap.add_argument("--calib-copy", type=int, default=0, metavar="BYTES",
                     help="only run device-to-device copies of BYTES bytes (PMC calibration)")
+    ap.add_argument("--phase-trace", action="store_true",
+                    help="only trace the GEMV's phases on --workload (diagnostic library) and "
+                         "print a JSON summary")
+    ap.add_argument("--jenks2", type=int, default=0, metavar="N",
+                    help="only time the two-class Jenks mask (fb_jenks2_gpu) over N values")
     args = ap.parse_args()
     if args.calib_copy:
         # a plain copy kernel of known size: FETCH_SIZE / WRITE_SIZE per dispatch of it
@@ -361,6 +534,12 @@ def main():
     if not torch.cuda.is_available():
         print("bench.py: no ROCm GPU visible", file=sys.stderr)
         sys.exit(1)
+    if args.phase_trace:
+        print(json.dumps(phase_trace(args.workload, 20, args.packer)))
+        return
+    if args.jenks2:
+        print(json.dumps(jenks2_bench(args.jenks2, min(args.steps, 50))))
+        return
 
     if args.sweep:
         Path(args.sweep_out).parent.mkdir(parents=True, exist_ok=True)

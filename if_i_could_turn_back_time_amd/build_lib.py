@@ -1,5 +1,7 @@
 """Builds libfourbit.so in-tree: hipcc for the gfx950 kernels, g++ for the host packers;
-then ``tests/c/abi_gpu``, the GPU tests' native caller of the library's C ABI.
+then ``tests/c/abi_gpu``, the GPU tests' native caller of the library's C ABI, and
+``libfourbit_trace.so``, a diagnostic copy of the library whose GEMV also records per-wave
+phase timestamps (``FB_PHASE_TRACE``; read by ``bench.py --phase-trace``).
 
 Run as ``python -m if_i_could_turn_back_time_amd.build_lib`` (``__graft_entry__.build()``
 calls :func:`build`).  Always recompiles.  Objects go to ``_build/`` at the repo root;
@@ -11,6 +13,7 @@ import os
 import shutil
 import subprocess
 import sys
+from concurrent.futures import ThreadPoolExecutor
 from pathlib import Path
 
 PKG = Path(__file__).resolve().parent
@@ -19,6 +22,7 @@ CSRC = PKG / "csrc"
 INCLUDE = ROOT / "include"
 BUILD = ROOT / "_build"
 LIB = PKG / "libfourbit.so"
+TRACE_LIB = PKG / "libfourbit_trace.so"
 C_TESTS = ROOT / "tests" / "c"
 ARCH = "gfx950"
 
@@ -63,6 +67,7 @@ def build(verbose: bool = False) -> Path:
     gemv_o = BUILD / "fourbit_gemv.o"
     pack_o = BUILD / "fourbit_pack.o"
     jenks2_o = BUILD / "fourbit_jenks2.o"
+    trace_o = BUILD / "fourbit_gemv_trace.o"
     steps = [
         ["g++", *HOST_FLAGS, *inc, "-c", str(CSRC / "fourbit_host.cpp"), "-o", str(host_o)],
         [_hipcc(), *HIP_FLAGS, *inc, "-c", str(CSRC / "fourbit_gemv.hip"), "-o", str(gemv_o)],
@@ -72,15 +77,24 @@ def build(verbose: bool = False) -> Path:
         # the two-class Jenks rounds every fp64 operation as its host twin does
         [_hipcc(), *HIP_FLAGS, "-ffp-contract=off", *inc, "-c", str(CSRC / "fourbit_jenks2.hip"),
          "-o", str(jenks2_o)],
+        [_hipcc(), *HIP_FLAGS, "-DFB_PHASE_TRACE", *inc, "-c", str(CSRC / "fourbit_gemv.hip"),
+         "-o", str(trace_o)],
     ]
-    tmp = LIB.with_suffix(".so.tmp")
-    steps.append([_hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", str(host_o), str(gemv_o),
-                  str(pack_o), str(jenks2_o), "-o", str(tmp), "-lpthread"])
     for cmd in steps:
         if verbose:
             print(" ".join(cmd), flush=True)
-        _run(cmd)
-    os.replace(tmp, LIB)
+    # the translation units are independent: compile them side by side
+    with ThreadPoolExecutor(max_workers=len(steps)) as ex:
+        for f in [ex.submit(_run, cmd) for cmd in steps]:
+            f.result()
+    for lib, kern_o in ((LIB, gemv_o), (TRACE_LIB, trace_o)):
+        tmp = lib.with_suffix(".so.tmp")
+        link = [_hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", str(host_o), str(kern_o),
+                str(pack_o), str(jenks2_o), "-o", str(tmp), "-lpthread"]
+        if verbose:
+            print(" ".join(link), flush=True)
+        _run(link)
+        os.replace(tmp, lib)
     # the GPU test suite's native (no Python) caller of the C ABI, linked to the library
     # through a path relative to itself, so that it runs wherever the tree is copied
     caller = [_hipcc(), *HIP_FLAGS, f"-I{INCLUDE}", str(C_TESTS / "abi_gpu.cpp"), "-o",

@@ -263,6 +263,59 @@ __device__ void stage_plain(uint8_t* lds, const XPre<XP>& xp, const uint16_t* __
   }
 }
 
+// ---------------------------------------------------------------------------------
+// Phase timestamps, compiled in only for the diagnostic library (FB_PHASE_TRACE,
+// libfourbit_trace.so): lane i of each wave keeps the s_memrealtime value (a 100 MHz
+// clock common to the chip) at which the wave passed phase i; at the end of the kernel each
+// wave writes its 64 values to the buffer given to fb_phase_trace_set, at
+// ((blockIdx.x * NW + wave) * 64 + lane).  Lane 16 holds the XCC (XCD) id and lane 17 the
+// slice count.  Each mark waits for the wave's outstanding LDS and scalar operations (the
+// counter read goes through the scalar memory path), so traced timings run a little long.
+// ---------------------------------------------------------------------------------
+enum {
+  kPhStart = 0, kPhXIssued = 1, kPhXArrived = 2, kPhU0Issued = 3, kPhStages07 = 4,
+  kPhPhaseBar = 5, kPhStages811 = 6, kPhStaged = 7, kPhUnit0 = 8, kPhLoopEnd = 9,
+  kPhFinalBar = 10, kPhEnd = 11, kPhStaged1 = 12, kPhStaged2 = 13, kPhSliceEnd0 = 14,
+  kPhSliceEnd1 = 15, kPhXcc = 16, kPhSlices = 17
+};
+#ifdef FB_PHASE_TRACE
+struct Phases {
+  unsigned lo = 0, hi = 0;
+  __device__ __forceinline__ void put(int i, unsigned long long t) {
+    const bool me = (int)(threadIdx.x & 63) == i;
+    lo = me ? (unsigned)t : lo;
+    hi = me ? (unsigned)(t >> 32) : hi;
+  }
+  __device__ __forceinline__ void mark(int i) { put(i, __builtin_amdgcn_s_memrealtime()); }
+  __device__ __forceinline__ void flush(int nw, unsigned long long* buf) {
+    put(kPhXcc, __builtin_amdgcn_s_getreg(20 | (15 << 11)));  // HW_REG_XCC_ID
+    const size_t i = ((size_t)blockIdx.x * nw + (threadIdx.x >> 6)) * 64 + (threadIdx.x & 63);
+    if (buf) buf[i] = ((unsigned long long)hi << 32) | lo;
+  }
+};
+// Host side: the buffer the next launches write to (fb_phase_trace_set), and its size.
+unsigned long long* g_phase_host = nullptr;
+size_t g_phase_entries = 0;
+// The marks are macros so that the product build's code is exactly what it is without them.
+#define PH_DECL Phases ph;
+#define PH_PARAM , Phases& ph
+#define PH_ARG , ph
+#define PH_MARK(i) ph.mark(i)
+#define PH_PUT(i, v) ph.put(i, v)
+#define PH_FLUSH(nw) ph.flush(nw, phase_buf)
+#define PH_KPARAM , unsigned long long* __restrict__ phase_buf
+#define PH_KARG(n) , (g_phase_entries >= (size_t)(n) ? g_phase_host : nullptr)
+#else
+#define PH_DECL
+#define PH_PARAM
+#define PH_ARG
+#define PH_MARK(i) ((void)0)
+#define PH_PUT(i, v) ((void)0)
+#define PH_FLUSH(nw) ((void)0)
+#define PH_KPARAM
+#define PH_KARG(n)
+#endif
+
 // Blockwise normalised FWHT (fp32 butterflies) of x[b, k0 : k0+kw] into the staged
 // layout (rounded to fp16); kw is a whole number of blocks of fb.
 //  - Stages 0..7 run in registers.  The B*kw values are cut into 256-value sub-blocks,
@@ -386,7 +439,8 @@ __device__ __forceinline__ f32x4 fwht256_mfma(uint2 raw, const H16Ops& h) {
 
 template <int NW>
 __device__ void stage_fwht(uint8_t* lds, float* F, const XRot& xr, rsrc_t xrs, int K, int B,
-                           int k0, int kw, int nsl, int RS, int fb, float sc, int tid) {
+                           int k0, int kw, int nsl, int RS, int fb, float sc,
+                           int tid PH_PARAM) {
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
   const int lg_fb = 31 - __builtin_clz(fb);
   const int nsb = (kw + 255) >> 8;  // 256-value sub-blocks per batch row
@@ -458,8 +512,10 @@ __device__ void stage_fwht(uint8_t* lds, float* F, const XRot& xr, rsrc_t xrs, i
       *reinterpret_cast<f32x4*>(F + fpad(p)) = f32x4{v[0], v[1], v[2], v[3]};
     }
   }
+  PH_MARK(kPhStages07);
   if (lg_fb > 8) {
     __syncthreads();
+    PH_MARK(kPhPhaseBar);
     const int total = B * kw;
     const float inv_kw = 1.0f / (float)kw;
     const int npieces = ((total + 4095) >> 12) << 4;  // (4096-value piece, column group)
@@ -512,6 +568,7 @@ __device__ void stage_fwht(uint8_t* lds, float* F, const XRot& xr, rsrc_t xrs, i
       }
     }
   }
+  PH_MARK(kPhStages811);
   // zeros past the rotated width (the weight stream is zero there too)
   const int width = nsl * 128;
   for (int t = tid; t < B * ((width - kw) >> 3); t += NW * 64) {
@@ -576,8 +633,10 @@ template <int FMT, int XDT, int MODE, int NW, int XP>
 __global__ __launch_bounds__(NW * 64) void gemv_kernel(
     const uint8_t* __restrict__ w, const void* __restrict__ x, int K, int B, int SPL, int GS,
     int tq, int tr, unsigned spl_m, int S, int fwht_block, int RS, float fwht_scale,
-    void* __restrict__ y, int N, int ydt) {
+    void* __restrict__ y, int N, int ydt PH_KPARAM) {
   extern __shared__ __align__(16) uint8_t lds[];
+  PH_DECL
+  PH_MARK(kPhStart);
   const int xbytes = x_lds_bytes(B, K, SPL, fwht_block);  // staged x; the slots follow
   constexpr int BB = FMT == FB_FMT_GF4 ? fb::kGf4BlockBytes : fb::kE2m1BlockBytes;
   constexpr int NT = NW * 64;
@@ -678,6 +737,7 @@ __global__ __launch_bounds__(NW * 64) void gemv_kernel(
       rot_preload<NW>(xr, xrs, K, B, k0, kw, fwht_block, tid);
     else
       x_preload<NT, XP>(xp, xg, K, k0, per_row, B * per_row, row_of, tid);
+    if (s == 0) PH_MARK(kPhXIssued);
     if constexpr (MODE != kFlat) {
       if (s == nslices - 1 && spl_last != SPL) {  // a last slice with fewer spans
         sp = spl_last;
@@ -689,7 +749,9 @@ __global__ __launch_bounds__(NW * 64) void gemv_kernel(
     // the rotation cannot start before its x has arrived, and x loads queued behind the
     // first weight unit arrive later: wait for x first
     if constexpr (rot) __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+    if (rot && s == 0) PH_MARK(kPhXArrived);
     issue(s, u0, ring[0]);
+    if (s == 0) PH_MARK(kPhU0Issued);
     // The next slice's x (into registers) and first weight unit are requested before the
     // barrier that closes the previous slice, so their latency overlaps the slowest wave.
     if (s > 0) {  // every wave is done with the previous slice: x may be restaged
@@ -702,13 +764,15 @@ __global__ __launch_bounds__(NW * 64) void gemv_kernel(
     }
     if constexpr (rot)
       stage_fwht<NW>(xst, reinterpret_cast<float*>(xst + B * RS), xr, xrs, K, B, k0, kw, nsl, RS,
-                 fwht_block, fwht_scale, tid);
+                 fwht_block, fwht_scale, tid PH_ARG);
     else
       stage_plain<NT, XP>(xst, xp, xg, K, B, k0, nsl, RS, row_of, tid);
     __syncthreads();  // x staged, counter set
+    PH_MARK(s == 0 ? kPhStaged : s == 1 ? kPhStaged1 : kPhStaged2);
     issue(s, u1, ring[1]);
     __builtin_amdgcn_sched_barrier(0);  // keep the prefetch ahead of the compute
     if (u0 < nu) process(ring[0], s, u0);
+    if (s == 0) PH_MARK(kPhUnit0);
     int un = grab();
     for (;;) {
       u0 = __builtin_amdgcn_readfirstlane(un);
@@ -724,8 +788,10 @@ __global__ __launch_bounds__(NW * 64) void gemv_kernel(
       if (u0 >= nu) break;
       process(ring[0], s, u0);
     }
+    PH_MARK(s == nslices - 1 ? kPhLoopEnd : s == 0 ? kPhSliceEnd0 : kPhSliceEnd1);
   }
   __syncthreads();  // every slice done: slots are complete
+  PH_MARK(kPhFinalBar);
 
   // y[col][row] = sum over the spans of the tile, in span order
   const int nt = t1 - t0;
@@ -740,6 +806,9 @@ __global__ __launch_bounds__(NW * 64) void gemv_kernel(
     for (int j = 0; j < SPL; ++j) sum += sl[(size_t)j * 4 * B][r & 3];
     if (row < N) store_y(y, (int64_t)c * N + row, sum, ydt);
   }
+  PH_MARK(kPhEnd);
+  PH_PUT(kPhSlices, (unsigned long long)nslices);
+  PH_FLUSH(NW);
 }
 
 // ---------------------------------------------------------------------------------
@@ -825,8 +894,9 @@ __global__ __launch_bounds__(NW * 64) void rotate_kernel(const uint16_t* __restr
   const rsrc_t xrs = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(xrow), (short)0,
                                                        K * 2, kRsrcWord3);
   XRot xr;
+  PH_DECL  // not written out: the trace covers the GEMV
   rot_preload<NW>(xr, xrs, K, 1, k0, kw, fb, tid);
-  stage_fwht<NW>(lds, F, xr, xrs, K, 1, k0, kw, nsl, RS, fb, sc, tid);
+  stage_fwht<NW>(lds, F, xr, xrs, K, 1, k0, kw, nsl, RS, fb, sc, tid PH_ARG);
   __syncthreads();
   uint16_t* orow = xo + (int64_t)b * K + k0;
   for (int t = tid; t < kw / 8; t += NW * 64) {
@@ -947,7 +1017,7 @@ int launch_gemv(const void* wdev, const void* x, void* y, const fb_shape_t* s, c
                      static_cast<const uint8_t*>(wdev), x, s->K, s->B, pl.SPL, pl.GS, pl.tq,
                      pl.tr, div_magic(pl.SPL), pl.S, s->fwht_block, x_row_stride(pl.SPL * 4),
                      fwht_scale(s->fwht_block), y,
-                     s->N, s->y_dtype);
+                     s->N, s->y_dtype PH_KARG((size_t)pl.grid * NW * 64));
   return hipGetLastError() == hipSuccess ? FB_OK : FB_ERR_HIP;
 }
 
@@ -1125,5 +1195,32 @@ int fb_dequant(const void* wdev, void* w_out, int32_t out_dtype, const fb_shape_
                        static_cast<const uint8_t*>(wdev), w_out, s->N, s->K, out_dtype);
   return hipGetLastError() == hipSuccess ? FB_OK : FB_ERR_HIP;
 }
+
+#ifdef FB_PHASE_TRACE
+// Diagnostic library only.  The buffer (device memory, `entries` 64-bit values) that the
+// following GEMV launches write their phase timestamps to, or null for none.  A launch
+// whose grid needs more entries writes nothing.  Not for concurrent use.
+int fb_phase_trace_set(void* buf, size_t entries) {
+  g_phase_host = static_cast<unsigned long long*>(buf);
+  g_phase_entries = buf ? entries : 0;
+  return FB_OK;
+}
+
+// The launch plan fb_gemv uses for a shape on the current device: workgroups, waves per
+// workgroup, K-slices, row tiles per workgroup (the first tr take one more).
+int fb_phase_plan(const fb_shape_t* s, int* grid, int* waves, int* slices, int* tq, int* tr) {
+  if (!s || !grid || !waves || !slices || !tq || !tr) return FB_ERR_NULL;
+  const int st = fb_validate(s);
+  if (st != FB_OK) return st;
+  Plan pl;
+  if (!make_plan(s, device_cus(), pl)) return FB_ERR_LDS;
+  *grid = pl.grid;
+  *waves = pl.nw;
+  *slices = pl.S;
+  *tq = pl.tq;
+  *tr = pl.tr;
+  return FB_OK;
+}
+#endif
 
 }  // extern "C"

@@ -27,8 +27,8 @@ def say(*a):
 
 
 def within_tol(y, yref, extra_rel=0.0):
-    y = y.float().cpu()
-    yref = yref.float().cpu()
+    y = y.detach().float().cpu()
+    yref = yref.detach().float().cpu()
     err = (y - yref).abs()
     bound = ATOL + (RTOL + extra_rel) * yref.abs()
     return bool((err <= bound).all()), float(err.max()), float((err / (yref.abs() + 1e-6)).max())
