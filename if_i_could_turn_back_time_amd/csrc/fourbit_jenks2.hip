@@ -216,11 +216,21 @@ __global__ void j2_final(const double* __restrict__ smin, const int* __restrict_
   *gvf = (t - best) / (t + 1e-8);
 }
 
-// keep[index of sorted position t] = t >= split
-__global__ void j2_mask(const int* __restrict__ order, int n, const int64_t* __restrict__ split,
+// keep[i] = 1 when w[i] sits at a sorted position >= split.  With t the value at position
+// split: every value above t is kept and every value below is not; values equal to t sit in
+// index order (the sort is stable), so of those the ones at index >= order[split] are kept.
+// A streaming pass over w, not a scatter through the permutation.  (-0.0 == +0.0 as floats,
+// as in the sort's keys.)
+__global__ void j2_mask(const float* __restrict__ w, const float* __restrict__ skeys,
+                        const int* __restrict__ order, int n, const int64_t* __restrict__ split,
                         uint8_t* __restrict__ keep) {
-  const int t = blockIdx.x * blockDim.x + threadIdx.x;
-  if (t < n) keep[order[t]] = (int64_t)t >= *split ? 1 : 0;
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  const int64_t sp = *split;
+  const float t = skeys[sp];
+  const int it = order[sp];
+  const float v = w[i];
+  keep[i] = (v > t || (v == t && i >= it)) ? 1 : 0;
 }
 
 int grid_of(int64_t items, int threads) { return (int)((items + threads - 1) / threads); }
@@ -282,7 +292,8 @@ int fb_jenks2_gpu(const float* w, int64_t n, uint8_t* keep, int64_t* split, doub
   hipLaunchKernelGGL(j2_min_super, dim3(grid_of(nsup, 64)), dim3(64), 0, hs, bmin, bidx, nblk, nsup,
                      smin, sidx);
   hipLaunchKernelGGL(j2_final, dim3(1), dim3(1), 0, hs, smin, sidx, nsup, ssd0, split, gvf);
-  hipLaunchKernelGGL(j2_mask, dim3(grid_of(n, 256)), dim3(256), 0, hs, vals_out, ni, split, keep);
+  hipLaunchKernelGGL(j2_mask, dim3(grid_of(n, 256)), dim3(256), 0, hs, w, keys_out, vals_out, ni,
+                     split, keep);
   return hipGetLastError() == hipSuccess ? FB_OK : FB_ERR_HIP;
 }
 
