@@ -95,6 +95,12 @@ __device__ __forceinline__ double centre(const float* __restrict__ s, int n) {
   return (double)s[n / 2];
 }
 
+// The serial sums below keep the fixed association order; what changes between kernels is
+// only how the operands reach the thread.  A thread that walks one block reads it in
+// 16-value pieces, one contiguous 64-byte read per lane (lanes are a block apart, so
+// single-value reads would touch 64 lines per instruction for 4 bytes each).
+constexpr int kPiece = 16;
+
 // Block totals of d and q: one thread per block of kBlk sorted values.
 __global__ void j2_block_totals(const float* __restrict__ s, int n, int nblk,
                                 double* __restrict__ t1, double* __restrict__ t2) {
@@ -103,7 +109,21 @@ __global__ void j2_block_totals(const float* __restrict__ s, int n, int nblk,
   const double c = centre(s, n);
   const int i0 = b * kBlk, i1 = min(n, i0 + kBlk);
   double a1 = 0.0, a2 = 0.0;
-  for (int i = i0; i < i1; ++i) {
+  int i = i0;
+  for (; i + kPiece <= i1; i += kPiece) {
+    float f[kPiece];
+#pragma unroll
+    for (int r = 0; r < kPiece / 4; ++r)
+      *reinterpret_cast<float4*>(f + 4 * r) = reinterpret_cast<const float4*>(s + i)[r];
+#pragma unroll
+    for (int e = 0; e < kPiece; ++e) {
+      const double d = (double)f[e] - c;
+      const double q = d * d;
+      a1 = a1 + d;
+      a2 = a2 + q;
+    }
+  }
+  for (; i < i1; ++i) {
     const double d = (double)s[i] - c;
     const double q = d * d;
     a1 = a1 + d;
@@ -113,7 +133,8 @@ __global__ void j2_block_totals(const float* __restrict__ s, int n, int nblk,
   t2[b] = a2;
 }
 
-// Exclusive block prefixes within each superblock and the superblock totals.
+// Exclusive block prefixes within each superblock and the superblock totals: one thread per
+// superblock, reading and writing 4 blocks' values at a time.
 __global__ void j2_super(const double* __restrict__ t1, const double* __restrict__ t2, int nblk,
                          int nsup, double* __restrict__ bx1, double* __restrict__ bx2,
                          double* __restrict__ u1, double* __restrict__ u2) {
@@ -121,7 +142,26 @@ __global__ void j2_super(const double* __restrict__ t1, const double* __restrict
   if (s >= nsup) return;
   const int b0 = s * kSup, b1 = min(nblk, b0 + kSup);
   double a1 = 0.0, a2 = 0.0;
-  for (int b = b0; b < b1; ++b) {
+  int b = b0;
+  for (; b + 4 <= b1; b += 4) {
+    double v1[4], v2[4], o1[4], o2[4];
+    *reinterpret_cast<double2*>(v1) = reinterpret_cast<const double2*>(t1 + b)[0];
+    *reinterpret_cast<double2*>(v1 + 2) = reinterpret_cast<const double2*>(t1 + b)[1];
+    *reinterpret_cast<double2*>(v2) = reinterpret_cast<const double2*>(t2 + b)[0];
+    *reinterpret_cast<double2*>(v2 + 2) = reinterpret_cast<const double2*>(t2 + b)[1];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      o1[e] = a1;
+      o2[e] = a2;
+      a1 = a1 + v1[e];
+      a2 = a2 + v2[e];
+    }
+    reinterpret_cast<double2*>(bx1 + b)[0] = *reinterpret_cast<double2*>(o1);
+    reinterpret_cast<double2*>(bx1 + b)[1] = *reinterpret_cast<double2*>(o1 + 2);
+    reinterpret_cast<double2*>(bx2 + b)[0] = *reinterpret_cast<double2*>(o2);
+    reinterpret_cast<double2*>(bx2 + b)[1] = *reinterpret_cast<double2*>(o2 + 2);
+  }
+  for (; b < b1; ++b) {
     bx1[b] = a1;
     bx2[b] = a2;
     a1 = a1 + t1[b];
@@ -131,19 +171,37 @@ __global__ void j2_super(const double* __restrict__ t1, const double* __restrict
   u2[s] = a2;
 }
 
-// Exclusive superblock prefixes; sx[nsup] is the total.  One thread.
-__global__ void j2_top(const double* __restrict__ u1, const double* __restrict__ u2, int nsup,
-                       double* __restrict__ sx1, double* __restrict__ sx2) {
-  if (blockIdx.x != 0 || threadIdx.x != 0) return;
+// Exclusive superblock prefixes; sx[nsup] is the total.  The workgroup stages the superblock
+// totals through LDS in chunks; thread 0 runs the sequential sums from there.
+constexpr int kTopThreads = 256;
+constexpr int kTopChunk = 2048;
+__global__ __launch_bounds__(kTopThreads) void j2_top(const double* __restrict__ u1,
+                                                      const double* __restrict__ u2, int nsup,
+                                                      double* __restrict__ sx1,
+                                                      double* __restrict__ sx2) {
+  __shared__ double l1[kTopChunk], l2[kTopChunk];
   double a1 = 0.0, a2 = 0.0;
-  for (int s = 0; s < nsup; ++s) {
-    sx1[s] = a1;
-    sx2[s] = a2;
-    a1 = a1 + u1[s];
-    a2 = a2 + u2[s];
+  for (int base = 0; base < nsup; base += kTopChunk) {
+    const int m = min(kTopChunk, nsup - base);
+    for (int i = threadIdx.x; i < m; i += kTopThreads) {
+      l1[i] = u1[base + i];
+      l2[i] = u2[base + i];
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      for (int i = 0; i < m; ++i) {
+        sx1[base + i] = a1;
+        sx2[base + i] = a2;
+        a1 = a1 + l1[i];
+        a2 = a2 + l2[i];
+      }
+    }
+    __syncthreads();
   }
-  sx1[nsup] = a1;
-  sx2[nsup] = a2;
+  if (threadIdx.x == 0) {
+    sx1[nsup] = a1;
+    sx2[nsup] = a2;
+  }
 }
 
 // The SSD of every split of one block, and the block's first minimum.
@@ -162,58 +220,95 @@ __global__ void j2_ssd(const float* __restrict__ s, int n, int nblk, int nsup,
   double l1 = 0.0, l2 = 0.0;
   double best = 0.0;
   int arg = -1;
-  for (int i = i0; i < i1; ++i) {
+  auto step = [&](int i, float v) {
     const double p = base1 + l1, q = base2 + l2;
     const double left = i == 0 ? 0.0 : q - (p * p) / (double)i;
     const double rp = pt - p;
     const double right = (qt - q) - (rp * rp) / (double)(n - i);
-    const double v = left + right;
-    if (arg < 0 || v < best) {
-      best = v;
+    const double sv = left + right;
+    if (arg < 0 || sv < best) {
+      best = sv;
       arg = i;
     }
-    if (i == 0) *ssd0 = v;
-    const double d = (double)s[i] - c;
+    if (i == 0) *ssd0 = sv;
+    const double d = (double)v - c;
     const double dq = d * d;
     l1 = l1 + d;
     l2 = l2 + dq;
+  };
+  int i = i0;
+  for (; i + kPiece <= i1; i += kPiece) {
+    float f[kPiece];
+#pragma unroll
+    for (int r = 0; r < kPiece / 4; ++r)
+      *reinterpret_cast<float4*>(f + 4 * r) = reinterpret_cast<const float4*>(s + i)[r];
+#pragma unroll
+    for (int e = 0; e < kPiece; ++e) step(i + e, f[e]);
   }
+  for (; i < i1; ++i) step(i, s[i]);
   bmin[b] = best;
   bidx[b] = arg;
 }
 
-// First minimum over the blocks of each superblock.
-__global__ void j2_min_super(const double* __restrict__ bmin, const int* __restrict__ bidx,
-                             int nblk, int nsup, double* __restrict__ smin,
-                             int* __restrict__ sidx) {
-  const int s = blockIdx.x * blockDim.x + threadIdx.x;
-  if (s >= nsup) return;
+// (value, index) pairs in the order "first index of the minimum": a smaller value wins, an
+// equal value goes to the smaller index.  Over indices that increase along the array this
+// is exactly the sequential scan with strict <, so a tree of it gives the same winner.
+__device__ __forceinline__ void lex_min(double& v, int& i, double v2, int i2) {
+  if (v2 < v || (v2 == v && i2 < i)) {
+    v = v2;
+    i = i2;
+  }
+}
+
+__device__ __forceinline__ void wave_lex_min(double& v, int& i) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) {
+    const double v2 = __shfl_xor(v, m, 64);
+    const int i2 = __shfl_xor(i, m, 64);
+    lex_min(v, i, v2, i2);
+  }
+}
+
+// First minimum over the blocks of each superblock: one wave per superblock.
+__global__ __launch_bounds__(64) void j2_min_super(const double* __restrict__ bmin,
+                                                   const int* __restrict__ bidx, int nblk,
+                                                   int nsup, double* __restrict__ smin,
+                                                   int* __restrict__ sidx) {
+  const int s = blockIdx.x;
   const int b0 = s * kSup, b1 = min(nblk, b0 + kSup);
   double best = bmin[b0];
   int arg = bidx[b0];
-  for (int b = b0 + 1; b < b1; ++b)
-    if (bmin[b] < best) {
-      best = bmin[b];
-      arg = bidx[b];
-    }
-  smin[s] = best;
-  sidx[s] = arg;
+  for (int b = b0 + (int)threadIdx.x; b < b1; b += 64) lex_min(best, arg, bmin[b], bidx[b]);
+  wave_lex_min(best, arg);
+  if (threadIdx.x == 0) {
+    smin[s] = best;
+    sidx[s] = arg;
+  }
 }
 
-__global__ void j2_final(const double* __restrict__ smin, const int* __restrict__ sidx, int nsup,
-                         const double* __restrict__ ssd0, int64_t* __restrict__ split,
-                         double* __restrict__ gvf) {
-  if (blockIdx.x != 0 || threadIdx.x != 0) return;
+constexpr int kFinalThreads = 256;
+__global__ __launch_bounds__(kFinalThreads) void j2_final(const double* __restrict__ smin,
+                                                          const int* __restrict__ sidx, int nsup,
+                                                          const double* __restrict__ ssd0,
+                                                          int64_t* __restrict__ split,
+                                                          double* __restrict__ gvf) {
+  __shared__ double lv[kFinalThreads / 64];
+  __shared__ int li[kFinalThreads / 64];
   double best = smin[0];
   int arg = sidx[0];
-  for (int s = 1; s < nsup; ++s)
-    if (smin[s] < best) {
-      best = smin[s];
-      arg = sidx[s];
-    }
-  *split = arg;
-  const double t = *ssd0;
-  *gvf = (t - best) / (t + 1e-8);
+  for (int s = threadIdx.x; s < nsup; s += kFinalThreads) lex_min(best, arg, smin[s], sidx[s]);
+  wave_lex_min(best, arg);
+  if ((threadIdx.x & 63) == 0) {
+    lv[threadIdx.x >> 6] = best;
+    li[threadIdx.x >> 6] = arg;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    for (int w = 1; w < kFinalThreads / 64; ++w) lex_min(best, arg, lv[w], li[w]);
+    *split = arg;
+    const double t = *ssd0;
+    *gvf = (t - best) / (t + 1e-8);
+  }
 }
 
 // keep[i] = 1 when w[i] sits at a sorted position >= split.  With t the value at position
@@ -286,12 +381,13 @@ int fb_jenks2_gpu(const float* w, int64_t n, uint8_t* keep, int64_t* split, doub
                      t1, t2);
   hipLaunchKernelGGL(j2_super, dim3(grid_of(nsup, 64)), dim3(64), 0, hs, t1, t2, nblk, nsup, bx1,
                      bx2, u1, u2);
-  hipLaunchKernelGGL(j2_top, dim3(1), dim3(1), 0, hs, u1, u2, nsup, sx1, sx2);
+  hipLaunchKernelGGL(j2_top, dim3(1), dim3(kTopThreads), 0, hs, u1, u2, nsup, sx1, sx2);
   hipLaunchKernelGGL(j2_ssd, dim3(grid_of(nblk, 64)), dim3(64), 0, hs, keys_out, ni, nblk, nsup,
                      bx1, bx2, sx1, sx2, bmin, bidx, ssd0);
-  hipLaunchKernelGGL(j2_min_super, dim3(grid_of(nsup, 64)), dim3(64), 0, hs, bmin, bidx, nblk, nsup,
-                     smin, sidx);
-  hipLaunchKernelGGL(j2_final, dim3(1), dim3(1), 0, hs, smin, sidx, nsup, ssd0, split, gvf);
+  hipLaunchKernelGGL(j2_min_super, dim3(nsup), dim3(64), 0, hs, bmin, bidx, nblk, nsup, smin,
+                     sidx);
+  hipLaunchKernelGGL(j2_final, dim3(1), dim3(kFinalThreads), 0, hs, smin, sidx, nsup, ssd0, split,
+                     gvf);
   hipLaunchKernelGGL(j2_mask, dim3(grid_of(n, 256)), dim3(256), 0, hs, w, keys_out, vals_out, ni,
                      split, keep);
   return hipGetLastError() == hipSuccess ? FB_OK : FB_ERR_HIP;
