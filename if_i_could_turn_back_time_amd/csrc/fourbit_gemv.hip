@@ -623,20 +623,26 @@ __device__ __forceinline__ f32x4 unit_partial(const Rec<FMT>& r, const uint8_t* 
 // first tr workgroups); GS: 512-element spans per row; RS: LDS bytes per staged x row;
 // spl_m: div_magic(SPL).
 // MODE: kFlat = one K-slice, no rotation (the common case); kSliced = several K-slices, no
-// rotation; kRotated = rotation of x.  Each is compiled with only the staging it needs, which
+// rotation; kRotated = rotation of x; kRot1 = rotation at batch 1 in one K-slice.  Each is
+// compiled with only the staging it needs, which
 // keeps the kernel short and its registers few.
-enum { kFlat = 0, kSliced = 1, kRotated = 2 };
+enum { kFlat = 0, kSliced = 1, kRotated = 2, kRot1 = 3 };
 // NW: waves per workgroup.  16 (one workgroup per CU) in general; 8 (two per CU) for
 // layers with few row tiles per CU, where twice the workgroups, each with half the waves,
 // finish sooner.
 template <int FMT, int XDT, int MODE, int NW, int XP>
 __global__ __launch_bounds__(NW * 64) void gemv_kernel(
-    const uint8_t* __restrict__ w, const void* __restrict__ x, int K, int B, int SPL, int GS,
+    const uint8_t* __restrict__ w, const void* __restrict__ x, int K, int Bin, int SPL, int GS,
     int tq, int tr, unsigned spl_m, int S, int fwht_block, int RS, float fwht_scale,
     void* __restrict__ y, int N, int ydt PH_KPARAM) {
   extern __shared__ __align__(16) uint8_t lds[];
   PH_DECL
   PH_MARK(kPhStart);
+  // kRot1: batch 1 in one K-slice, with both fixed at compile time so that the batch-row
+  // and slice bookkeeping folds away (16 waves per CU share one scalar unit, and the
+  // rotated prologue is on the critical path of small layers)
+  constexpr bool rot1 = MODE == kRot1;
+  const int B = rot1 ? 1 : Bin;
   const int xbytes = x_lds_bytes(B, K, SPL, fwht_block);  // staged x; the slots follow
   constexpr int BB = FMT == FB_FMT_GF4 ? fb::kGf4BlockBytes : fb::kE2m1BlockBytes;
   constexpr int NT = NW * 64;
@@ -718,8 +724,8 @@ __global__ __launch_bounds__(NW * 64) void gemv_kernel(
                                                        kRsrcWord3);
   // Each wave's first two units are static (wave, wave + NW); the counter hands out
   // the rest.
-  constexpr bool rot = MODE == kRotated;
-  const int nslices = MODE == kFlat ? 1 : S;
+  constexpr bool rot = MODE == kRotated || rot1;
+  const int nslices = MODE == kFlat || rot1 ? 1 : S;
   for (int s = 0; s < nslices; ++s) {
     const int k0 = s * SPL * 512;
     const int kw = min(K - k0, nsl * 128);  // rotated width of the slice
@@ -730,7 +736,7 @@ __global__ __launch_bounds__(NW * 64) void gemv_kernel(
     // hoisting the staging index math out of the slice loop (it would stay live, in
     // registers the decode needs, for the whole kernel).
     int tid = threadIdx.x;
-    if constexpr (MODE != kFlat) asm volatile("" : "+v"(tid));
+    if constexpr (MODE != kFlat && !rot1) asm volatile("" : "+v"(tid));
     XPre<XP> xp;
     XRot xr;
     if constexpr (rot)
@@ -738,7 +744,7 @@ __global__ __launch_bounds__(NW * 64) void gemv_kernel(
     else
       x_preload<NT, XP>(xp, xg, K, k0, per_row, B * per_row, row_of, tid);
     if (s == 0) PH_MARK(kPhXIssued);
-    if constexpr (MODE != kFlat) {
+    if constexpr (MODE != kFlat && !rot1) {
       if (s == nslices - 1 && spl_last != SPL) {  // a last slice with fewer spans
         sp = spl_last;
         sp_m = 0xFFFFFFFFu / (unsigned)spl_last;  // floor(2^32 / sp), or one less: fdiv fixes it
@@ -1036,12 +1042,14 @@ int launch_mode(int mode, const void* wdev, const void* x, void* y, const fb_sha
     return deep ? launch_gemv<FMT, XDT, kSliced, kWaves, 8>(wdev, x, y, s, pl, stream)
                 : launch_gemv<FMT, XDT, kSliced, kWaves, 4>(wdev, x, y, s, pl, stream);
   // the rotation preloads kXPre 256-value sub-blocks per wave instead
+  if (mode == kRot1) return launch_gemv<FMT, XDT, kRot1, kWaves, 4>(wdev, x, y, s, pl, stream);
   return launch_gemv<FMT, XDT, kRotated, kWaves, 4>(wdev, x, y, s, pl, stream);
 }
 
 int launch_plan(const void* wdev, const void* x, void* y, const fb_shape_t* s, const Plan& pl,
                 hipStream_t hs) {
-  const int mode = s->fwht_block ? kRotated : pl.S > 1 ? kSliced : kFlat;
+  const int mode = s->fwht_block ? (s->B == 1 && pl.S == 1 ? kRot1 : kRotated)
+                                 : pl.S > 1 ? kSliced : kFlat;
   if (s->fmt == FB_FMT_GF4) return launch_mode<FB_FMT_GF4, FB_DT_F16>(mode, wdev, x, y, s, pl, hs);
   if (s->x_dtype == FB_DT_BF16)
     return launch_mode<FB_FMT_E2M1, FB_DT_BF16>(mode, wdev, x, y, s, pl, hs);
