@@ -622,11 +622,11 @@ __device__ __forceinline__ f32x4 unit_partial(const Rec<FMT>& r, const uint8_t* 
 // an argument, so nothing early waits for that load).  tq, tr: row tiles per workgroup = tq (+1 for the
 // first tr workgroups); GS: 512-element spans per row; RS: LDS bytes per staged x row;
 // spl_m: div_magic(SPL).
-// MODE: kFlat = one K-slice, no rotation (the common case); kSliced = several K-slices, no
-// rotation; kRotated = rotation of x; kRot1 = rotation at batch 1 in one K-slice.  Each is
-// compiled with only the staging it needs, which
+// MODE: kFlat = one K-slice, no rotation (the common case); kFlat1 = the same at batch 1;
+// kSliced = several K-slices, no rotation; kRotated = rotation of x; kRot1 = rotation at
+// batch 1 in one K-slice.  Each is compiled with only the staging it needs, which
 // keeps the kernel short and its registers few.
-enum { kFlat = 0, kSliced = 1, kRotated = 2, kRot1 = 3 };
+enum { kFlat = 0, kSliced = 1, kRotated = 2, kRot1 = 3, kFlat1 = 4 };
 // NW: waves per workgroup.  16 (one workgroup per CU) in general; 8 (two per CU) for
 // layers with few row tiles per CU, where twice the workgroups, each with half the waves,
 // finish sooner.
@@ -638,11 +638,12 @@ __global__ __launch_bounds__(NW * 64) void gemv_kernel(
   extern __shared__ __align__(16) uint8_t lds[];
   PH_DECL
   PH_MARK(kPhStart);
-  // kRot1: batch 1 in one K-slice, with both fixed at compile time so that the batch-row
-  // and slice bookkeeping folds away (16 waves per CU share one scalar unit, and the
-  // rotated prologue is on the critical path of small layers)
+  // kRot1 / kFlat1: batch 1 in one K-slice, with both fixed at compile time so that the
+  // batch-row and slice bookkeeping folds away (16 waves per CU share one scalar unit, and
+  // the prologue is on the critical path of small layers)
   constexpr bool rot1 = MODE == kRot1;
-  const int B = rot1 ? 1 : Bin;
+  constexpr bool flat1 = MODE == kFlat1;
+  const int B = rot1 || flat1 ? 1 : Bin;
   const int xbytes = x_lds_bytes(B, K, SPL, fwht_block);  // staged x; the slots follow
   constexpr int BB = FMT == FB_FMT_GF4 ? fb::kGf4BlockBytes : fb::kE2m1BlockBytes;
   constexpr int NT = NW * 64;
@@ -725,7 +726,7 @@ __global__ __launch_bounds__(NW * 64) void gemv_kernel(
   // Each wave's first two units are static (wave, wave + NW); the counter hands out
   // the rest.
   constexpr bool rot = MODE == kRotated || rot1;
-  const int nslices = MODE == kFlat || rot1 ? 1 : S;
+  const int nslices = MODE == kFlat || rot1 || flat1 ? 1 : S;
   for (int s = 0; s < nslices; ++s) {
     const int k0 = s * SPL * 512;
     const int kw = min(K - k0, nsl * 128);  // rotated width of the slice
@@ -736,7 +737,7 @@ __global__ __launch_bounds__(NW * 64) void gemv_kernel(
     // hoisting the staging index math out of the slice loop (it would stay live, in
     // registers the decode needs, for the whole kernel).
     int tid = threadIdx.x;
-    if constexpr (MODE != kFlat && !rot1) asm volatile("" : "+v"(tid));
+    if constexpr (MODE != kFlat && !rot1 && !flat1) asm volatile("" : "+v"(tid));
     XPre<XP> xp;
     XRot xr;
     if constexpr (rot)
@@ -744,7 +745,7 @@ __global__ __launch_bounds__(NW * 64) void gemv_kernel(
     else
       x_preload<NT, XP>(xp, xg, K, k0, per_row, B * per_row, row_of, tid);
     if (s == 0) PH_MARK(kPhXIssued);
-    if constexpr (MODE != kFlat && !rot1) {
+    if constexpr (MODE != kFlat && !rot1 && !flat1) {
       if (s == nslices - 1 && spl_last != SPL) {  // a last slice with fewer spans
         sp = spl_last;
         sp_m = 0xFFFFFFFFu / (unsigned)spl_last;  // floor(2^32 / sp), or one less: fdiv fixes it
@@ -1031,6 +1032,13 @@ template <int FMT, int XDT>
 int launch_mode(int mode, const void* wdev, const void* x, void* y, const fb_shape_t* s,
                 const Plan& pl, hipStream_t stream) {
   const bool deep = pl.xp == 8;
+  if (mode == kFlat1) {
+    if (pl.nw == kWaves / 2)
+      return deep ? launch_gemv<FMT, XDT, kFlat1, kWaves / 2, 8>(wdev, x, y, s, pl, stream)
+                  : launch_gemv<FMT, XDT, kFlat1, kWaves / 2, 4>(wdev, x, y, s, pl, stream);
+    return deep ? launch_gemv<FMT, XDT, kFlat1, kWaves, 8>(wdev, x, y, s, pl, stream)
+                : launch_gemv<FMT, XDT, kFlat1, kWaves, 4>(wdev, x, y, s, pl, stream);
+  }
   if (mode == kFlat) {
     if (pl.nw == kWaves / 2)
       return deep ? launch_gemv<FMT, XDT, kFlat, kWaves / 2, 8>(wdev, x, y, s, pl, stream)
@@ -1049,7 +1057,7 @@ int launch_mode(int mode, const void* wdev, const void* x, void* y, const fb_sha
 int launch_plan(const void* wdev, const void* x, void* y, const fb_shape_t* s, const Plan& pl,
                 hipStream_t hs) {
   const int mode = s->fwht_block ? (s->B == 1 && pl.S == 1 ? kRot1 : kRotated)
-                                 : pl.S > 1 ? kSliced : kFlat;
+                                 : pl.S > 1 ? kSliced : s->B == 1 ? kFlat1 : kFlat;
   if (s->fmt == FB_FMT_GF4) return launch_mode<FB_FMT_GF4, FB_DT_F16>(mode, wdev, x, y, s, pl, hs);
   if (s->x_dtype == FB_DT_BF16)
     return launch_mode<FB_FMT_E2M1, FB_DT_BF16>(mode, wdev, x, y, s, pl, hs);
