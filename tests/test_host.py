@@ -32,6 +32,22 @@ def test_abi_exports_every_declared_symbol():
     assert L.fb_abi_version() == C.ABI_VERSION
 
 
+def test_diagnostic_trace_library_exports():
+    """libfourbit_trace.so (the GEMV with per-wave phase timestamps, read by
+    `bench.py --phase-trace`) exports the same C ABI plus its two diagnostic entry points;
+    the product library exports neither of those."""
+    path = Path(C.__file__).resolve().parent / "libfourbit_trace.so"
+    T = ctypes.CDLL(str(path))
+    for name in C.EXPORTED:
+        assert getattr(T, name) is not None
+    assert T.fb_phase_trace_set is not None and T.fb_phase_plan is not None
+    T.fb_phase_trace_set.argtypes = [ctypes.c_void_p, ctypes.c_size_t]
+    assert T.fb_phase_trace_set(None, 0) == 0  # host-side only: needs no GPU
+    for name in ("fb_phase_trace_set", "fb_phase_plan"):
+        with pytest.raises(AttributeError):
+            getattr(C.lib(), name)
+
+
 @pytest.mark.parametrize("kw,err", [
     (dict(K=100), -2), (dict(K=0), -2), (dict(N=0), -2), (dict(B=0), -2),
     (dict(group=64), -3), (dict(fmt=7), -4), (dict(x_dtype=C.DT_BF16), -5),
