@@ -399,6 +399,36 @@ class QuantLinear(nn.Linear):
 
     def _load_from_state_dict(self, state_dict, prefix, local_metadata, strict, missing_keys,
                               unexpected_keys, error_msgs):
+        # A reference QuantLinear's own state (layers.py:23-31: weight, s, Q, Theta, mask,
+        # bias) loads too: it is packed as from_reference packs it (its committed 4-bit
+        # weight as GF4 integer levels), whatever format this module was built with.
+        ref_keys = ("s", "Q", "Theta")
+        if (all(prefix + k in state_dict for k in ref_keys)
+                and prefix + "codes" not in state_dict):
+            sd = {k: state_dict[prefix + k] for k in ref_keys + ("mask", "bias")
+                  if prefix + k in state_dict}
+            if "mask" not in sd:  # the reference's default mask is all ones
+                sd["mask"] = torch.ones_like(sd["Q"])
+            if ("bias" in sd) != (self.bias is not None):
+                error_msgs.append(f"{prefix}bias: the module and the checkpoint disagree on "
+                                  "having a bias")
+                return
+            if tuple(sd["Q"].shape) != (self.out_features, self.in_features):
+                error_msgs.append(f"{prefix}Q: shape {tuple(sd['Q'].shape)} does not match "
+                                  f"({self.out_features}, {self.in_features})")
+                return
+            q = QuantLinear.from_reference(sd, nthreads=self.nthreads)
+            dev = self.weight.device
+            with torch.no_grad():
+                self.weight.data = q.weight.data.to(dev)
+                if self.bias is not None:
+                    self.bias.data = q.bias.data.to(dev)
+            self.mask = q.mask.to(dev)
+            self.fb_header = q.fb_header.clone()
+            self.codes = q.codes.to(dev)
+            self.meta = q.meta.to(dev)
+            self.hard_quant = False
+            return
         # packed buffers take the checkpoint's shape/dtype (format may differ from ctor),
         # and the mask is present exactly when the checkpoint has one
         for name in ("codes", "meta", "fb_header"):
@@ -413,6 +443,8 @@ class QuantLinear(nn.Linear):
                                       unexpected_keys, error_msgs)
 
     def _rebuild_after_load(self, incompatible_keys) -> None:
+        if self.codes.numel() == 0:  # nothing packed was loaded (the load reports why)
+            return
         hdr = self.fb_header.tolist()
         if hdr[0] != LAYOUT_VERSION:
             raise RuntimeError(f"packed layout version {hdr[0]} != {LAYOUT_VERSION}")

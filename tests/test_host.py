@@ -357,6 +357,29 @@ def test_from_reference_decodes_the_committed_weight(K):
     assert torch.equal(q3.wdev, q.wdev)
 
 
+def test_load_state_dict_takes_the_reference_layers_own_state():
+    """A reference QuantLinear's state_dict (layers.py:23-31) loads into the drop-in, in
+    a model as in a bare layer, and packs exactly as from_reference does; without a mask the
+    reference's default (all ones) applies; mismatched shapes are load errors."""
+    sd = reference_state(24, 256, seed=3)
+    q = QuantLinear(torch.nn.Linear(256, 24), fmt="e2m1", pack=False)
+    q.load_state_dict(sd)
+    ref = QuantLinear.from_reference(sd)
+    assert q.fmt == "gf4" and torch.equal(q.wdev, ref.wdev)
+    assert torch.equal(q.weight.data, ref.weight.data) and torch.equal(q.mask, sd["mask"])
+    net = torch.nn.Sequential(torch.nn.Flatten(), QuantLinear(torch.nn.Linear(256, 24), pack=False))
+    net.load_state_dict({f"1.{k}": v for k, v in sd.items()})
+    assert torch.equal(net[1].wdev, ref.wdev)
+    nomask = {k: v for k, v in sd.items() if k != "mask"}
+    q2 = QuantLinear(torch.nn.Linear(256, 24), pack=False)
+    q2.load_state_dict(nomask)
+    assert torch.equal(q2.mask, torch.ones(24, 256))
+    ones = dict(sd, mask=torch.ones(24, 256))
+    assert torch.equal(q2.wdev, QuantLinear.from_reference(ones).wdev)
+    with pytest.raises(RuntimeError, match="does not match"):
+        QuantLinear(torch.nn.Linear(128, 24), pack=False).load_state_dict(sd)
+
+
 def test_replace_forward_packs_adaround_levels():
     from types import SimpleNamespace
     from if_i_could_turn_back_time_amd import adaround_levels, pack_quantized_linears
