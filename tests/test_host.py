@@ -460,6 +460,41 @@ def test_c_abi_from_c(tmp_path):
     assert r.stdout.strip() == "ok"
 
 
+def _sanitizers_available(tmp_path) -> bool:
+    src = tmp_path / "probe.c"
+    src.write_text("int main(void) { return 0; }\n")
+    r = subprocess.run(["gcc", "-fsanitize=address,undefined", str(src), "-o",
+                        str(tmp_path / "probe")], capture_output=True)
+    return r.returncode == 0
+
+
+@pytest.mark.skipif(shutil.which("gcc") is None or shutil.which("g++") is None,
+                    reason="gcc/g++ not on PATH")
+def test_host_packers_under_address_and_ub_sanitizers(tmp_path):
+    """The host side (csrc/fourbit_host.cpp alone: packers, integer levels, FWHT, layout
+    transform, decode, two-class split) built with -fsanitize=address,undefined and driven
+    by tests/c/sanitize_host.c over edge shapes and inputs; any memory error, leak or
+    undefined operation fails the run."""
+    if not _sanitizers_available(tmp_path):
+        pytest.skip("this toolchain has no AddressSanitizer / UBSan runtime")
+    root = Path(__file__).resolve().parents[1]
+    inc = [f"-I{root / 'include'}", f"-I{root / 'if_i_could_turn_back_time_amd' / 'csrc'}"]
+    san = ["-fsanitize=address,undefined", "-fno-sanitize-recover=all",
+           "-fno-omit-frame-pointer", "-g", "-O1"]
+    drv, host, exe = tmp_path / "drv.o", tmp_path / "host.o", tmp_path / "sanitize_host"
+    subprocess.run(["gcc", "-std=c99", "-Wall", "-Wextra", "-Werror", *san, *inc, "-c",
+                    str(root / "tests" / "c" / "sanitize_host.c"), "-o", str(drv)], check=True)
+    subprocess.run(["g++", "-std=c++17", "-ffp-contract=off", *san, *inc, "-c",
+                    str(root / "if_i_could_turn_back_time_amd" / "csrc" / "fourbit_host.cpp"),
+                    "-o", str(host)], check=True)
+    subprocess.run(["g++", "-fsanitize=address,undefined", str(drv), str(host), "-o", str(exe),
+                    "-lpthread", "-lm"], check=True)
+    r = subprocess.run([str(exe)], capture_output=True, text=True, timeout=300,
+                       env={"ASAN_OPTIONS": "detect_leaks=1", "PATH": "/usr/bin:/bin"})
+    assert r.returncode == 0, r.stderr[-4000:]
+    assert r.stdout.strip() == "ok"
+
+
 def test_bench_refuses_several_gpus():
     """bench.py runs on one GPU: --gpus N > 1 exits non-zero with a message, before any
     GPU work (this runs without a GPU)."""
