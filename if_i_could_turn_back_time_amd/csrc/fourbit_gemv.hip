@@ -14,8 +14,9 @@
 // Its (tile, span) units are handed to its waves through an LDS counter: the SIMDs issue
 // the oldest wave first, so with a fixed split the youngest wave of each SIMD would finish
 // long after the others; taking units on demand keeps all waves busy to the end.  Each
-// unit's partial sums go to a slot of their own, and after the last unit the workgroup
-// adds each output's slots in span order, so results do not depend on which wave did what.
+// unit's partial sums go to a slot of their own, and the wave that finishes a row tile's
+// last unit adds each of its outputs' slots in span order, so results do not depend on
+// which wave did what.
 // When x does not fit LDS the K range is cut into S slices staged one after the other.
 // No workgroup talks to another: no global atomics or device-scope fences.
 #include <hip/hip_runtime.h>
@@ -644,6 +645,9 @@ __global__ __launch_bounds__(NW * 64) void gemv_kernel(
   constexpr bool rot1 = MODE == kRot1;
   constexpr bool flat1 = MODE == kFlat1;
   const int B = rot1 || flat1 ? 1 : Bin;
+  // batch 1 in one K-slice: each tile is reduced by the wave that finishes it
+  constexpr bool tile_reduce = rot1 || flat1;
+  const int nslices = MODE == kFlat || rot1 || flat1 ? 1 : S;
   const int xbytes = x_lds_bytes(B, K, SPL, fwht_block);  // staged x; the slots follow
   constexpr int BB = FMT == FB_FMT_GF4 ? fb::kGf4BlockBytes : fb::kE2m1BlockBytes;
   constexpr int NT = NW * 64;
@@ -659,7 +663,8 @@ __global__ __launch_bounds__(NW * 64) void gemv_kernel(
   unsigned sp_m = spl_m;
   int nu = (t1 - t0) * SPL;  // units of this workgroup in the current slice
   auto tile_of = [&](int u) { return fdiv(u, sp, sp_m); };
-  // LDS: unit counter (16 B) | zero block (256 B) | staged x (xbytes) | partial-sum slots
+  // LDS: unit counter (16 B) | zero block (256 B) | staged x (xbytes) | partial-sum slots |
+  // per-tile unit counts
   int* counter = reinterpret_cast<int*>(lds);
   uint8_t* zeros = lds + 16;
   uint8_t* xst = lds + 16 + 256;
@@ -693,9 +698,26 @@ __global__ __launch_bounds__(NW * 64) void gemv_kernel(
     return (unsigned)((lt * GS + s * SPL + (u - lt * sp)) * BB);
   };
 
+  // Per-tile count of the last slice's finished units, after the slots.
+  int* tile_cnt = reinterpret_cast<int*>(slots + (size_t)(t1 - t0) * SPL * 4 * B);
+  // y of tile lt: each output sums its tile's span slots in span order (the wave that
+  // finished the tile's last unit does it, while the others go on).
+  auto reduce_tile = [&](int lt) {
+    for (int o = lane; o < 16 * B; o += 64) {
+      const int r = o & 15, c = o >> 4;
+      const int row = (t0 + lt) * 16 + r;
+      const f32x4* sl = slots + ((size_t)lt * SPL * 4 + (r >> 2)) * B + c;
+      float sum = 0.0f;
+      for (int j = 0; j < SPL; ++j) sum += sl[(size_t)j * 4 * B][r & 3];
+      if (row < N) store_y(y, (int64_t)c * N + row, sum, ydt);
+    }
+  };
   // Decode + MFMA of unit u (slice s) from record r; the unit's partial sums go to its own
   // LDS slot (added to the earlier slices' value), so the final sum has a fixed order
-  // whichever wave did the unit.
+  // whichever wave did the unit.  At batch 1 (kFlat1, kRot1) the unit is counted on its
+  // tile, and the unit that completes a tile reduces it: a tile is 16 outputs, and the
+  // workgroup then needs no final barrier and epilogue.  Larger batches keep the epilogue,
+  // spread over all the workgroup's threads (16 B outputs per tile for one wave was slower).
   auto process = [&](const Rec<FMT>& r, int s, int u) {
     const int lt = tile_of(u);
     const int span = u - lt * sp;
@@ -706,6 +728,17 @@ __global__ __launch_bounds__(NW * 64) void gemv_kernel(
         *sl = acc;
       else
         *sl += acc;
+    }
+    if constexpr (tile_reduce) {
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");  // the slot, then the count
+      int old = 0;
+      if (lane == 0)
+        old = __hip_atomic_fetch_add(&tile_cnt[lt], 1, __ATOMIC_RELAXED,
+                                     __HIP_MEMORY_SCOPE_WORKGROUP);
+      if (__builtin_amdgcn_readfirstlane(old) + 1 == sp) {
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");  // every slot of lt
+        reduce_tile(lt);
+      }
     }
   };
 
@@ -726,7 +759,6 @@ __global__ __launch_bounds__(NW * 64) void gemv_kernel(
   // Each wave's first two units are static (wave, wave + NW); the counter hands out
   // the rest.
   constexpr bool rot = MODE == kRotated || rot1;
-  const int nslices = MODE == kFlat || rot1 || flat1 ? 1 : S;
   for (int s = 0; s < nslices; ++s) {
     const int k0 = s * SPL * 512;
     const int kw = min(K - k0, nsl * 128);  // rotated width of the slice
@@ -766,6 +798,7 @@ __global__ __launch_bounds__(NW * 64) void gemv_kernel(
       if (threadIdx.x == 0) *counter = 2 * NW;
     }
     if (s == 0) {
+      if (tile_reduce && (int)threadIdx.x < t1 - t0) tile_cnt[threadIdx.x] = 0;
       if (threadIdx.x == 0) *counter = 2 * NW;
       if (threadIdx.x < 16) reinterpret_cast<u32x4*>(zeros)[threadIdx.x] = u32x4{0u, 0u, 0u, 0u};
     }
@@ -797,21 +830,22 @@ __global__ __launch_bounds__(NW * 64) void gemv_kernel(
     }
     PH_MARK(s == nslices - 1 ? kPhLoopEnd : s == 0 ? kPhSliceEnd0 : kPhSliceEnd1);
   }
-  __syncthreads();  // every slice done: slots are complete
-  PH_MARK(kPhFinalBar);
-
-  // y[col][row] = sum over the spans of the tile, in span order
-  const int nt = t1 - t0;
-  for (int e = threadIdx.x; e < nt * 256; e += NT) {
-    const int c = e & 15;
-    if (c >= B) continue;
-    const int r = (e >> 4) & 15;
-    const int lt = e >> 8;
-    const int row = (t0 + lt) * 16 + r;
-    const f32x4* sl = slots + ((size_t)lt * SPL * 4 + (r >> 2)) * B + c;
-    float sum = 0.0f;
-    for (int j = 0; j < SPL; ++j) sum += sl[(size_t)j * 4 * B][r & 3];
-    if (row < N) store_y(y, (int64_t)c * N + row, sum, ydt);
+  if constexpr (!tile_reduce) {
+    __syncthreads();  // every slice done: slots are complete
+    PH_MARK(kPhFinalBar);
+    // y[col][row] = sum over the spans of the tile, in span order
+    const int nt = t1 - t0;
+    for (int e = threadIdx.x; e < nt * 256; e += NT) {
+      const int c = e & 15;
+      if (c >= B) continue;
+      const int r = (e >> 4) & 15;
+      const int lt = e >> 8;
+      const int row = (t0 + lt) * 16 + r;
+      const f32x4* sl = slots + ((size_t)lt * SPL * 4 + (r >> 2)) * B + c;
+      float sum = 0.0f;
+      for (int j = 0; j < SPL; ++j) sum += sl[(size_t)j * 4 * B][r & 3];
+      if (row < N) store_y(y, (int64_t)c * N + row, sum, ydt);
+    }
   }
   PH_MARK(kPhEnd);
   PH_PUT(kPhSlices, (unsigned long long)nslices);
@@ -955,8 +989,9 @@ unsigned div_magic(int d) { return d == 1 ? 0xFFFFFFFFu : (unsigned)((1ull << 32
 // LDS of one workgroup: the unit counter, the zero block that MFMA columns past the batch
 // read, staged x, and one partial-sum slot per unit.
 size_t plan_lds(const fb_shape_t* s, int tpw, int SPL) {
+  // batch 1 adds the per-tile unit counts of the tile-by-tile reduction
   return (size_t)x_lds_bytes(s->B, s->K, SPL, s->fwht_block) + (size_t)tpw * SPL * 64 * s->B +
-         16 + 256;
+         (s->B == 1 ? (size_t)((tpw * 4 + 15) & ~15) : 0) + 16 + 256;
 }
 
 // The fewest K-slices whose LDS fits.  One 16-wave workgroup per CU (up to the number of
