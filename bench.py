@@ -439,6 +439,15 @@ def phase_trace(name: str, calls: int, packer: str) -> dict:
         "xcd_spread_us_median": round(float(np.median(np.nanmax(xcd_med, 1) - np.nanmin(xcd_med, 1))), 3),
         "gap_last_end_to_next_start_us": stats(np.array(gaps)) if gaps else None,
         "start_to_next_start_us": stats(np.array(period)) if period else None,
+        # whether the slow workgroups are the same ones from call to call
+        "slowest_workgroups_per_call": [[int(g) for g in np.argsort(wg_end[c])[-4:][::-1]]
+                                        for c in range(calls)],
+        "workgroup_end_rank_corr_between_calls": round(float(np.mean(
+            [np.corrcoef(np.argsort(np.argsort(wg_end[c])), np.argsort(np.argsort(wg_end[c + 1])))[0, 1]
+             for c in range(calls - 1)])), 3) if calls > 1 else None,
+        "workgroup_start_us": stats(us(start.min(axis=2) - g0[:, :, 0])),
+        "corr_start_end": round(float(np.corrcoef(us(start.min(axis=2) - g0[:, :, 0]).ravel(),
+                                                  wg_end.ravel())[0, 1]), 3),
     }
 
 
