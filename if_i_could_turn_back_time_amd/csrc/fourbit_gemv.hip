@@ -163,6 +163,8 @@ struct Rec {
 typedef __amdgpu_buffer_rsrc_t rsrc_t;
 constexpr int kRsrcWord3 = 0x00020000;  // raw (untyped) buffer, gfx9 family
 constexpr int kNT = 2;                  // streaming (non-temporal) cache policy
+// a buffer offset past every resource's range: the load returns zeros and moves no data
+constexpr unsigned kXOutOfRange = 0x7FFFFFF0u;
 
 // Loads one lane's record of the block at byte offset `boff` of the weight stream.
 // With a zero-sized resource the loads are out of range: they return zeros and move no
@@ -220,47 +222,52 @@ struct XPre {
   u32x4 v[XP];
 };
 
-__device__ __forceinline__ u32x4 x_load8(const uint16_t* __restrict__ x, int K, int b, int k) {
-  u32x4 v = {0u, 0u, 0u, 0u};
-  if (k < K) v = *reinterpret_cast<const u32x4*>(x + (int64_t)b * K + k);
-  return v;
-}
-
-// Chunk t of a slice is batch row t / per_row, values k0 + 8 * (t % per_row) ...; thread
-// j * NT + threadIdx.x of an NT-thread workgroup takes chunk t in step j.
-// row_of(t) = t / per_row.
-template <int NT, int XP, typename RowOf>
-__device__ __forceinline__ void x_preload(XPre<XP>& xp, const uint16_t* __restrict__ x, int K, int k0,
-                                          int per_row, int nchunks, RowOf row_of, int tid) {
+// Chunk t of a slice is batch row b = t / per_row, values k0 + 8 (t - b per_row) ...;
+// thread j NT + threadIdx.x of an NT-thread workgroup takes chunk t in step j.  per_row is a
+// multiple of 64, so the 64 chunks of one wave's step share a row: row_of_wave(tw) (tw = the
+// wave's first chunk of the step) runs once per wave, on the scalar unit, and with ONE_ROW
+// (batch 1, one slice) the row is 0.  Reads go through a buffer resource over x (B K 2
+// bytes): a chunk past K gets an out-of-range offset and reads zeros, with no branch per lane
+// and no 64-bit address arithmetic (with ONE_ROW the resource's own size does it).  The 16
+// waves of a CU share their SIMDs and scalar unit, and this is the last step before the
+// first weight request.
+template <int NT, int XP, bool ONE_ROW, typename RowOf>
+__device__ __forceinline__ void x_preload(XPre<XP>& xp, rsrc_t xrs, int K, int k0, int per_row,
+                                          int nchunks, RowOf row_of_wave, int wave, int tid) {
 #pragma unroll
   for (int j = 0; j < XP; ++j) {
-    const int t = tid + j * NT;
-    if (t < nchunks) {
-      const int b = row_of(t);
-      xp.v[j] = x_load8(x, K, b, k0 + (t - b * per_row) * 8);
+    const int tw = wave * 64 + j * NT;
+    if (tw < nchunks) {
+      const int b = ONE_ROW ? 0 : row_of_wave(tw);
+      const int k = k0 + (tid + j * NT - b * per_row) * 8;
+      const unsigned off = ONE_ROW || k < K ? (unsigned)(b * K + k) * 2u : kXOutOfRange;
+      xp.v[j] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(xrs, off, 0, 0));
     }
   }
 }
 
-// Plain staging: chunk t lands in its 128-value group of the slice layout.
-template <int NT, int XP, typename RowOf>
-__device__ void stage_plain(uint8_t* lds, const XPre<XP>& xp, const uint16_t* __restrict__ x, int K,
-                            int B, int k0, int nsl, int RS, RowOf row_of, int tid) {
+// Plain staging: chunk t lands in its 128-value group of the slice layout.  Chunks past the
+// preload are read here, the same way.
+template <int NT, int XP, bool ONE_ROW, typename RowOf>
+__device__ void stage_plain(uint8_t* lds, const XPre<XP>& xp, rsrc_t xrs, int K, int B, int k0,
+                            int nsl, int RS, RowOf row_of_wave, int wave, int tid) {
   const int per_row = nsl * 16;
   const int n = B * per_row;
-  auto put = [&](int t, const u32x4& v) {
-    const int b = row_of(t);
+  auto put = [&](int b, int t, const u32x4& v) {
     const int c8 = t - b * per_row;
     *reinterpret_cast<u32x4*>(lds + b * RS + (c8 >> 4) * kSliceBytes + (c8 & 15) * 16) = v;
   };
 #pragma unroll
   for (int j = 0; j < XP; ++j) {
-    const int t = tid + j * NT;
-    if (t < n) put(t, xp.v[j]);
+    const int tw = wave * 64 + j * NT;
+    if (tw < n) put(ONE_ROW ? 0 : row_of_wave(tw), tid + j * NT, xp.v[j]);
   }
-  for (int t = tid + XP * NT; t < n; t += NT) {
-    const int b = row_of(t);
-    put(t, x_load8(x, K, b, k0 + (t - b * per_row) * 8));
+  for (int j = XP; wave * 64 + j * NT < n; ++j) {
+    const int b = ONE_ROW ? 0 : row_of_wave(wave * 64 + j * NT);
+    const int t = tid + j * NT;
+    const int k = k0 + (t - b * per_row) * 8;
+    const unsigned off = ONE_ROW || k < K ? (unsigned)(b * K + k) * 2u : kXOutOfRange;
+    put(b, t, __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(xrs, off, 0, 0)));
   }
 }
 
@@ -340,7 +347,6 @@ struct XRot {
 // past the last one, and lanes past kw, get an out-of-range offset, which returns zeros and
 // moves no data.  The loads are issued back to back with no branch, and nothing waits for
 // them before stage_fwht.
-constexpr unsigned kXOutOfRange = 0x7FFFFFF0u;
 // Position of lane l's four values inside a 256-value sub-block: 4l for the butterflies;
 // 16 (l % 16) + 4 (l / 16) for the matrix-core transform (blocks of 256 or more), where they
 // are row l % 16, columns 4 (l / 16) .. + 3 of the sub-block as a 16 x 16 matrix.
@@ -752,8 +758,7 @@ __global__ __launch_bounds__(NW * 64) void gemv_kernel(
                                                         real ? 0x7fffffff : 0, kRsrcWord3);
     load_rec<FMT>(rs, real ? unit_off(s, u) : 0u, lane, r);
   };
-  const uint16_t* xg = static_cast<const uint16_t*>(x);
-  // x through a buffer resource for the rotation's loads (out-of-range offsets read zeros)
+  // x through a buffer resource (out-of-range offsets read zeros)
   const rsrc_t xrs = __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(x), (short)0, B * K * 2,
                                                        kRsrcWord3);
   // Each wave's first two units are static (wave, wave + NW); the counter hands out
@@ -764,18 +769,22 @@ __global__ __launch_bounds__(NW * 64) void gemv_kernel(
     const int kw = min(K - k0, nsl * 128);  // rotated width of the slice
     const int per_row = rot ? kw / 8 : nsl * 16;  // x chunks per batch row
     // batch row of x chunk t: per_row = 64 SPL without a rotation
-    auto row_of = [&](int t) { return rot ? t / per_row : fdiv(t >> 6, SPL, spl_m); };
+    // batch row of the plain layout's chunks tw .. tw + 63 (per_row = 64 SPL)
+    auto row_of_wave = [&](int tw) { return fdiv(tw >> 6, SPL, spl_m); };
     // With several slices, an opaque copy of the thread index keeps the compiler from
     // hoisting the staging index math out of the slice loop (it would stay live, in
     // registers the decode needs, for the whole kernel).
-    int tid = threadIdx.x;
-    if constexpr (MODE != kFlat && !rot1 && !flat1) asm volatile("" : "+v"(tid));
+    int tid = threadIdx.x, wv = wave;
+    if constexpr (MODE != kFlat && !rot1 && !flat1) {
+      asm volatile("" : "+v"(tid));
+      asm volatile("" : "+s"(wv));
+    }
     XPre<XP> xp;
     XRot xr;
     if constexpr (rot)
       rot_preload<NW>(xr, xrs, K, B, k0, kw, fwht_block, tid);
     else
-      x_preload<NT, XP>(xp, xg, K, k0, per_row, B * per_row, row_of, tid);
+      x_preload<NT, XP, flat1>(xp, xrs, K, k0, per_row, B * per_row, row_of_wave, wv, tid);
     if (s == 0) PH_MARK(kPhXIssued);
     if constexpr (MODE != kFlat && !rot1 && !flat1) {
       if (s == nslices - 1 && spl_last != SPL) {  // a last slice with fewer spans
@@ -806,7 +815,7 @@ __global__ __launch_bounds__(NW * 64) void gemv_kernel(
       stage_fwht<NW>(xst, reinterpret_cast<float*>(xst + B * RS), xr, xrs, K, B, k0, kw, nsl, RS,
                  fwht_block, fwht_scale, tid PH_ARG);
     else
-      stage_plain<NT, XP>(xst, xp, xg, K, B, k0, nsl, RS, row_of, tid);
+      stage_plain<NT, XP, flat1>(xst, xp, xrs, K, B, k0, nsl, RS, row_of_wave, wv, tid);
     __syncthreads();  // x staged, counter set
     PH_MARK(s == 0 ? kPhStaged : s == 1 ? kPhStaged1 : kPhStaged2);
     issue(s, u1, ring[1]);
