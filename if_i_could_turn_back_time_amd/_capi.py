@@ -34,7 +34,7 @@ EXPORTED = (
     "fb_fwht_rows_f32", "fb_to_device",
     "fb_from_device", "fb_dequant_host", "fb_gemv", "fb_dequant", "fb_quantize_gf4_gpu",
     "fb_quantize_e2m1_gpu", "fb_jenks2_host", "fb_jenks2_workspace", "fb_jenks2_gpu",
-    "fb_gemv_noalloc",
+    "fb_jenks2_filters_host", "fb_jenks2_filters_gpu", "fb_gemv_noalloc",
 )
 
 
@@ -79,6 +79,10 @@ def lib() -> ctypes.CDLL:
         "fb_jenks2_host": (ctypes.c_int, [vp, ctypes.c_int64, vp, vp, vp]),
         "fb_jenks2_workspace": (ctypes.c_int, [ctypes.c_int64, ctypes.POINTER(sz)]),
         "fb_jenks2_gpu": (ctypes.c_int, [vp, ctypes.c_int64, vp, vp, vp, vp, sz, vp]),
+        "fb_jenks2_filters_host": (ctypes.c_int, [vp, ctypes.c_int64, ctypes.c_int32, vp, vp, vp,
+                                                  ctypes.c_int32]),
+        "fb_jenks2_filters_gpu": (ctypes.c_int, [vp, ctypes.c_int64, ctypes.c_int32, vp, vp, vp,
+                                                 vp]),
         "fb_gemv_noalloc": (ctypes.c_int, [vp, vp, vp, sp, vp]),
     }
     for name, (res, args) in sigs.items():
@@ -343,3 +347,42 @@ def jenks2_gpu(w: torch.Tensor):
         host = out.cpu()
     split = int(host[:1].view(torch.int64).item())
     return keep.bool(), split, float(host[1].item())
+
+
+JENKS2_FILTER_MAX = 1024  # FB_JENKS2_FILTER_MAX
+
+
+def jenks2_filters_host(w: torch.Tensor, nthreads: int | None = None):
+    """fb_jenks2_filters_host over w [nf, n] (fp32, each row one filter): (keep bool [nf, n],
+    split int32 [nf], gvf float64 [nf])."""
+    w = _host_contig(w, torch.float32)
+    if w.dim() != 2:
+        raise ValueError("w must be [filters, values per filter]")
+    nf, n = w.shape
+    keep = torch.empty(nf, n, dtype=torch.uint8)
+    split = torch.empty(nf, dtype=torch.int32)
+    gvf = torch.empty(nf, dtype=torch.float64)
+    check(lib().fb_jenks2_filters_host(_ptr(w), nf, n, _ptr(keep), _ptr(split), _ptr(gvf),
+                                       nthreads or nthreads_default()))
+    return keep.bool(), split, gvf
+
+
+def jenks2_filters_gpu(w: torch.Tensor):
+    """fb_jenks2_filters_gpu over a device tensor w [nf, n]: (keep bool [nf, n], split int32
+    [nf], gvf float64 [nf]), on the device.  Raises on non-finite values (one torch
+    reduction first)."""
+    if not w.is_cuda:
+        raise RuntimeError("fb_jenks2_filters_gpu needs a device tensor (ROCm GPU)")
+    w = w.detach().to(torch.float32).contiguous()
+    if w.dim() != 2:
+        raise ValueError("w must be [filters, values per filter]")
+    if not bool(torch.isfinite(w).all()):
+        raise RuntimeError(strerror(ERR_VALUE))
+    nf, n = w.shape
+    with torch.cuda.device(w.device):
+        keep = torch.empty(nf, n, dtype=torch.uint8, device=w.device)
+        split = torch.empty(nf, dtype=torch.int32, device=w.device)
+        gvf = torch.empty(nf, dtype=torch.float64, device=w.device)
+        check(lib().fb_jenks2_filters_gpu(_ptr(w), nf, n, _ptr(keep), _ptr(split), _ptr(gvf),
+                                          _stream(w.device)))
+    return keep.bool(), split, gvf

@@ -499,14 +499,10 @@ int fb_dequant_host(const uint8_t* codes, const void* meta, float* w_out, const 
   return FB_OK;
 }
 
-// Two-class natural breaks over a whole array (the reference's Linear_Mask / Bias_Mask,
-// cuda_helpers.py:378-411): the same arithmetic, in the same association order, as
-// fb_jenks2_gpu (fourbit_jenks2.hip), so the two give the same split, GVF and mask bits.
-int fb_jenks2_host(const float* w, int64_t n, uint8_t* keep, int64_t* split, double* gvf) {
-  if (!w || !keep || !split || !gvf) return FB_ERR_NULL;
-  if (n < 1 || n > INT32_MAX) return FB_ERR_SHAPE;
-  for (int64_t t = 0; t < n; ++t)
-    if (!std::isfinite(w[t])) return FB_ERR_VALUE;
+// Two-class natural breaks over one array of n finite values (1 <= n < 2^31): the same
+// arithmetic, in the same association order, as fb_jenks2_gpu and the filter kernel of
+// fourbit_jenks2.hip, so that they give the same split, GVF and mask bits.
+static void jenks2_one(const float* w, int64_t n, uint8_t* keep, int64_t* split, double* gvf) {
   constexpr int64_t kBlk = 256, kSup = 256;
   std::vector<int> order((size_t)n);
   std::iota(order.begin(), order.end(), 0);
@@ -577,6 +573,35 @@ int fb_jenks2_host(const float* w, int64_t n, uint8_t* keep, int64_t* split, dou
   for (int64_t t = 0; t < n; ++t) keep[order[t]] = t >= arg ? 1 : 0;
   *split = arg;
   *gvf = (ssd0 - best) / (ssd0 + 1e-8);
+}
+
+// The whole array (the reference's Linear_Mask / Bias_Mask, cuda_helpers.py:378-411).
+int fb_jenks2_host(const float* w, int64_t n, uint8_t* keep, int64_t* split, double* gvf) {
+  if (!w || !keep || !split || !gvf) return FB_ERR_NULL;
+  if (n < 1 || n > INT32_MAX) return FB_ERR_SHAPE;
+  for (int64_t t = 0; t < n; ++t)
+    if (!std::isfinite(w[t])) return FB_ERR_VALUE;
+  jenks2_one(w, n, keep, split, gvf);
+  return FB_OK;
+}
+
+// Every filter on its own (the reference's Conv_Mask, cuda_helpers.py:333-376): filter f is
+// w[f n .. f n + n), as a [out, in, kh, kw] weight's (out, in) slices are.
+int fb_jenks2_filters_host(const float* w, int64_t nf, int32_t n, uint8_t* keep, int32_t* split,
+                           double* gvf, int32_t nthreads) {
+  if (!w || !keep || !split || !gvf) return FB_ERR_NULL;
+  if (nf < 1 || n < 1 || n > FB_JENKS2_FILTER_MAX || nf > INT32_MAX) return FB_ERR_SHAPE;
+  if (nthreads < 1) return FB_ERR_THREADS;
+  const int64_t total = nf * n;
+  for (int64_t t = 0; t < total; ++t)
+    if (!std::isfinite(w[t])) return FB_ERR_VALUE;
+  parallel_for(nf, nthreads, [&](int64_t b, int64_t e) {
+    for (int64_t f = b; f < e; ++f) {
+      int64_t sp = 0;
+      jenks2_one(w + f * n, n, keep + f * n, &sp, gvf + f);
+      split[f] = (int32_t)sp;
+    }
+  });
   return FB_OK;
 }
 

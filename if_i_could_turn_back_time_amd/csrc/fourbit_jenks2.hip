@@ -330,6 +330,105 @@ __global__ void j2_mask(const float* __restrict__ w, const float* __restrict__ s
 
 int grid_of(int64_t items, int threads) { return (int)((items + threads - 1) / threads); }
 
+// ---------------------------------------------------------------------------------
+// Every filter of a convolution weight on its own (the reference's Conv_Mask,
+// cuda_helpers.py:333-376, over its kernel at :219-255): one 64-lane workgroup per filter of
+// n <= FB_JENKS2_FILTER_MAX values.
+//  - The stable ascending order by counting: the rank of value i is the number of values
+//    that sort before it, (w_j < w_i) or (w_j == w_i and j < i), so -0.0 and +0.0 tie and
+//    keep their index order, as the host's stable sort does.  O(n^2 / 64) per lane, no
+//    sorting network, no workspace.
+//  - The fp64 sums of the rule above in one lane, in the host's association order: with
+//    n <= 1024 there are at most 4 blocks and one superblock, and every addition the host
+//    makes (zeros included) is made here in the same order.
+// ---------------------------------------------------------------------------------
+constexpr int kFilterMax = FB_JENKS2_FILTER_MAX;
+static_assert(kFilterMax <= 4 * kBlk, "one superblock of at most 4 blocks");
+
+__global__ __launch_bounds__(64) void j2_filters(const float* __restrict__ w, int n,
+                                                 uint8_t* __restrict__ keep,
+                                                 int* __restrict__ split,
+                                                 double* __restrict__ gvf) {
+  __shared__ float v[kFilterMax];
+  __shared__ float srt[kFilterMax];
+  __shared__ int ord[kFilterMax];
+  __shared__ int arg_s;
+  const int64_t f = blockIdx.x;
+  const int lane = threadIdx.x;
+  const float* wf = w + f * n;
+  for (int i = lane; i < n; i += 64) v[i] = wf[i];
+  __syncthreads();
+  for (int i = lane; i < n; i += 64) {
+    const float x = v[i];
+    int r = 0;
+    for (int j = 0; j < n; ++j) {
+      const float y = v[j];
+      r += (y < x || (y == x && j < i)) ? 1 : 0;
+    }
+    srt[r] = x;
+    ord[r] = i;
+  }
+  __syncthreads();
+  if (lane == 0) {
+    const int nblk = (n + kBlk - 1) / kBlk;
+    const double c = (double)srt[n / 2];
+    double t1[4], t2[4], bx1[4], bx2[4];
+    for (int b = 0; b < nblk; ++b) {  // block totals
+      double a1 = 0.0, a2 = 0.0;
+      for (int i = b * kBlk; i < min(n, b * kBlk + kBlk); ++i) {
+        const double d = (double)srt[i] - c;
+        const double q = d * d;
+        a1 = a1 + d;
+        a2 = a2 + q;
+      }
+      t1[b] = a1;
+      t2[b] = a2;
+    }
+    double u1, u2;  // the one superblock: exclusive block offsets, then its total
+    {
+      double a1 = 0.0, a2 = 0.0;
+      for (int b = 0; b < nblk; ++b) {
+        bx1[b] = a1;
+        bx2[b] = a2;
+        a1 = a1 + t1[b];
+        a2 = a2 + t2[b];
+      }
+      u1 = a1;
+      u2 = a2;
+    }
+    const double sx1 = 0.0, sx2 = 0.0;  // the superblocks' exclusive offset (one superblock)
+    const double pt = 0.0 + u1, qt = 0.0 + u2;
+    double best = 0.0, ssd0 = 0.0;
+    int arg = -1;
+    for (int b = 0; b < nblk; ++b) {
+      const double base1 = sx1 + bx1[b], base2 = sx2 + bx2[b];
+      double l1 = 0.0, l2 = 0.0;
+      for (int i = b * kBlk; i < min(n, b * kBlk + kBlk); ++i) {
+        const double p = base1 + l1, q = base2 + l2;
+        const double left = i == 0 ? 0.0 : q - (p * p) / (double)i;
+        const double rp = pt - p;
+        const double right = (qt - q) - (rp * rp) / (double)(n - i);
+        const double val = left + right;
+        if (arg < 0 || val < best) {
+          best = val;
+          arg = i;
+        }
+        if (i == 0) ssd0 = val;
+        const double d = (double)srt[i] - c;
+        const double dq = d * d;
+        l1 = l1 + d;
+        l2 = l2 + dq;
+      }
+    }
+    split[f] = arg;
+    gvf[f] = (ssd0 - best) / (ssd0 + 1e-8);
+    arg_s = arg;
+  }
+  __syncthreads();
+  const int arg = arg_s;
+  for (int r = lane; r < n; r += 64) keep[f * n + ord[r]] = r >= arg ? 1 : 0;
+}
+
 }  // namespace
 
 extern "C" {
@@ -390,6 +489,18 @@ int fb_jenks2_gpu(const float* w, int64_t n, uint8_t* keep, int64_t* split, doub
                      gvf);
   hipLaunchKernelGGL(j2_mask, dim3(grid_of(n, 256)), dim3(256), 0, hs, w, keys_out, vals_out, ni,
                      split, keep);
+  return hipGetLastError() == hipSuccess ? FB_OK : FB_ERR_HIP;
+}
+
+int fb_jenks2_filters_gpu(const float* w, int64_t nf, int32_t n, uint8_t* keep, int32_t* split,
+                          double* gvf, void* stream) {
+  if (!w || !keep || !split || !gvf) return FB_ERR_NULL;
+  if (nf < 1 || n < 1 || n > FB_JENKS2_FILTER_MAX || nf > INT32_MAX) return FB_ERR_SHAPE;
+  if ((reinterpret_cast<uintptr_t>(w) & 3u) || (reinterpret_cast<uintptr_t>(split) & 3u) ||
+      (reinterpret_cast<uintptr_t>(gvf) & 7u))
+    return FB_ERR_ALIGN;
+  hipLaunchKernelGGL(j2_filters, dim3((unsigned)nf), dim3(64), 0, static_cast<hipStream_t>(stream),
+                     w, (int)n, keep, split, gvf);
   return hipGetLastError() == hipSuccess ? FB_OK : FB_ERR_HIP;
 }
 

@@ -8,6 +8,13 @@ from the split on.  Here the same rule runs natively in O(n) after the sort
 (``fb_jenks2_gpu`` on a ROCm tensor, ``fb_jenks2_host`` on a CPU one; the two give the
 same bits).  The return values have the reference's types: a float32 CPU mask of the
 input's shape (1 = kept) and the goodness of variance fit as a Python float.
+
+``conv_mask`` is the reference's ``Conv_Mask`` (``:333-376``): the same rule on every
+(out, in) filter of a convolution weight on its own, over its per-filter kernel
+(``jenks_optimization_cuda_conv``, ``:219-289``, one thread per filter trying every split
+serially).  Here ``fb_jenks2_filters_gpu`` runs one 64-lane workgroup per filter
+(``fb_jenks2_filters_host`` on the CPU), each filter bit for bit what ``jenks2`` gives on it
+alone.
 """
 from __future__ import annotations
 
@@ -38,3 +45,27 @@ def bias_mask(weights_cuda: torch.Tensor):
         raise ValueError("bias_mask takes a 1-D tensor (Linear_Mask flattens any shape)")
     keep, _, gvf = jenks2(weights_cuda)
     return keep.to(device="cpu", dtype=torch.float32), gvf
+
+
+def jenks2_filters(weights: torch.Tensor):
+    """Per-filter split of ``weights`` [out, in, kh, kw] (or any [..., kh, kw]): (keep bool
+    tensor of ``weights``' shape, split int32 [out, in], GVF float64 [out, in]), on the
+    weights' device."""
+    if weights.dim() < 3:
+        raise ValueError("conv weights are [out, in, kh, kw]")
+    lead = weights.shape[:-2]
+    w2 = weights.reshape(-1, weights.shape[-2] * weights.shape[-1])
+    if weights.is_cuda:
+        keep, split, gvf = C.jenks2_filters_gpu(w2)
+    else:
+        keep, split, gvf = C.jenks2_filters_host(w2)
+    return keep.reshape(weights.shape), split.reshape(lead), gvf.reshape(lead)
+
+
+def conv_mask(weights_cuda: torch.Tensor):
+    """``Conv_Mask`` (``cuda_helpers.py:333-376``): a float32 mask of the weights' shape on
+    their device (1 = kept) and the GVF of every filter as a nested list [out][in]."""
+    if weights_cuda.dim() != 4:
+        raise ValueError("conv_mask takes [out, in, kh, kw] weights")
+    keep, _, gvf = jenks2_filters(weights_cuda)
+    return keep.to(torch.float32), gvf.cpu().tolist()

@@ -229,6 +229,30 @@ int fb_jenks2_workspace(int64_t n, size_t* bytes);
 int fb_jenks2_gpu(const float* w, int64_t n, uint8_t* keep, int64_t* split, double* gvf,
                   void* ws, size_t ws_bytes, void* stream);
 
+/* ---------------------------------------------------------------------------------
+ * The same two-class split on every filter of a convolution weight on its own.  Replaces
+ * the reference's Conv_Mask (Python_Jenks_Test/Jenks_Tests/cuda_helpers.py:333-376) over its
+ * per-filter kernel jenks_optimization_cuda_conv (:219-289: one thread per (out, in) filter
+ * pair trying every split of the kh*kw values serially, O(n^2) per filter).
+ *   w      fp32 [nf, n]: filter f is w[f*n .. f*n + n), the (out, in) slices of an
+ *          [out, in, kh, kw] weight (nf = out*in, n = kh*kw), finite
+ *   keep   uint8 [nf, n]: fb_jenks2_host's mask of each filter
+ *   split  int32 [nf]: each filter's first argmin over idx in [0, n)
+ *   gvf    double [nf]: each filter's GVF
+ * Each filter's split, GVF and mask are bit for bit what fb_jenks2_host gives on that
+ * filter alone.  1 <= n <= FB_JENKS2_FILTER_MAX (a 32x32 kernel), 1 <= nf < 2^31.
+ * ------------------------------------------------------------------------------- */
+#define FB_JENKS2_FILTER_MAX 1024
+int fb_jenks2_filters_host(const float* w, int64_t nf, int32_t n, uint8_t* keep, int32_t* split,
+                           double* gvf, int32_t nthreads);
+
+/* GPU version, bit-identical to fb_jenks2_filters_host: one 64-lane workgroup per filter
+ * (stable ranks by counting, the fp64 sums in one lane), no workspace.  w, keep, split and
+ * gvf are device pointers; asynchronous on the stream.  Non-finite values are not detected
+ * (the host version rejects them with FB_ERR_VALUE). */
+int fb_jenks2_filters_gpu(const float* w, int64_t nf, int32_t n, uint8_t* keep, int32_t* split,
+                          double* gvf, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

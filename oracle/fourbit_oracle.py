@@ -159,6 +159,22 @@ def jenks2(values: np.ndarray):
     return keep, split, float(gvf), ssd
 
 
+def jenks2_filters(w: np.ndarray):
+    """The reference's ``Conv_Mask`` (``cuda_helpers.py:333-376``) over its per-filter kernel
+    (``:219-255``): the two-class rule of ``jenks2`` on every filter on its own, a filter being
+    one (out, in) slice of an ``[out, in, kh, kw]`` weight (``flat = w.view(out * in, -1)``,
+    sorted per row, ``min(dim=2)`` per filter).  ``w`` is ``[nf, n]``; returns ``(keep bool
+    [nf, n], split int [nf], gvf float [nf])``."""
+    w = np.asarray(w, dtype=np.float32)
+    nf, n = w.shape
+    keep = np.zeros((nf, n), bool)
+    split = np.zeros(nf, np.int64)
+    gvf = np.zeros(nf, np.float64)
+    for f in range(nf):
+        keep[f], split[f], gvf[f], _ = jenks2(w[f])
+    return keep, split, gvf
+
+
 def f64_to_f16_bits(x: np.ndarray) -> np.ndarray:
     """fp64 -> fp32 -> fp16, each step round-to-nearest-even; returns uint16 bits."""
     return np.asarray(x, np.float64).astype(np.float32).astype(np.float16).view(np.uint16)

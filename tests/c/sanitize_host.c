@@ -143,6 +143,27 @@ int main(void) {
     free(w);
     free(keep);
   }
+  /* every filter on its own, at the per-filter sizes' edges (1, a 256-block, the maximum) */
+  static const int fsz[] = {1, 9, 25, 255, 256, 257, FB_JENKS2_FILTER_MAX};
+  for (size_t i = 0; i < sizeof(fsz) / sizeof(fsz[0]); ++i) {
+    const int n = fsz[i];
+    const int64_t nf = 7;
+    float* w = malloc(sizeof(float) * nf * n);
+    uint8_t* keep = malloc((size_t)nf * n);
+    int32_t* split = malloc(sizeof(int32_t) * nf);
+    double* gvf = malloc(sizeof(double) * nf);
+    fill(w, nf * n, (int)(i % 4));
+    CHECK(fb_jenks2_filters_host(w, nf, n, keep, split, gvf, (int)(i % 3) + 1) == FB_OK);
+    for (int64_t f = 0; f < nf; ++f) {
+      int64_t kept = 0;
+      for (int j = 0; j < n; ++j) kept += keep[f * n + j];
+      CHECK(split[f] >= 0 && split[f] < n && kept == n - split[f]);
+    }
+    free(w);
+    free(keep);
+    free(split);
+    free(gvf);
+  }
   /* errors are reported, not crashed on */
   float bad[2] = {1.0f, NAN};
   uint8_t k2[2];
@@ -150,6 +171,9 @@ int main(void) {
   double gv;
   CHECK(fb_jenks2_host(bad, 2, k2, &sp, &gv) == FB_ERR_VALUE);
   CHECK(fb_jenks2_host(bad, 0, k2, &sp, &gv) == FB_ERR_SHAPE);
+  int32_t sp32;
+  CHECK(fb_jenks2_filters_host(bad, 1, 2, k2, &sp32, &gv, 1) == FB_ERR_VALUE);
+  CHECK(fb_jenks2_filters_host(bad, 1, FB_JENKS2_FILTER_MAX + 1, k2, &sp32, &gv, 1) == FB_ERR_SHAPE);
   printf("ok\n");
   return 0;
 }

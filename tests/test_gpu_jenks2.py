@@ -80,3 +80,52 @@ def test_jenks2_gpu_large_array():
         "allocation and the host copy of split / GVF)")
     assert split_g == split_h and gvf_g == gvf_h
     assert torch.equal(keep_g.cpu(), keep_h)
+
+
+def _filter_inputs():
+    """Convolution weights [out, in, kh, kw]: LeNet-5, VGG, AlexNet-stem and ResNet-stem
+    filter sizes, the per-filter maximum of 1024 values, ties, signed zeros and constant
+    filters."""
+    rng = np.random.default_rng(12)
+    for shape in ((6, 1, 5, 5), (64, 64, 3, 3), (64, 3, 11, 11), (64, 3, 7, 7), (2, 3, 32, 32),
+                  (7, 5, 1, 1), (3, 2, 16, 17)):
+        yield f"random{shape}", (rng.standard_normal(shape) * 0.05).astype(np.float32)
+    w = (np.round(rng.standard_normal((32, 16, 3, 3)) * 2) / 4).astype(np.float32)
+    w[::3] = 0.0
+    w[1::5, :, ::2] = -0.0
+    w[2] = 0.7
+    yield "ties", w
+
+
+@pytest.mark.parametrize("case", list(range(8)))
+def test_jenks2_filters_gpu_bit_exact_vs_host(case):
+    """fb_jenks2_filters_gpu (the reference's Conv_Mask, cuda_helpers.py:333-376) against
+    its host twin, bit for bit, on every filter: split, GVF and mask."""
+    name, w = list(_filter_inputs())[case]
+    say("jenks2 filters", name)
+    w2 = torch.from_numpy(w.reshape(w.shape[0] * w.shape[1], -1))
+    keep_h, split_h, gvf_h = C.jenks2_filters_host(w2)
+    keep_g, split_g, gvf_g = C.jenks2_filters_gpu(w2.to(DEV))
+    torch.cuda.synchronize()
+    assert torch.equal(split_g.cpu(), split_h), name
+    assert torch.equal(gvf_g.cpu().view(torch.int64), gvf_h.view(torch.int64)), name
+    assert torch.equal(keep_g.cpu(), keep_h), name
+
+
+def test_conv_mask_on_device_matches_host():
+    """conv_mask keeps the mask on the weights' device (as the reference's Conv_Mask does)
+    and gives the host's mask and GVF list; a 512 x 512 x 3 x 3 layer is timed."""
+    from if_i_could_turn_back_time_amd import jenks
+    g = torch.Generator().manual_seed(5)
+    w = torch.randn(512, 512, 3, 3, generator=g) * 0.05
+    mh, gh = jenks.conv_mask(w)
+    wd = w.to(DEV)
+    jenks.conv_mask(wd)                                # warm-up
+    torch.cuda.synchronize()
+    t = time.perf_counter()
+    md, gd = jenks.conv_mask(wd)
+    torch.cuda.synchronize()
+    say(f"conv_mask 512x512x3x3 on the GPU: {(time.perf_counter() - t) * 1e3:.2f} ms (incl. the "
+        "finiteness check and the GVF copy to the host)")
+    assert md.device.type == "cuda" and md.dtype == torch.float32
+    assert torch.equal(md.cpu(), mh) and gd == gh

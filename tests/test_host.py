@@ -609,6 +609,57 @@ def test_jenks2_host_errors_and_mask_api():
         bias_mask(W)
 
 
+def _jenks2_filter_inputs():
+    """Convolution weights as [filters, values per filter]: LeNet-5 / VGG / AlexNet filter
+    sizes, the per-filter maximum (1024, four 256-blocks), ties, signed zeros and constant
+    filters."""
+    for shape in ((6, 1, 5, 5), (16, 8, 3, 3), (8, 3, 11, 11), (2, 2, 16, 16), (2, 1, 32, 32),
+                  (5, 3, 1, 1), (3, 3, 1, 2), (2, 2, 17, 17)):
+        w = (RNG.standard_normal(shape) * 0.05).astype(np.float32)
+        yield f"random{shape}", w.reshape(shape[0] * shape[1], -1)
+    w = (np.round(RNG.standard_normal((40, 9)) * 2) / 4).astype(np.float32)   # ties
+    w[::3] = 0.0
+    w[1::5, ::2] = -0.0
+    w[2] = 0.7                                                            # constant filter
+    yield "ties", w
+
+
+def test_jenks2_filters_host_bit_exact_vs_oracle():
+    """fb_jenks2_filters_host gives, for every filter, the oracle's split, GVF bits and
+    mask (the whole-array rule on each filter alone)."""
+    for name, w in _jenks2_filter_inputs():
+        keep_o, split_o, gvf_o = O.jenks2_filters(w)
+        keep_h, split_h, gvf_h = C.jenks2_filters_host(torch.from_numpy(w), nthreads=3)
+        assert np.array_equal(split_h.numpy(), split_o), name
+        assert np.array_equal(gvf_h.numpy().view(np.int64), gvf_o.view(np.int64)), name
+        assert np.array_equal(keep_h.numpy(), keep_o), name
+
+
+def test_jenks2_filters_host_errors_and_conv_mask_api():
+    L = C.lib()
+    buf = torch.zeros(64, dtype=torch.float64)
+    p = buf.data_ptr()
+    w = torch.tensor([[1.0, float("nan")]])
+    assert L.fb_jenks2_filters_host(w.data_ptr(), 1, 2, p, p, p, 1) == -10
+    w = torch.zeros(2, 4)
+    assert L.fb_jenks2_filters_host(w.data_ptr(), 0, 4, p, p, p, 1) == -2
+    assert L.fb_jenks2_filters_host(w.data_ptr(), 2, 0, p, p, p, 1) == -2
+    assert L.fb_jenks2_filters_host(w.data_ptr(), 1, C.JENKS2_FILTER_MAX + 1, p, p, p, 1) == -2
+    assert L.fb_jenks2_filters_host(w.data_ptr(), 2, 4, p, p, p, 0) == -12
+    assert L.fb_jenks2_filters_host(None, 2, 4, p, p, p, 1) == -1
+    assert L.fb_jenks2_filters_gpu(None, 2, 4, p, p, p, None) == -1     # no device call
+    assert L.fb_jenks2_filters_gpu(w.data_ptr(), 2, 2000, p, p, p, None) == -2
+    from if_i_could_turn_back_time_amd import jenks
+    W = torch.randn(8, 4, 3, 3) * 0.05
+    m, gvf = jenks.conv_mask(W)                     # cuda_helpers.py:333-376 return types
+    assert m.shape == W.shape and m.dtype == torch.float32
+    assert len(gvf) == 8 and len(gvf[0]) == 4 and isinstance(gvf[0][0], float)
+    keep, split, g = O.jenks2_filters(W.reshape(32, 9).numpy())
+    assert torch.equal(m.reshape(32, 9).bool(), torch.from_numpy(keep))
+    with pytest.raises(ValueError):
+        jenks.conv_mask(torch.randn(4, 9))
+
+
 def test_gemv_noalloc_validation_needs_no_gpu():
     """fb_gemv_noalloc checks the shape and its scratch need before any device call: a
     rotated call of more than 524288 activation values (1 MiB of fp16) is FB_ERR_SCRATCH."""

@@ -470,6 +470,40 @@ def test_jenks2_brute_force_over_all_two_way_partitions():
             assert abs(ssd[split] - best) <= 1e-12 + 1e-9 * best, (n, w)
 
 
+def _reference_filter_mask(indices, min_indices):
+    """The reference's vectorized_filter_mask (cuda_helpers.py:302-330) restated: ones, then
+    the sorted positions below each filter's min index scattered to zero."""
+    nf, n = indices.shape
+    cutoff = np.arange(n)[None, :] < min_indices[:, None]
+    mask = np.ones((nf, n), np.float32)
+    np.put_along_axis(mask, indices, (~cutoff).astype(np.float32), axis=1)
+    return mask
+
+
+def test_jenks2_filters_matches_reference_conv_kernel():
+    """Conv_Mask (cuda_helpers.py:333-376) on [out, in, kh, kw] weights: per filter, the
+    conv kernel's rule (:219-255, the same per-split means and SSDs as the linear kernel,
+    in float64 and in its own float32) picks the oracle's split wherever the minimum is not
+    a near-tie, and the reference's mask construction from the sorted indices gives the
+    oracle's mask; GVF follows (SSD_total - min) / (SSD_total + 1e-8)."""
+    for shape in ((6, 3, 5, 5), (4, 2, 3, 3), (2, 2, 11, 11), (3, 1, 1, 1)):
+        w = (RNG.standard_t(4, size=shape) * 0.05).astype(np.float32)
+        w2 = w.reshape(shape[0] * shape[1], -1)
+        keep, split, gvf = O.jenks2_filters(w2)
+        order = np.argsort(w2, axis=1, kind="stable")
+        mins = np.zeros(w2.shape[0], np.int64)
+        for f in range(w2.shape[0]):
+            v = w2[f][order[f]]
+            s64, var64 = _reference_k2_split(v.astype(np.float64))
+            mins[f] = split[f]
+            srt = np.sort(var64)
+            if v.size == 1 or srt[1] - srt[0] > 1e-5 * srt[0]:
+                assert split[f] == s64 == _reference_k2_split_fp32(v)[0], (shape, f)
+            assert np.isclose(gvf[f], (var64[0] - var64.min()) / (var64[0] + 1e-8), rtol=1e-8,
+                              atol=1e-12)
+        assert np.array_equal(_reference_filter_mask(order, mins), keep.astype(np.float32))
+
+
 def test_jenks2_degenerate_inputs():
     """A constant array is 'no split' (split 0, everything kept, GVF 0); two constant runs
     split exactly between them; -0.0 and +0.0 are equal and keep their index order."""
