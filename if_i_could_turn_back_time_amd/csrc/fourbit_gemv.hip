@@ -631,9 +631,11 @@ __device__ __forceinline__ f32x4 unit_partial(const Rec<FMT>& r, const uint8_t* 
 // spl_m: div_magic(SPL).
 // MODE: kFlat = one K-slice, no rotation (the common case); kFlat1 = the same at batch 1;
 // kSliced = several K-slices, no rotation; kRotated = rotation of x; kRot1 = rotation at
-// batch 1 in one K-slice.  Each is compiled with only the staging it needs, which
-// keeps the kernel short and its registers few.
-enum { kFlat = 0, kSliced = 1, kRotated = 2, kRot1 = 3, kFlat1 = 4 };
+// batch 1 in one K-slice; kSplitK = one K-part per workgroup (blockIdx.y = the part), the
+// parts' fp32 sums written to the caller's workspace and added by splitk_sum.  Each is
+// compiled with only the staging it needs, which keeps the kernel short and its registers
+// few.
+enum { kFlat = 0, kSliced = 1, kRotated = 2, kRot1 = 3, kFlat1 = 4, kSplitK = 5 };
 // NW: waves per workgroup.  16 (one workgroup per CU) in general; 8 (two per CU) for
 // layers with few row tiles per CU, where twice the workgroups, each with half the waves,
 // finish sooner.
@@ -654,6 +656,12 @@ __global__ __launch_bounds__(NW * 64) void gemv_kernel(
   // batch 1 in one K-slice: each tile is reduced by the wave that finishes it
   constexpr bool tile_reduce = rot1 || flat1;
   const int nslices = MODE == kFlat || rot1 || flat1 ? 1 : S;
+  // kSplitK: this workgroup runs the one slice (K-part) blockIdx.y of the sliced layout and
+  // writes its part's sums, fp32, to y + part * B * N
+  constexpr bool splitk = MODE == kSplitK;
+  const int s_begin = splitk ? (int)blockIdx.y : 0;
+  const int s_end = splitk ? s_begin + 1 : nslices;
+  void* yo = splitk ? static_cast<void*>(static_cast<float*>(y) + (size_t)s_begin * Bin * N) : y;
   const int xbytes = x_lds_bytes(B, K, SPL, fwht_block);  // staged x; the slots follow
   constexpr int BB = FMT == FB_FMT_GF4 ? fb::kGf4BlockBytes : fb::kE2m1BlockBytes;
   constexpr int NT = NW * 64;
@@ -715,7 +723,7 @@ __global__ __launch_bounds__(NW * 64) void gemv_kernel(
       const f32x4* sl = slots + ((size_t)lt * SPL * 4 + (r >> 2)) * B + c;
       float sum = 0.0f;
       for (int j = 0; j < SPL; ++j) sum += sl[(size_t)j * 4 * B][r & 3];
-      if (row < N) store_y(y, (int64_t)c * N + row, sum, ydt);
+      if (row < N) store_y(yo, (int64_t)c * N + row, sum, ydt);
     }
   };
   // Decode + MFMA of unit u (slice s) from record r; the unit's partial sums go to its own
@@ -730,7 +738,7 @@ __global__ __launch_bounds__(NW * 64) void gemv_kernel(
     const f32x4 acc = unit_partial<FMT, XDT>(r, xl + span * xspan);
     if (col < B) {
       f32x4* sl = slots + ((size_t)(lt * SPL + span) * 4 + q) * B + col;
-      if (s == 0)
+      if (s == s_begin)
         *sl = acc;
       else
         *sl += acc;
@@ -764,7 +772,7 @@ __global__ __launch_bounds__(NW * 64) void gemv_kernel(
   // Each wave's first two units are static (wave, wave + NW); the counter hands out
   // the rest.
   constexpr bool rot = MODE == kRotated || rot1;
-  for (int s = 0; s < nslices; ++s) {
+  for (int s = s_begin; s < s_end; ++s) {
     const int k0 = s * SPL * 512;
     const int kw = min(K - k0, nsl * 128);  // rotated width of the slice
     const int per_row = rot ? kw / 8 : nsl * 16;  // x chunks per batch row
@@ -802,11 +810,11 @@ __global__ __launch_bounds__(NW * 64) void gemv_kernel(
     if (s == 0) PH_MARK(kPhU0Issued);
     // The next slice's x (into registers) and first weight unit are requested before the
     // barrier that closes the previous slice, so their latency overlaps the slowest wave.
-    if (s > 0) {  // every wave is done with the previous slice: x may be restaged
+    if (s > s_begin) {  // every wave is done with the previous slice: x may be restaged
       __syncthreads();
       if (threadIdx.x == 0) *counter = 2 * NW;
     }
-    if (s == 0) {
+    if (s == s_begin) {
       if (tile_reduce && (int)threadIdx.x < t1 - t0) tile_cnt[threadIdx.x] = 0;
       if (threadIdx.x == 0) *counter = 2 * NW;
       if (threadIdx.x < 16) reinterpret_cast<u32x4*>(zeros)[threadIdx.x] = u32x4{0u, 0u, 0u, 0u};
@@ -842,8 +850,10 @@ __global__ __launch_bounds__(NW * 64) void gemv_kernel(
   if constexpr (!tile_reduce) {
     __syncthreads();  // every slice done: slots are complete
     PH_MARK(kPhFinalBar);
-    // y[col][row] = sum over the spans of the tile, in span order
+    // y[col][row] = sum over the spans of the tile, in span order (kSplitK: the spans of
+    // this workgroup's part, sp of them)
     const int nt = t1 - t0;
+    const int nsp = splitk ? sp : SPL;
     for (int e = threadIdx.x; e < nt * 256; e += NT) {
       const int c = e & 15;
       if (c >= B) continue;
@@ -852,8 +862,8 @@ __global__ __launch_bounds__(NW * 64) void gemv_kernel(
       const int row = (t0 + lt) * 16 + r;
       const f32x4* sl = slots + ((size_t)lt * SPL * 4 + (r >> 2)) * B + c;
       float sum = 0.0f;
-      for (int j = 0; j < SPL; ++j) sum += sl[(size_t)j * 4 * B][r & 3];
-      if (row < N) store_y(y, (int64_t)c * N + row, sum, ydt);
+      for (int j = 0; j < nsp; ++j) sum += sl[(size_t)j * 4 * B][r & 3];
+      if (row < N) store_y(yo, (int64_t)c * N + row, sum, ydt);
     }
   }
   PH_MARK(kPhEnd);
@@ -862,6 +872,26 @@ __global__ __launch_bounds__(NW * 64) void gemv_kernel(
 }
 
 // ---------------------------------------------------------------------------------
+// The split-K sum: y[i] = ((part_0[i] + part_1[i]) + ...) + part_{P-1}[i], fp32, in part
+// order whichever workgroup finished first; four outputs per thread, 16-byte reads where
+// the batch-by-rows count allows.
+__global__ __launch_bounds__(256) void splitk_sum(const float* __restrict__ part, int P,
+                                                  int64_t n, void* __restrict__ y, int ydt) {
+  const int64_t i0 = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4;
+  if (i0 >= n) return;
+  if (i0 + 4 <= n && (n & 3) == 0) {
+    f32x4 a = *reinterpret_cast<const f32x4*>(part + i0);
+    for (int p = 1; p < P; ++p) a += *reinterpret_cast<const f32x4*>(part + (int64_t)p * n + i0);
+    for (int j = 0; j < 4; ++j) store_y(y, i0 + j, a[j], ydt);
+  } else {
+    for (int64_t i = i0; i < min(n, i0 + 4); ++i) {
+      float a = part[i];
+      for (int p = 1; p < P; ++p) a += part[(int64_t)p * n + i];
+      store_y(y, i, a, ydt);
+    }
+  }
+}
+
 // Device decode: one thread per item writes 128 values of row n.
 // ---------------------------------------------------------------------------------
 template <int FMT>
@@ -986,6 +1016,7 @@ struct Plan {
   int nw = 0;    // waves per workgroup: 16 (one workgroup per CU) or 8 (two per CU)
   int xp = 4;    // x chunks each thread preloads per slice: 4, or 8 for larger slices
   size_t lds = 0;
+  int P = 0;     // kSplitK: K-parts run side by side (grid grid x P); 0: slices in turn
 };
 
 // The rotation's normalisation 1 / sqrt(b), rounded as fp32 (correctly rounded sqrt and
@@ -1043,6 +1074,51 @@ bool make_plan(const fb_shape_t* s, int cus, Plan& pl) {
   return false;
 }
 
+// kSplitK (batch >= 2, unrotated): the K-slices of the sliced layout run side by side, P
+// workgroups per row range, each staging only its own part of x, with no slice barrier.  The
+// parts' fp32 sums (P * B * N * 4 bytes) go to the caller's workspace and splitk_sum adds
+// them in part order (one more launch, and the sums' traffic).  Measured on MI355X against
+// the slices in turn, it pays only where the sliced plan needs 3 or more slices of a long K
+// (K >= 10240) with at most 2 row tiles per workgroup: 11008 -> 4096 at batch 16, GF4
+// 16.7 -> 14.3 us and E2M1 13.4 -> 11.1 us (P = 4).  With 2 slices it was within +-1 us
+// either way (batch 8 at K = 11008, batch 4 at K = 28672), and on layers of more row tiles
+// per workgroup (8192 -> 8192, 8192 -> 28672 at batch 8/16) up to 8 us slower.  P: the
+// sliced plan's slice count rounded up to a power of two (at most 8), if its LDS fits.
+// 0 where it does not apply.
+int splitk_parts(const fb_shape_t* s, int cus, Plan* out) {
+  if (s->fwht_block || s->B < 2 || s->K < 10240) return 0;
+  Plan std_pl;
+  if (!make_plan(s, cus, std_pl) || std_pl.S < 3) return 0;
+  const int GS = (s->K / 128 + 3) / 4;
+  const int T = (s->N + 15) / 16;
+  if ((T + std_pl.grid - 1) / std_pl.grid > 2) return 0;
+  int P = 2;
+  while (P < std_pl.S) P *= 2;
+  if (P > 8 || P > GS) return 0;
+  const int SPL = (GS + P - 1) / P;
+  if ((P - 1) * SPL >= GS) return 0;  // the last part would have no span
+  const int gx = std::max(1, std::min(T, cus / P));
+  const size_t lds = plan_lds(s, (T + gx - 1) / gx, SPL);
+  if (lds > (size_t)kLdsLimit) return 0;
+  if (out) {
+    out->S = P;
+    out->SPL = SPL;
+    out->grid = gx;
+    out->GS = GS;
+    out->tq = T / gx;
+    out->tr = T % gx;
+    out->nw = kWaves;
+    out->xp = (s->B * SPL + kWaves - 1) / kWaves <= 4 ? 4 : 8;
+    out->lds = lds;
+    out->P = P;
+  }
+  return P;
+}
+
+size_t splitk_bytes(const fb_shape_t* s, int P) {
+  return P ? ((size_t)P * s->B * s->N * 4 + 255) & ~size_t(255) : 0;
+}
+
 int device_cus() {
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess) return 256;
@@ -1064,7 +1140,7 @@ int launch_gemv(const void* wdev, const void* x, void* y, const fb_shape_t* s, c
       return FB_ERR_HIP;
     attr_set.fetch_or(bit, std::memory_order_release);
   }
-  hipLaunchKernelGGL(kern, dim3(pl.grid), dim3(NW * 64), pl.lds, stream,
+  hipLaunchKernelGGL(kern, dim3(pl.grid, pl.P ? pl.P : 1), dim3(NW * 64), pl.lds, stream,
                      static_cast<const uint8_t*>(wdev), x, s->K, s->B, pl.SPL, pl.GS, pl.tq,
                      pl.tr, div_magic(pl.SPL), pl.S, s->fwht_block, x_row_stride(pl.SPL * 4),
                      fwht_scale(s->fwht_block), y,
@@ -1076,6 +1152,9 @@ template <int FMT, int XDT>
 int launch_mode(int mode, const void* wdev, const void* x, void* y, const fb_shape_t* s,
                 const Plan& pl, hipStream_t stream) {
   const bool deep = pl.xp == 8;
+  if (mode == kSplitK)
+    return deep ? launch_gemv<FMT, XDT, kSplitK, kWaves, 8>(wdev, x, y, s, pl, stream)
+                : launch_gemv<FMT, XDT, kSplitK, kWaves, 4>(wdev, x, y, s, pl, stream);
   if (mode == kFlat1) {
     if (pl.nw == kWaves / 2)
       return deep ? launch_gemv<FMT, XDT, kFlat1, kWaves / 2, 8>(wdev, x, y, s, pl, stream)
@@ -1101,7 +1180,10 @@ int launch_mode(int mode, const void* wdev, const void* x, void* y, const fb_sha
 int launch_plan(const void* wdev, const void* x, void* y, const fb_shape_t* s, const Plan& pl,
                 hipStream_t hs) {
   const int mode = s->fwht_block ? (s->B == 1 && pl.S == 1 ? kRot1 : kRotated)
-                                 : pl.S > 1 ? kSliced : s->B == 1 ? kFlat1 : kFlat;
+                   : pl.P         ? kSplitK
+                   : pl.S > 1     ? kSliced
+                   : s->B == 1    ? kFlat1
+                                  : kFlat;
   if (s->fmt == FB_FMT_GF4) return launch_mode<FB_FMT_GF4, FB_DT_F16>(mode, wdev, x, y, s, pl, hs);
   if (s->x_dtype == FB_DT_BF16)
     return launch_mode<FB_FMT_E2M1, FB_DT_BF16>(mode, wdev, x, y, s, pl, hs);
@@ -1132,8 +1214,19 @@ int launch_rotate(const void* x, void* xo, const fb_shape_t* s, hipStream_t hs) 
 
 // The GEMV of a validated shape: one launch when a plan fits LDS, else row chunks.
 int gemv_planned(const void* wdev, const void* x, void* y, const fb_shape_t* s, int cus,
-                 hipStream_t hs) {
+                 hipStream_t hs, void* ws, size_t ws_bytes) {
   Plan pl;
+  // batch 8-16 on layers of few row tiles: the K-parts side by side, through the workspace
+  if (ws && splitk_parts(s, cus, &pl) && ws_bytes >= splitk_bytes(s, pl.P)) {
+    fb_shape_t sp = *s;
+    sp.y_dtype = FB_DT_F32;  // the parts' sums
+    const int st = launch_plan(wdev, x, ws, &sp, pl, hs);
+    if (st != FB_OK) return st;
+    const int64_t n = (int64_t)s->B * s->N;
+    hipLaunchKernelGGL(splitk_sum, dim3((unsigned)((n + 1023) / 1024)), dim3(256), 0, hs,
+                       static_cast<const float*>(ws), pl.P, n, y, s->y_dtype);
+    return hipGetLastError() == hipSuccess ? FB_OK : FB_ERR_HIP;
+  }
   if (make_plan(s, cus, pl)) return launch_plan(wdev, x, y, s, pl, hs);
   // No plan holds the whole batch in LDS (a 4096-wide rotation keeps an fp32 copy of every
   // batch row): the rows run in the largest chunks that fit, each streaming the weights.
@@ -1155,8 +1248,9 @@ int gemv_planned(const void* wdev, const void* x, void* y, const fb_shape_t* s, 
   return FB_OK;
 }
 
-// fb_gemv behind the ABI.  ws (ws_bytes) is the scratch for the once-per-call rotation of
-// larger batches; without enough of it the rotation runs in every workgroup's prologue.
+// fb_gemv behind the ABI.  ws (ws_bytes) holds the once-per-call rotation of larger batches
+// (rotated x, first) and the split-K parts' sums (after it); without enough of it the
+// rotation runs in every workgroup's prologue and the K-slices in turn.
 int gemv_impl(const void* wdev, const void* x, void* y, const fb_shape_t* s, void* ws,
               size_t ws_bytes, hipStream_t hs) {
   if (!s || !wdev || !x || !y) return FB_ERR_NULL;
@@ -1176,15 +1270,18 @@ int gemv_impl(const void* wdev, const void* x, void* y, const fb_shape_t* s, voi
     const int64_t grid = std::min<int64_t>(T, cus);
     if ((T + grid - 1) / grid * GS * fb::block_bytes(s->fmt) > INT32_MAX) return FB_ERR_SHAPE;
   }
+  if (ws && (reinterpret_cast<uintptr_t>(ws) & 255u)) ws = nullptr;  // misaligned: unused
+  if (!ws) ws_bytes = 0;
   const size_t need = rot_once_bytes(s);
-  if (need && ws && ws_bytes >= need && (reinterpret_cast<uintptr_t>(ws) & 255u) == 0) {
+  if (need && ws_bytes >= need) {
     st = launch_rotate(x, ws, s, hs);
     if (st != FB_OK) return st;
     fb_shape_t u = *s;
     u.fwht_block = 0;  // x' is rotated
-    return gemv_planned(wdev, ws, y, &u, cus, hs);
+    return gemv_planned(wdev, ws, y, &u, cus, hs, static_cast<uint8_t*>(ws) + need,
+                        ws_bytes - need);
   }
-  return gemv_planned(wdev, x, y, s, cus, hs);
+  return gemv_planned(wdev, x, y, s, cus, hs, ws, ws_bytes);
 }
 
 // Scratch of the allocation-free entry point: a file-scope device array (one per GPU the
@@ -1216,19 +1313,24 @@ int fb_gemv_noalloc(const void* wdev, const void* x, void* y, const fb_shape_t* 
   if (st != FB_OK) return st;
   const size_t need = rot_once_bytes(s);
   if (need > kScratchBytes) return FB_ERR_SCRATCH;
+  // the rotation's x' and, where they fit after it, the split-K parts' sums (else the
+  // K-slices run in turn, as without a workspace)
   void* ws = nullptr;
-  if (need) {
+  if (fb_workspace_bytes(s)) {
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess) return FB_ERR_HIP;
     ws = scratch_ptr(dev);
     if (!ws) return FB_ERR_HIP;
   }
-  return gemv_impl(wdev, x, y, s, ws, need ? kScratchBytes : 0, static_cast<hipStream_t>(stream));
+  return gemv_impl(wdev, x, y, s, ws, ws ? kScratchBytes : 0, static_cast<hipStream_t>(stream));
 }
 
 size_t fb_workspace_bytes(const fb_shape_t* s) {
   if (fb_validate(s) != FB_OK) return 0;
-  return rot_once_bytes(s);
+  const size_t rot = rot_once_bytes(s);
+  fb_shape_t u = *s;
+  if (rot) u.fwht_block = 0;  // the GEMV after the rotation is unrotated
+  return rot + splitk_bytes(&u, splitk_parts(&u, device_cus(), nullptr));
 }
 
 int fb_gemv(const void* wdev, const void* x, void* y, const fb_shape_t* s, void* ws,

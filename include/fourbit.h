@@ -75,9 +75,15 @@ int fb_validate(const fb_shape_t* s);
  * fb_gemv. */
 size_t fb_device_bytes(const fb_shape_t* s);
 
-/* Workspace bytes fb_gemv can use for this shape: B*K*2 (rounded up to 256) for rotated
- * shapes with B*K >= 16384, where x is rotated once into the workspace by its own small
- * kernel before the GEMV; 0 otherwise (and for invalid shapes). */
+/* Workspace bytes fb_gemv can use for this shape on the current device (0 for invalid
+ * shapes):
+ *  - B*K*2 (rounded up to 256) for rotated shapes with B*K >= 16384, where x is rotated
+ *    once into the workspace by its own small kernel before the GEMV;
+ *  - plus P*B*N*4 (rounded up to 256) where the GEMV runs its K-parts side by side (batch
+ *    >= 2 over a long K whose staged x would need 3 or more K-slices on few row tiles, e.g.
+ *    11008 -> 4096 at batch 16, P = 4): each part's fp32 sums, added by one more small
+ *    kernel in part order.
+ * The contents need no initialisation and are not kept between calls. */
 size_t fb_workspace_bytes(const fb_shape_t* s);
 
 /* ---------------------------------------------------------------------------------
@@ -149,9 +155,11 @@ int fb_dequant_host(const uint8_t* codes, const void* meta, float* w_out, const 
  * device memory; x is [B,K] of x_dtype, y is [B,N] of y_dtype.
  * ws: device workspace (256-byte aligned) of fb_workspace_bytes(s) bytes, or NULL.  With it,
  * a rotated call of B*K >= 16384 values rotates x once into ws (one extra small kernel)
- * and runs the unrotated GEMV on it; without it (NULL, too small or misaligned) every
- * workgroup rotates x in its prologue, which gives the same results within the tolerance
- * and is slower for such batches.  Calls that share a workspace must not overlap.
+ * and runs the unrotated GEMV on it, and a split-K shape runs its K-parts side by side with
+ * their sums in ws; without it (NULL, too small or misaligned) every workgroup rotates x in
+ * its prologue and the K-slices run in turn, which gives the same results within the
+ * tolerance (each plan is deterministic) and is slower for such shapes.  Calls that share a
+ * workspace must not overlap.
  * A batch whose staged activations do not fit LDS at once (a 4096-wide rotation done in
  * the prologue keeps an fp32 copy of every batch row) runs as several launches over row
  * chunks, each streaming the weights; FB_ERR_LDS only when a single row does not fit. */

@@ -259,8 +259,9 @@ def test_backward_matches_linear_with_decoded_weight(fmt, K, hadamard):
                                          (520, 8192, 4, 4096), (64, 4096, 4, 2048)])
 def test_rotated_batch_with_and_without_workspace(N, K, B, block):
     """Rotated batches of B*K >= 16384 values rotate x once into the workspace (an extra
-    small kernel), else (no workspace passed) in every workgroup's prologue: both within
-    tolerance of the oracle's rotated product, and of each other."""
+    small kernel; at batch 16 with K = 11008 the GEMV after it also runs its K-parts side by
+    side through the workspace), else (no workspace passed) in every workgroup's prologue:
+    both within tolerance of the oracle's rotated product, and of each other."""
     import ctypes
     say("rotate once", N, K, B, block)
     g = torch.Generator().manual_seed(N + K + B)
@@ -271,7 +272,8 @@ def test_rotated_batch_with_and_without_workspace(N, K, B, block):
     yref = O.y_ref("gf4", codes, pw.meta.numpy().view(np.uint16), x, block)
     shape = pw.shape(B, torch.float16, torch.float32)
     need = C.workspace_bytes(shape)
-    assert need == B * K * 2
+    # the rotated x, then (batch 16 at K = 11008) the split-K parts' sums
+    assert need == B * K * 2 or need == B * K * 2 + 4 * B * N * 4
     xd = x.to(DEV)
     ys = {}
     for mode in ("workspace", "none"):
@@ -287,3 +289,48 @@ def test_rotated_batch_with_and_without_workspace(N, K, B, block):
         ys[mode] = y.cpu()
     ok, emax = within_tol(ys["workspace"], ys["none"])
     assert ok, emax
+
+
+@pytest.mark.parametrize("fmt,N,ydt", [("gf4", 4096, torch.float16), ("e2m1", 4096, torch.bfloat16),
+                                       ("gf4", 1000, torch.float32), ("e2m1", 72, torch.float16)])
+def test_splitk_against_slices_and_oracle(fmt, N, ydt):
+    """Batch 16 at K = 11008 (22 spans: parts of 6, 6, 6 and 4) runs its K-parts side by side
+    through the workspace and adds their fp32 sums in part order: within tolerance of the
+    sliced plan (no workspace) and of the device-decoded weight x fp32 torch on all rows,
+    the same bits on a second call (the last part sums only its own spans), and sampled rows
+    against the oracle's exact decode.  The reference's batched product it replaces is
+    layers.h:9828-9839 / layers.py:36-38."""
+    import ctypes
+    K, B = 11008, 16
+    say("split-K", fmt, N, K, B, ydt)
+    g = torch.Generator().manual_seed(N + 7)
+    w = torch.randn(N, K, generator=g) * 0.02
+    pw = PackedWeight.quantize(w, fmt, device=DEV, packer="gpu" if fmt == "gf4" else "host")
+    xdt = torch.float16 if fmt == "gf4" else torch.bfloat16
+    x = (torch.randn(B, K, generator=g) * 0.5).to(xdt).to(DEV)
+    shape = pw.shape(B, xdt, ydt)
+    need = C.workspace_bytes(shape)
+    assert need == 4 * B * N * 4   # four parts
+    ws = torch.full((need,), 0xFF, dtype=torch.uint8, device=DEV)   # no zero-fill needed
+    L = C.lib()
+    sp = torch.cuda.current_stream().cuda_stream
+    outs = []
+    for ws_ptr, nws in ((ws.data_ptr(), need), (ws.data_ptr(), need), (None, 0)):
+        y = torch.full((B, N), float("nan"), dtype=ydt, device=DEV)
+        assert L.fb_gemv(pw.wdev.data_ptr(), x.data_ptr(), y.data_ptr(), ctypes.byref(shape),
+                         ws_ptr, nws, sp) == 0
+        outs.append(y)
+    torch.cuda.synchronize()
+    y_sk, y_sk2, y_sl = outs
+    assert torch.equal(y_sk, y_sk2)
+    W = pw.dequant_device(torch.float32)
+    yref = x.float() @ W.t()
+    extra = 4e-3 if ydt != torch.float32 else 0.0   # the output's own rounding
+    ok, emax = within_tol(y_sk, yref, extra)
+    assert ok, f"split-K vs torch: {emax}"
+    ok, emax = within_tol(y_sk, y_sl.float(), extra)
+    assert ok, f"split-K vs slices: {emax}"
+    rows = torch.randint(0, N, (8,), generator=g)
+    host = pw.dequant_host()[rows]
+    ok, emax = within_tol(y_sk[:, rows], torch.nn.functional.linear(x.cpu().float(), host), extra)
+    assert ok, f"split-K vs oracle decode: {emax}"

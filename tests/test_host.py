@@ -238,11 +238,22 @@ def test_quantize_module_swaps_linears_and_keeps_masks():
 
 
 def test_workspace_contract():
-    """fb_gemv's workspace is only for rotating x once per call: 0 bytes for unrotated
-    shapes and for rotated ones under 16384 activation values (B*K), else B*K*2 rounded
-    up to 256; invalid shapes report 0 and are still rejected by fb_gemv."""
+    """fb_gemv's workspace holds x rotated once per call (rotated shapes of at least 16384
+    activation values, B*K*2 rounded up to 256) and, for the split-K plan, the K-parts' fp32
+    sums after it (P*B*N*4: unrotated batches whose sliced plan needs 3 or more slices of a
+    long K over few row tiles); 0 bytes otherwise.  Invalid shapes report 0 and are still
+    rejected by fb_gemv."""
     for B in (1, 4, 16):
         assert C.workspace_bytes(C.make_shape(8192, 28672, B)) == 0
+    # 11008 -> 4096 at batch 16: 3 slices of 1 row tile each -> 4 parts side by side
+    assert C.workspace_bytes(C.make_shape(4096, 11008, 16)) == 4 * 16 * 4096 * 4
+    assert C.workspace_bytes(C.make_shape(4096, 11008, 16, C.FMT_E2M1, 0, C.DT_BF16)) == \
+        4 * 16 * 4096 * 4
+    assert C.workspace_bytes(C.make_shape(4096, 11008, 8)) == 0      # 2 slices
+    assert C.workspace_bytes(C.make_shape(8192, 8192, 16)) == 0      # K too short
+    # rotated once, then split-K on the rotated x: both, the sums after x'
+    assert C.workspace_bytes(C.make_shape(96, 11008, 16, C.FMT_GF4, 256)) == \
+        16 * 11008 * 2 + 4 * 16 * 96 * 4
     assert C.workspace_bytes(C.make_shape(4096, 4096, 3, C.FMT_GF4, 4096)) == 0
     assert C.workspace_bytes(C.make_shape(4096, 4096, 4, C.FMT_GF4, 4096)) == 4 * 4096 * 2
     assert C.workspace_bytes(C.make_shape(4096, 11008, 2, C.FMT_GF4, 256)) == 44032
