@@ -174,7 +174,9 @@ int fb_gemv(const void* wdev, const void* x, void* y, const fb_shape_t* s, void*
  * ends): rotated calls of B*K > 524288 values return FB_ERR_SCRATCH.  No hipMalloc, hipFree
  * or allocating library call is made.  Every call on a GPU shares that GPU's array, so
  * calls that overlap on one GPU (several streams or host threads) race; serialise them.
- * Results equal fb_gemv's with a workspace. */
+ * Split-K shapes keep their parts' sums in the array after the rotated x where they fit.
+ * Results equal fb_gemv's with a workspace bit for bit, except for split-K shapes whose sums
+ * do not fit: those run the K-slices in turn, within the tolerance of fb_gemv's result. */
 int fb_gemv_noalloc(const void* wdev, const void* x, void* y, const fb_shape_t* s,
                     void* stream);
 
