@@ -501,6 +501,53 @@ def jenks2_bench(n: int, steps: int) -> dict:
             "host_twin_threads": 1, "identical_to_host": bool(same)}
 
 
+def jenks2_filters_bench(shape, steps: int) -> dict:
+    """The per-filter two-class split (fb_jenks2_filters_gpu, the reference's Conv_Mask) over
+    a resident [out, in, kh, kw] fp32 weight: one 64-lane workgroup per filter.  Timed with
+    HIP events over back-to-back calls; the host twin (fb_jenks2_filters_host, 16 threads)
+    runs once on the same weight and must give the same splits, GVFs and mask."""
+    L = C.lib()
+    out_c, in_c, kh, kw = shape
+    nf, n = out_c * in_c, kh * kw
+    g = torch.Generator().manual_seed(8)
+    w = torch.randn(nf, n, generator=g) * 0.05
+    wd = w.to("cuda:0")
+    keep = torch.empty(nf, n, dtype=torch.uint8, device="cuda:0")
+    split = torch.empty(nf, dtype=torch.int32, device="cuda:0")
+    gvf = torch.empty(nf, dtype=torch.float64, device="cuda:0")
+    sp = torch.cuda.current_stream().cuda_stream
+
+    def call():
+        C.check(L.fb_jenks2_filters_gpu(wd.data_ptr(), nf, n, keep.data_ptr(), split.data_ptr(),
+                                        gvf.data_ptr(), sp))
+
+    t_end = time.perf_counter() + MIN_WARM_S
+    while time.perf_counter() < t_end:
+        for _ in range(5):
+            call()
+        torch.cuda.synchronize()
+    regions = []
+    for _ in range(5):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        call()
+        e0.record()
+        for _ in range(steps):
+            call()
+        e1.record()
+        torch.cuda.synchronize()
+        regions.append(e0.elapsed_time(e1) / steps * 1e3)
+    t = time.perf_counter()
+    hk, hs, hg = C.jenks2_filters_host(w, nthreads=16)
+    host_s = time.perf_counter() - t
+    same = (torch.equal(hk, keep.cpu().bool()) and torch.equal(hs, split.cpu())
+            and torch.equal(hg.view(torch.int64), gvf.cpu().view(torch.int64)))
+    us = float(np.median(regions))
+    return {"jenks2_filters": list(shape), "filters": nf, "values_per_filter": n,
+            "us_per_call_median": us, "us_per_call_regions": regions,
+            "filters_per_s": nf / (us * 1e-6), "host_twin_s": host_s, "host_twin_threads": 16,
+            "identical_to_host": bool(same)}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -524,6 +571,9 @@ def main():
                          "print a JSON summary")
     ap.add_argument("--jenks2", type=int, default=0, metavar="N",
                     help="only time the two-class Jenks mask (fb_jenks2_gpu) over N values")
+    ap.add_argument("--jenks2-filters", default="", metavar="OUT,IN,KH,KW",
+                    help="only time the per-filter Jenks mask (fb_jenks2_filters_gpu) on a "
+                         "convolution weight of that shape")
     args = ap.parse_args()
     if args.calib_copy:
         # a plain copy kernel of known size: FETCH_SIZE / WRITE_SIZE per dispatch of it
@@ -548,6 +598,12 @@ def main():
         return
     if args.jenks2:
         print(json.dumps(jenks2_bench(args.jenks2, min(args.steps, 50))))
+        return
+    if args.jenks2_filters:
+        shape = tuple(int(v) for v in args.jenks2_filters.split(","))
+        if len(shape) != 4:
+            ap.error("--jenks2-filters takes OUT,IN,KH,KW")
+        print(json.dumps(jenks2_filters_bench(shape, min(args.steps, 50))))
         return
 
     if args.sweep:

@@ -332,100 +332,267 @@ int grid_of(int64_t items, int threads) { return (int)((items + threads - 1) / t
 
 // ---------------------------------------------------------------------------------
 // Every filter of a convolution weight on its own (the reference's Conv_Mask,
-// cuda_helpers.py:333-376, over its kernel at :219-255): one 64-lane workgroup per filter of
-// n <= FB_JENKS2_FILTER_MAX values.
+// cuda_helpers.py:333-376, over its kernel at :219-255), filters of n <= FB_JENKS2_FILTER_MAX
+// values:
 //  - The stable ascending order by counting: the rank of value i is the number of values
 //    that sort before it, (w_j < w_i) or (w_j == w_i and j < i), so -0.0 and +0.0 tie and
-//    keep their index order, as the host's stable sort does.  O(n^2 / 64) per lane, no
-//    sorting network, no workspace.
-//  - The fp64 sums of the rule above in one lane, in the host's association order: with
-//    n <= 1024 there are at most 4 blocks and one superblock, and every addition the host
-//    makes (zeros included) is made here in the same order.
+//    keep their index order, as the host's stable sort does.  No sorting network, no
+//    workspace.
+//  - The fp64 sums of the rule above in one lane per filter, in the host's association
+//    order: with n <= 1024 there are at most 4 blocks and one superblock, and every
+//    addition the host makes (zeros included) is made here in the same order.
+// Many small filters (n <= kLaneFilterMax: 1x1 to 5x5, the common conv kernels; at least
+// kLaneFilterMin of them) run one filter per lane, 256 per workgroup.  Otherwise each filter
+// has a one-wave workgroup (so that a few filters still spread over the CUs), each lane
+// ranking its up to 16 values against the filter, read once per value from LDS.
 // ---------------------------------------------------------------------------------
 constexpr int kFilterMax = FB_JENKS2_FILTER_MAX;
+constexpr int kLaneFilterMax = 25;  // 256 filters x 10 bytes per value fit 64 KiB of LDS
+constexpr int kLaneFilterMin = 1024;  // 4 workgroups: fewer filters spread better one per wave
 static_assert(kFilterMax <= 4 * kBlk, "one superblock of at most 4 blocks");
 
-__global__ __launch_bounds__(64) void j2_filters(const float* __restrict__ w, int n,
-                                                 uint8_t* __restrict__ keep,
-                                                 int* __restrict__ split,
-                                                 double* __restrict__ gvf) {
-  __shared__ float v[kFilterMax];
-  __shared__ float srt[kFilterMax];
-  __shared__ int ord[kFilterMax];
-  __shared__ int arg_s;
-  const int64_t f = blockIdx.x;
-  const int lane = threadIdx.x;
-  const float* wf = w + f * n;
-  for (int i = lane; i < n; i += 64) v[i] = wf[i];
-  __syncthreads();
-  for (int i = lane; i < n; i += 64) {
-    const float x = v[i];
-    int r = 0;
-    for (int j = 0; j < n; ++j) {
-      const float y = v[j];
-      r += (y < x || (y == x && j < i)) ? 1 : 0;
+// The split and GVF of one sorted filter (srt, n values), in the host's order.
+__device__ void filter_split(const float* srt, int n, int& arg_out, double& gvf_out) {
+  const int nblk = (n + kBlk - 1) / kBlk;
+  const double c = (double)srt[n / 2];
+  double t1[4], t2[4], bx1[4], bx2[4];
+  for (int b = 0; b < nblk; ++b) {  // block totals
+    double a1 = 0.0, a2 = 0.0;
+    for (int i = b * kBlk; i < min(n, b * kBlk + kBlk); ++i) {
+      const double d = (double)srt[i] - c;
+      const double q = d * d;
+      a1 = a1 + d;
+      a2 = a2 + q;
     }
-    srt[r] = x;
-    ord[r] = i;
+    t1[b] = a1;
+    t2[b] = a2;
+  }
+  double u1, u2;  // the one superblock: exclusive block offsets, then its total
+  {
+    double a1 = 0.0, a2 = 0.0;
+    for (int b = 0; b < nblk; ++b) {
+      bx1[b] = a1;
+      bx2[b] = a2;
+      a1 = a1 + t1[b];
+      a2 = a2 + t2[b];
+    }
+    u1 = a1;
+    u2 = a2;
+  }
+  const double sx1 = 0.0, sx2 = 0.0;  // the superblocks' exclusive offset (one superblock)
+  const double pt = 0.0 + u1, qt = 0.0 + u2;
+  double best = 0.0, ssd0 = 0.0;
+  int arg = -1;
+  for (int b = 0; b < nblk; ++b) {
+    const double base1 = sx1 + bx1[b], base2 = sx2 + bx2[b];
+    double l1 = 0.0, l2 = 0.0;
+    for (int i = b * kBlk; i < min(n, b * kBlk + kBlk); ++i) {
+      const double p = base1 + l1, q = base2 + l2;
+      const double left = i == 0 ? 0.0 : q - (p * p) / (double)i;
+      const double rp = pt - p;
+      const double right = (qt - q) - (rp * rp) / (double)(n - i);
+      const double val = left + right;
+      if (arg < 0 || val < best) {
+        best = val;
+        arg = i;
+      }
+      if (i == 0) ssd0 = val;
+      const double d = (double)srt[i] - c;
+      const double dq = d * d;
+      l1 = l1 + d;
+      l2 = l2 + dq;
+    }
+  }
+  arg_out = arg;
+  gvf_out = (ssd0 - best) / (ssd0 + 1e-8);
+}
+
+// The same sums for a wave: one lane stores P(i), Q(i) (the class-0 sums before value i, in
+// the host's association order) and the totals; the SSD of every split (two fp64 divisions
+// each, the bulk of the work) is then evaluated by all lanes, and the first minimum found by
+// a (value, index) reduction, which picks what the host's sequential strict-< scan picks.
+__device__ void filter_prefix(const float* srt, int n, double* P, double* Q, double* tot) {
+  const int nblk = (n + kBlk - 1) / kBlk;
+  const double c = (double)srt[n / 2];
+  double t1[4], t2[4], bx1[4], bx2[4];
+  for (int b = 0; b < nblk; ++b) {
+    double a1 = 0.0, a2 = 0.0;
+    for (int i = b * kBlk; i < min(n, b * kBlk + kBlk); ++i) {
+      const double d = (double)srt[i] - c;
+      const double q = d * d;
+      a1 = a1 + d;
+      a2 = a2 + q;
+    }
+    t1[b] = a1;
+    t2[b] = a2;
+  }
+  double u1, u2;
+  {
+    double a1 = 0.0, a2 = 0.0;
+    for (int b = 0; b < nblk; ++b) {
+      bx1[b] = a1;
+      bx2[b] = a2;
+      a1 = a1 + t1[b];
+      a2 = a2 + t2[b];
+    }
+    u1 = a1;
+    u2 = a2;
+  }
+  const double sx1 = 0.0, sx2 = 0.0;
+  tot[0] = 0.0 + u1;
+  tot[1] = 0.0 + u2;
+  for (int b = 0; b < nblk; ++b) {
+    const double base1 = sx1 + bx1[b], base2 = sx2 + bx2[b];
+    double l1 = 0.0, l2 = 0.0;
+    for (int i = b * kBlk; i < min(n, b * kBlk + kBlk); ++i) {
+      P[i] = base1 + l1;
+      Q[i] = base2 + l2;
+      const double d = (double)srt[i] - c;
+      const double dq = d * d;
+      l1 = l1 + d;
+      l2 = l2 + dq;
+    }
+  }
+}
+
+// n <= kLaneFilterMax: thread t of the workgroup does filter blockIdx.x * 256 + t.  LDS: the
+// values, their sorted copy, the positions (bytes) and the mask (bytes), 256 filters each.
+__global__ __launch_bounds__(256) void j2_filters_lane(const float* __restrict__ w, int64_t nf,
+                                                       int n, uint8_t* __restrict__ keep,
+                                                       int* __restrict__ split,
+                                                       double* __restrict__ gvf) {
+  extern __shared__ float lds_f[];
+  const int64_t f0 = (int64_t)blockIdx.x * 256;
+  const int cnt = (int)min((int64_t)256, nf - f0);
+  float* v = lds_f;
+  float* srt = v + 256 * n;
+  uint8_t* ord = reinterpret_cast<uint8_t*>(srt + 256 * n);
+  uint8_t* mk = ord + 256 * n;
+  for (int e = threadIdx.x; e < cnt * n; e += 256) v[e] = w[f0 * n + e];  // coalesced
+  __syncthreads();
+  const int t = threadIdx.x;
+  if (t < cnt) {
+    const float* vf = v + t * n;
+    float* sf = srt + t * n;
+    uint8_t* of = ord + t * n;
+    for (int i = 0; i < n; ++i) {
+      const float x = vf[i];
+      int r = 0;
+#pragma unroll 5
+      for (int j = 0; j < n; ++j) {
+        const float y = vf[j];
+        r += (int)(y < x) | ((int)(y == x) & (int)(j < i));
+      }
+      sf[r] = x;
+      of[r] = (uint8_t)i;
+    }
+    int arg;
+    double g;
+    filter_split(sf, n, arg, g);
+    split[f0 + t] = arg;
+    gvf[f0 + t] = g;
+    for (int r = 0; r < n; ++r) mk[t * n + of[r]] = r >= arg ? 1 : 0;
   }
   __syncthreads();
+  for (int e = threadIdx.x; e < cnt * n; e += 256) keep[f0 * n + e] = mk[e];  // coalesced
+}
+
+// LDS of the one-wave filter kernel: the values and their sorted copy (fp32), the positions
+// (int16, padded to 8 bytes), then the class sums P, Q and the two totals (fp64).
+__host__ __device__ inline size_t wave_sums_offset(int n) {
+  return ((size_t)n * 8 + (size_t)n * 2 + 7) & ~size_t(7);
+}
+__host__ __device__ inline size_t wave_lds_bytes(int n) {
+  return wave_sums_offset(n) + (size_t)n * 16 + 16;
+}
+
+// One filter per one-wave workgroup (blockIdx.x).  Each lane keeps its values l, l + 64, ...
+// (KC of them, KC = n / 64 rounded up to a power of two, at most 16) in registers and counts,
+// for each of them, the values that sort before it, reading every value of the filter once
+// from LDS; KC is a template argument so that the counting loop has no branch.
+constexpr int kPerLane = (kFilterMax + 63) / 64;
+template <int KC>
+__device__ void rank_wave(const float* v, int n, int lane, float* srt, int16_t* ord) {
+  float xs[KC];
+  int rs[KC];
+#pragma unroll
+  for (int k = 0; k < KC; ++k) {
+    const int i = lane + 64 * k;
+    xs[k] = i < n ? v[i] : 0.0f;
+    rs[k] = 0;
+  }
+  for (int j = 0; j < n; ++j) {
+    const float y = v[j];
+#pragma unroll
+    for (int k = 0; k < KC; ++k)  // branch-free: bitwise, not short-circuit, operators
+      rs[k] += (int)(y < xs[k]) | ((int)(y == xs[k]) & (int)(j < lane + 64 * k));
+  }
+#pragma unroll
+  for (int k = 0; k < KC; ++k) {
+    const int i = lane + 64 * k;
+    if (i < n) {
+      srt[rs[k]] = xs[k];
+      ord[rs[k]] = (int16_t)i;
+    }
+  }
+}
+
+__global__ __launch_bounds__(64) void j2_filters_wave(const float* __restrict__ w, int n,
+                                                      uint8_t* __restrict__ keep,
+                                                      int* __restrict__ split,
+                                                      double* __restrict__ gvf) {
+  extern __shared__ float lds_f[];
+  const int lane = threadIdx.x;
+  const int64_t f = blockIdx.x;
+  float* v = lds_f;
+  float* srt = v + n;
+  int16_t* ord = reinterpret_cast<int16_t*>(srt + n);
+  for (int i = lane; i < n; i += 64) v[i] = w[f * n + i];
+  __syncthreads();
+  const int kc = (n + 63) / 64;
+  if (kc <= 1)
+    rank_wave<1>(v, n, lane, srt, ord);
+  else if (kc <= 2)
+    rank_wave<2>(v, n, lane, srt, ord);
+  else if (kc <= 4)
+    rank_wave<4>(v, n, lane, srt, ord);
+  else if (kc <= 8)
+    rank_wave<8>(v, n, lane, srt, ord);
+  else
+    rank_wave<kPerLane>(v, n, lane, srt, ord);
+  __syncthreads();
+  double* P = reinterpret_cast<double*>(reinterpret_cast<uint8_t*>(lds_f) + wave_sums_offset(n));
+  double* Q = P + n;
+  double* tot = Q + n;
+  if (lane == 0) filter_prefix(srt, n, P, Q, tot);
+  __syncthreads();
+  const double pt = tot[0], qt = tot[1];
+  double best = 0.0, ssd0 = 0.0;
+  int arg = -1;
+  for (int i = lane; i < n; i += 64) {  // ascending per lane: the lane's first minimum
+    const double p = P[i], q = Q[i];
+    const double left = i == 0 ? 0.0 : q - (p * p) / (double)i;
+    const double rp = pt - p;
+    const double right = (qt - q) - (rp * rp) / (double)(n - i);
+    const double val = left + right;
+    if (arg < 0 || val < best) {
+      best = val;
+      arg = i;
+    }
+    if (i == 0) ssd0 = val;
+  }
+  for (int m = 32; m >= 1; m >>= 1) {  // the smallest (value, index), lanes without one last
+    const double ob = __shfl_xor(best, m, 64);
+    const int oa = __shfl_xor(arg, m, 64);
+    if (oa >= 0 && (arg < 0 || ob < best || (ob == best && oa < arg))) {
+      best = ob;
+      arg = oa;
+    }
+  }
   if (lane == 0) {
-    const int nblk = (n + kBlk - 1) / kBlk;
-    const double c = (double)srt[n / 2];
-    double t1[4], t2[4], bx1[4], bx2[4];
-    for (int b = 0; b < nblk; ++b) {  // block totals
-      double a1 = 0.0, a2 = 0.0;
-      for (int i = b * kBlk; i < min(n, b * kBlk + kBlk); ++i) {
-        const double d = (double)srt[i] - c;
-        const double q = d * d;
-        a1 = a1 + d;
-        a2 = a2 + q;
-      }
-      t1[b] = a1;
-      t2[b] = a2;
-    }
-    double u1, u2;  // the one superblock: exclusive block offsets, then its total
-    {
-      double a1 = 0.0, a2 = 0.0;
-      for (int b = 0; b < nblk; ++b) {
-        bx1[b] = a1;
-        bx2[b] = a2;
-        a1 = a1 + t1[b];
-        a2 = a2 + t2[b];
-      }
-      u1 = a1;
-      u2 = a2;
-    }
-    const double sx1 = 0.0, sx2 = 0.0;  // the superblocks' exclusive offset (one superblock)
-    const double pt = 0.0 + u1, qt = 0.0 + u2;
-    double best = 0.0, ssd0 = 0.0;
-    int arg = -1;
-    for (int b = 0; b < nblk; ++b) {
-      const double base1 = sx1 + bx1[b], base2 = sx2 + bx2[b];
-      double l1 = 0.0, l2 = 0.0;
-      for (int i = b * kBlk; i < min(n, b * kBlk + kBlk); ++i) {
-        const double p = base1 + l1, q = base2 + l2;
-        const double left = i == 0 ? 0.0 : q - (p * p) / (double)i;
-        const double rp = pt - p;
-        const double right = (qt - q) - (rp * rp) / (double)(n - i);
-        const double val = left + right;
-        if (arg < 0 || val < best) {
-          best = val;
-          arg = i;
-        }
-        if (i == 0) ssd0 = val;
-        const double d = (double)srt[i] - c;
-        const double dq = d * d;
-        l1 = l1 + d;
-        l2 = l2 + dq;
-      }
-    }
     split[f] = arg;
     gvf[f] = (ssd0 - best) / (ssd0 + 1e-8);
-    arg_s = arg;
   }
-  __syncthreads();
-  const int arg = arg_s;
   for (int r = lane; r < n; r += 64) keep[f * n + ord[r]] = r >= arg ? 1 : 0;
 }
 
@@ -499,8 +666,13 @@ int fb_jenks2_filters_gpu(const float* w, int64_t nf, int32_t n, uint8_t* keep, 
   if ((reinterpret_cast<uintptr_t>(w) & 3u) || (reinterpret_cast<uintptr_t>(split) & 3u) ||
       (reinterpret_cast<uintptr_t>(gvf) & 7u))
     return FB_ERR_ALIGN;
-  hipLaunchKernelGGL(j2_filters, dim3((unsigned)nf), dim3(64), 0, static_cast<hipStream_t>(stream),
-                     w, (int)n, keep, split, gvf);
+  hipStream_t hs = static_cast<hipStream_t>(stream);
+  if (n <= kLaneFilterMax && nf >= kLaneFilterMin)
+    hipLaunchKernelGGL(j2_filters_lane, dim3((unsigned)((nf + 255) / 256)), dim3(256),
+                       (size_t)256 * n * 10, hs, w, nf, (int)n, keep, split, gvf);
+  else
+    hipLaunchKernelGGL(j2_filters_wave, dim3((unsigned)nf), dim3(64),
+                       wave_lds_bytes(n), hs, w, (int)n, keep, split, gvf);
   return hipGetLastError() == hipSuccess ? FB_OK : FB_ERR_HIP;
 }
 

@@ -87,8 +87,12 @@ def _filter_inputs():
     filter sizes, the per-filter maximum of 1024 values, ties, signed zeros and constant
     filters."""
     rng = np.random.default_rng(12)
+    # one filter per lane for 1024 or more filters of at most 25 values (2100 filters: a
+    # partial last workgroup; 1 and 4 values), else one filter per one-wave workgroup (25
+    # values in 6 filters; 26 values, the smallest size never run per lane)
     for shape in ((6, 1, 5, 5), (64, 64, 3, 3), (64, 3, 11, 11), (64, 3, 7, 7), (2, 3, 32, 32),
-                  (7, 5, 1, 1), (3, 2, 16, 17)):
+                  (7, 5, 1, 1), (3, 2, 16, 17), (3, 3, 2, 13), (300, 7, 3, 3), (7, 3, 2, 13),
+                  (1024, 2, 1, 1), (40, 30, 2, 2), (64, 32, 5, 5)):
         yield f"random{shape}", (rng.standard_normal(shape) * 0.05).astype(np.float32)
     w = (np.round(rng.standard_normal((32, 16, 3, 3)) * 2) / 4).astype(np.float32)
     w[::3] = 0.0
@@ -97,7 +101,7 @@ def _filter_inputs():
     yield "ties", w
 
 
-@pytest.mark.parametrize("case", list(range(8)))
+@pytest.mark.parametrize("case", list(range(14)))
 def test_jenks2_filters_gpu_bit_exact_vs_host(case):
     """fb_jenks2_filters_gpu (the reference's Conv_Mask, cuda_helpers.py:333-376) against
     its host twin, bit for bit, on every filter: split, GVF and mask."""
