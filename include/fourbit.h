@@ -256,10 +256,11 @@ int fb_jenks2_gpu(const float* w, int64_t n, uint8_t* keep, int64_t* split, doub
 int fb_jenks2_filters_host(const float* w, int64_t nf, int32_t n, uint8_t* keep, int32_t* split,
                            double* gvf, int32_t nthreads);
 
-/* GPU version, bit-identical to fb_jenks2_filters_host: one 64-lane workgroup per filter
- * (stable ranks by counting, the fp64 sums in one lane), no workspace.  w, keep, split and
- * gvf are device pointers; asynchronous on the stream.  Non-finite values are not detected
- * (the host version rejects them with FB_ERR_VALUE). */
+/* GPU version, bit-identical to fb_jenks2_filters_host: stable ranks by counting and the
+ * fp64 sums in the host's order, one filter per lane for 1024 or more filters of at most 25
+ * values, else one filter per one-wave workgroup; no workspace.  w, keep, split and gvf are
+ * device pointers; asynchronous on the stream.  Non-finite values are not detected (the
+ * host version rejects them with FB_ERR_VALUE). */
 int fb_jenks2_filters_gpu(const float* w, int64_t nf, int32_t n, uint8_t* keep, int32_t* split,
                           double* gvf, void* stream);
 
