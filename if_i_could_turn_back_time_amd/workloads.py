@@ -44,6 +44,10 @@ WORKLOADS = {
     "gf4_k8192_n8192_b16": ("gf4", 8192, 8192, 16, "cfg1", False),
     "gf4_k8192_n28672_b8": ("gf4", 8192, 28672, 8, "cfg1", False),
     "gf4_k8192_n28672_b16": ("gf4", 8192, 28672, 16, "cfg1", False),
+    # batch 16 over the Llama-7B down projection (K = 11008, 3 K-slices of x on one row tile
+    # per CU): the shape the split-K plan is for
+    "gf4_k11008_n4096_b16": ("gf4", 11008, 4096, 16, "cfg1", False),
+    "e2m1_k11008_n4096_b16": ("e2m1", 11008, 4096, 16, "cfg2", False),
     # the reference's own 4-bit weight (QuantLinear.commit) as GF4 integer-level codebooks
     "int4ref_k8192_n28672_b1": ("int4ref", 8192, 28672, 1, "cfg4", False),
 }

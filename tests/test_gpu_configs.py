@@ -90,6 +90,8 @@ def check_layer(fmt, K, N, B, kind):
     ("e2m1", 8192, 28672, "cfg2", 8), ("e2m1", 8192, 28672, "cfg2", 16),
     ("gf4", 8192, 8192, "cfg1", 8), ("gf4", 8192, 8192, "cfg1", 16),
     ("gf4", 8192, 28672, "cfg1", 8), ("gf4", 8192, 28672, "cfg1", 16),
+    # batch 16 over the Llama-7B down projection: the split-K plan's shape
+    ("e2m1", 11008, 4096, "cfg2", 16), ("gf4", 11008, 4096, "cfg1", 16),
 ], ids=lambda v: str(v))
 def test_config5_small_batch(fmt, K, N, kind, B):
     say("config 5", fmt, K, N, B)
