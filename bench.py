@@ -56,7 +56,7 @@ def n_copies(nbytes: int, cold: bool) -> int:
 
 
 def time_gpu(pw: PackedWeight, x: torch.Tensor, y: torch.Tensor, steps: int, warmup: int,
-             cold: bool = True, windows: int = 0):
+             cold: bool = True, windows: int = 0, mx: bool = False):
     """Back-to-back launches on the current stream, timed with HIP events on that stream
     (the stream fb_gemv launches on).  cold: cycle through weight copies that together
     exceed the Infinity Cache.
@@ -66,7 +66,8 @@ def time_gpu(pw: PackedWeight, x: torch.Tensor, y: torch.Tensor, steps: int, war
     event is stamped on a busy GPU: the host's first launch latency (argument checks,
     plan, ctypes) would otherwise land inside the region.  ``windows`` more regions of
     the same length follow for the median.  Returns (mean ms per call of the first
-    region, number of weight copies, [ms per call of each extra region])."""
+    region, number of weight copies, [ms per call of each extra region]).  mx: time
+    fb_gemv_mx (the native FP4 path, its x split included) instead of fb_gemv."""
     L = C.lib()
     shape = pw.shape(x.shape[0], x.dtype, y.dtype)
     sref = ctypes.byref(shape)
@@ -74,7 +75,12 @@ def time_gpu(pw: PackedWeight, x: torch.Tensor, y: torch.Tensor, steps: int, war
     copies = [pw.wdev] + [pw.wdev.clone() for _ in range(ncp - 1)]
     wps = [c.data_ptr() for c in copies]
     xp, yp = x.data_ptr(), y.data_ptr()
-    ws = C.new_workspace(shape, x.device)
+    if mx:
+        ws = torch.empty(C.mx_workspace_bytes(shape), dtype=torch.uint8, device=x.device)
+        gemv = L.fb_gemv_mx
+    else:
+        ws = C.new_workspace(shape, x.device)
+        gemv = L.fb_gemv
     wsp, nws = (ws.data_ptr(), ws.numel()) if ws is not None else (None, 0)
     stream = torch.cuda.current_stream()
     sp = stream.cuda_stream
@@ -84,7 +90,7 @@ def time_gpu(pw: PackedWeight, x: torch.Tensor, y: torch.Tensor, steps: int, war
     done, t_end = 0, time.perf_counter() + MIN_WARM_S
     while done < warmup or time.perf_counter() < t_end:
         for _ in range(50):
-            C.check(L.fb_gemv(wps[done % ncp], xp, yp, sref, wsp, nws, sp))
+            C.check(gemv(wps[done % ncp], xp, yp, sref, wsp, nws, sp))
             done += 1
         torch.cuda.synchronize()
     global LAST_WARMUP_CALLS
@@ -93,12 +99,12 @@ def time_gpu(pw: PackedWeight, x: torch.Tensor, y: torch.Tensor, steps: int, war
     def region():
         torch.cuda.synchronize()
         for i in range(PRE_CALLS):
-            L.fb_gemv(wps[i % ncp], xp, yp, sref, wsp, nws, sp)
+            gemv(wps[i % ncp], xp, yp, sref, wsp, nws, sp)
         t0 = torch.cuda.Event(enable_timing=True)
         t1 = torch.cuda.Event(enable_timing=True)
         t0.record(stream)
         for i in range(steps):
-            L.fb_gemv(wps[(PRE_CALLS + i) % ncp], xp, yp, sref, wsp, nws, sp)
+            gemv(wps[(PRE_CALLS + i) % ncp], xp, yp, sref, wsp, nws, sp)
         t1.record(stream)
         torch.cuda.synchronize()
         return t0.elapsed_time(t1) / steps
@@ -247,10 +253,14 @@ def time_gpu_pack(w: torch.Tensor, pw: PackedWeight, reps: int = 3):
 
 def run_workload(name: str, steps: int, warmup: int, want_cpu: bool, check: bool = True,
                  warm: bool = False, cache: dict | None = None, pack_check: bool = False,
-                 packer: str = "host", windows: int = 0, cpu_budget_s: float = 12.0):
+                 packer: str = "host", windows: int = 0, cpu_budget_s: float = 12.0,
+                 mx: bool = False):
     """cache: packed weights by (fmt, K, N, kind, rotation), reused across batch sizes (the
-    weights are drawn before the activations, so they do not depend on the batch)."""
+    weights are drawn before the activations, so they do not depend on the batch).  mx: the
+    native FP4 path (fb_gemv_mx; unrotated E2M1 workloads)."""
     fmt, K, N, B, kind, fwht = WORKLOADS[name]
+    if mx and (fmt != "e2m1" or fwht):
+        raise ValueError(f"{name}: the native FP4 path takes unrotated E2M1 layers")
     xdt = torch.float16 if fmt in ("gf4", "int4ref") else torch.bfloat16
     w, x = workloads.synth(kind, N, K, B, xdt)
     fb = fwht_block_for(K) if fwht else 0
@@ -276,7 +286,7 @@ def run_workload(name: str, steps: int, warmup: int, want_cpu: bool, check: bool
     del w
     xd = x.to("cuda:0")
     y = torch.empty(B, N, dtype=xdt, device="cuda:0")
-    ms, ncp, extra = time_gpu(pw, xd, y, steps, warmup, cold=True, windows=windows)
+    ms, ncp, extra = time_gpu(pw, xd, y, steps, warmup, cold=True, windows=windows, mx=mx)
     warm_calls = LAST_WARMUP_CALLS
     ms_warm = time_gpu(pw, xd, y, steps, warmup, cold=False)[0] if warm else None
     ms_graph = time_gpu_graph(pw, xd, y, min(steps, 200)) if warm else None
@@ -284,6 +294,7 @@ def run_workload(name: str, steps: int, warmup: int, want_cpu: bool, check: bool
     gbs = nbytes / (ms * 1e-3) / 1e9
     rec = {
         "workload": name, "fmt": fmt, "K": K, "N": N, "B": B, "fwht_block": fb,
+        "path": "fp4_mfma" if mx else "exact_decode",
         "bytes_per_call": nbytes, "weight_stream_bytes": N * K // 2,
         "us_per_call": ms * 1e3, "GBps": gbs, "frac_of_8TBps": gbs / PEAK_GBS,
         "weight_copies_cycled": ncp, "warmup_calls_run": warm_calls,
@@ -297,7 +308,10 @@ def run_workload(name: str, steps: int, warmup: int, want_cpu: bool, check: bool
     }
     if check:  # spot parity: sampled rows vs exact host decode + F.linear (fp32)
         yk = torch.empty(B, N, dtype=torch.float32, device="cuda:0")
-        pw.gemv(xd, out=yk)
+        if mx:
+            pw.gemv_mx(xd, out=yk)
+        else:
+            pw.gemv(xd, out=yk)
         rows = torch.randint(0, N, (64,), generator=torch.Generator().manual_seed(1))
         Wr = torch.from_numpy(np.stack([pw.dequant_host_row(int(r)) for r in rows]))
         xin = x.float()
@@ -571,6 +585,10 @@ def main():
                          "print a JSON summary")
     ap.add_argument("--jenks2", type=int, default=0, metavar="N",
                     help="only time the two-class Jenks mask (fb_jenks2_gpu) over N values")
+    ap.add_argument("--mx", action="store_true",
+                    help="only compare the native FP4 path (fb_gemv_mx) with the exact-decode "
+                         "path on every unrotated E2M1 workload (or --workload, if it is one), "
+                         "one JSON line per path")
     ap.add_argument("--jenks2-filters", default="", metavar="OUT,IN,KH,KW",
                     help="only time the per-filter Jenks mask (fb_jenks2_filters_gpu) on a "
                          "convolution weight of that shape")
@@ -598,6 +616,20 @@ def main():
         return
     if args.jenks2:
         print(json.dumps(jenks2_bench(args.jenks2, min(args.steps, 50))))
+        return
+    if args.mx:
+        names = [n for n in sorted(WORKLOADS) if WORKLOADS[n][0] == "e2m1" and not WORKLOADS[n][5]]
+        if args.workload in names:
+            names = [args.workload]
+        cache = {}
+        for name in names:
+            for mx in (False, True):
+                rec, pw = run_workload(name, args.steps, args.warmup, False, cache=cache,
+                                       windows=MEDIAN_WINDOWS, mx=mx)
+                del pw
+                print(json.dumps({k: rec[k] for k in (
+                    "workload", "path", "K", "N", "B", "bytes_per_call", "us_per_call_median",
+                    "us_per_call_windows", "parity_ok", "parity_max_abs_err")}), flush=True)
         return
     if args.jenks2_filters:
         shape = tuple(int(v) for v in args.jenks2_filters.split(","))

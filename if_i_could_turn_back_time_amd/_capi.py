@@ -35,6 +35,7 @@ EXPORTED = (
     "fb_from_device", "fb_dequant_host", "fb_gemv", "fb_dequant", "fb_quantize_gf4_gpu",
     "fb_quantize_e2m1_gpu", "fb_jenks2_host", "fb_jenks2_workspace", "fb_jenks2_gpu",
     "fb_jenks2_filters_host", "fb_jenks2_filters_gpu", "fb_gemv_noalloc",
+    "fb_mx_split_bytes", "fb_mx_split", "fb_mx_workspace_bytes", "fb_gemv_mx",
 )
 
 
@@ -84,6 +85,10 @@ def lib() -> ctypes.CDLL:
         "fb_jenks2_filters_gpu": (ctypes.c_int, [vp, ctypes.c_int64, ctypes.c_int32, vp, vp, vp,
                                                  vp]),
         "fb_gemv_noalloc": (ctypes.c_int, [vp, vp, vp, sp, vp]),
+        "fb_mx_split_bytes": (sz, [sp]),
+        "fb_mx_split": (ctypes.c_int, [vp, vp, sp, vp]),
+        "fb_mx_workspace_bytes": (sz, [sp]),
+        "fb_gemv_mx": (ctypes.c_int, [vp, vp, vp, sp, vp, sz, vp]),
     }
     for name, (res, args) in sigs.items():
         fn = getattr(L, name)
@@ -254,6 +259,75 @@ def gemv(wdev: torch.Tensor, x: torch.Tensor, y: torch.Tensor, shape: FbShape,
         check(lib().fb_gemv(_ptr(wdev), _ptr(x), _ptr(y), ctypes.byref(shape), wp, need,
                             _stream(x.device)))
     return y
+
+
+def _check_gemv_operands(name, wdev, x, y, shape):
+    if not (wdev.is_cuda and x.is_cuda and y.is_cuda):
+        raise RuntimeError(f"{name} needs device tensors (ROCm GPU)")
+    if not (wdev.device == x.device == y.device):
+        raise ValueError(f"{name} operands are on different devices: weight {wdev.device}, "
+                         f"x {x.device}, y {y.device}")
+    if not (x.is_contiguous() and y.is_contiguous()):
+        raise ValueError("x and y must be contiguous")
+    if x.dtype not in DTYPE_CODE or y.dtype not in DTYPE_CODE:
+        raise ValueError("x and y must be float16, bfloat16 or float32 tensors")
+    if DTYPE_CODE[x.dtype] != shape.x_dtype or DTYPE_CODE[y.dtype] != shape.y_dtype:
+        raise ValueError("x / y dtypes do not match the shape's x_dtype / y_dtype")
+    if tuple(x.shape) != (shape.B, shape.K) or tuple(y.shape) != (shape.B, shape.N):
+        raise ValueError(f"x {tuple(x.shape)} / y {tuple(y.shape)} do not match the shape "
+                         f"(B={shape.B}, K={shape.K}, N={shape.N})")
+    if wdev.numel() < device_bytes(shape):
+        raise ValueError("weight stream is smaller than fb_device_bytes(shape)")
+
+
+def _mx_refuse(shape: FbShape) -> None:
+    check(lib().fb_validate(ctypes.byref(shape)))
+    raise ValueError("the native FP4 path takes E2M1 weights, bfloat16 x, no rotation and "
+                     "batch <= 16")
+
+
+def mx_workspace_bytes(shape: FbShape) -> int:
+    """Workspace of fb_gemv_mx (0: the shape is not one the native FP4 path takes)."""
+    return lib().fb_mx_workspace_bytes(ctypes.byref(shape))
+
+
+def gemv_mx(wdev: torch.Tensor, x: torch.Tensor, y: torch.Tensor, shape: FbShape,
+            workspace: torch.Tensor | None = None) -> torch.Tensor:
+    """E2M1 y[B,N] = x[B,K] . W^T on the matrix cores' native FP4 path: x (bf16) split
+    into two MX-E4M3 terms, then v_mfma_scale_f32_16x16x128_f8f6f4 on the stored codes
+    (asynchronous on the current stream)."""
+    _check_gemv_operands("fb_gemv_mx", wdev, x, y, shape)
+    need = mx_workspace_bytes(shape)
+    if not need:
+        _mx_refuse(shape)
+    if workspace is None or workspace.numel() < need:
+        workspace = torch.empty(need, dtype=torch.uint8, device=x.device)
+    elif workspace.device != x.device:
+        raise ValueError("workspace is on another device")
+    with torch.cuda.device(x.device):
+        check(lib().fb_gemv_mx(_ptr(wdev), _ptr(x), _ptr(y), ctypes.byref(shape),
+                               _ptr(workspace), workspace.numel(), _stream(x.device)))
+    return y
+
+
+def mx_split(x: torch.Tensor, shape: FbShape):
+    """The split fb_gemv_mx makes of x (bf16 [B, K] on the GPU): (codes uint8 [2, B, K],
+    scales uint8 [2, B, K/32]) -- term t of value (b, k) and of its 32-value block."""
+    if not x.is_cuda or x.dtype != torch.bfloat16 or not x.is_contiguous():
+        raise ValueError("x must be a contiguous bfloat16 device tensor")
+    if tuple(x.shape) != (shape.B, shape.K):
+        raise ValueError("x does not match the shape")
+    B, K = shape.B, shape.K
+    nbytes = lib().fb_mx_split_bytes(ctypes.byref(shape))
+    if not nbytes:
+        _mx_refuse(shape)
+    out = torch.empty(nbytes, dtype=torch.uint8, device=x.device)
+    with torch.cuda.device(x.device):
+        check(lib().fb_mx_split(_ptr(x), _ptr(out), ctypes.byref(shape), _stream(x.device)))
+    soff = (B * K * 2 + 255) // 256 * 256
+    terms = out[:B * K * 2].view(B, K // 128, 2, 128).permute(2, 0, 1, 3).reshape(2, B, K)
+    sc = out[soff:soff + B * (K // 128) * 8].view(B, K // 128, 2, 4).permute(2, 0, 1, 3)
+    return terms.contiguous(), sc.reshape(2, B, K // 32).contiguous()
 
 
 def dequant_device(wdev: torch.Tensor, shape: FbShape, out_dtype=torch.float32) -> torch.Tensor:

@@ -621,6 +621,169 @@ __device__ __forceinline__ f32x4 unit_partial(const Rec<FMT>& r, const uint8_t* 
 }
 
 // ---------------------------------------------------------------------------------
+// The native FP4 path (fb_gemv_mx): E2M1 weights times x split into two MX-E4M3 terms
+// ---------------------------------------------------------------------------------
+// v_mfma_scale_f32_16x16x128_f8f6f4 multiplies the E2M1 codes as they are stored, with their
+// E8M0 group scales, by an 8-bit B operand with E8M0 scales of its own per 32 K-values.  x
+// (bf16) is split once per call into x = t0 + t1: t0 rounds x and t1 rounds what t0 left,
+// each to E4M3 values times a power of two 2^e per 32-value block, e the smallest for which
+// the block's largest magnitude is at most 448 (E4M3's largest finite value), so no value
+// saturates.  A bf16 value has 8 significant bits and an E4M3 value 4, so the two terms hold
+// x exactly unless a block spans more than E4M3's exponent range (values 2^14 times or more
+// below the block's largest, which then lose low bits).
+//
+// Layout of the split, which the GEMV stages as it stages bf16 x (2 bytes per value): for
+// batch row b and 128-value group g, 256 bytes at (b K/128 + g) 256 -- the 128 E4M3 codes of
+// t0, then the 128 of t1, in K order; the scales from byte mx_scale_offset(B, K) on, 8 bytes
+// per (b, g) -- the E8M0 bytes of the group's four 32-value blocks for t0, then for t1.  In
+// LDS the scales sit in the 16-byte pad of each staged 128-value group.
+constexpr int kFmtMx = 2;  // internal format code: E2M1 stream, x as the MX split
+
+__host__ __device__ inline size_t mx_scale_offset(int B, int K) {
+  return ((size_t)B * K * 2 + 255) & ~size_t(255);
+}
+__host__ __device__ inline size_t mx_split_bytes(int B, int K) {
+  return mx_scale_offset(B, K) + (((size_t)B * (K / 128) * 8 + 255) & ~size_t(255));
+}
+
+// E8M0 exponent of a block: the smallest e with amax <= 448 2^e, within [-127, 127] (a block
+// of zeros: -127).
+__device__ __forceinline__ int mx_exponent(float amax) {
+  if (!(amax > 0.0f)) return -127;
+  const int ex = __builtin_amdgcn_frexp_expf(amax);  // amax = m 2^ex, m in [0.5, 1)
+  const float m = __builtin_amdgcn_frexp_mantf(amax);
+  const int e = ex - 9 + (m > 0.875f ? 1 : 0);        // 448 = 0.875 2^9
+  return e < -127 ? -127 : e > 127 ? 127 : e;
+}
+
+// E4M3 (OCP e4m3fn: bias 7, 3 fraction bits, subnormal step 2^-9) code of v, |v| <= 448,
+// rounded to nearest, ties to even; *q = the code's value.
+__device__ __forceinline__ unsigned e4m3_rne(float v, float* q) {
+  const unsigned u = __builtin_bit_cast(unsigned, v);
+  const unsigned sign = (u >> 24) & 0x80u;
+  const float a = __builtin_fabsf(v);
+  unsigned code;
+  float qa;
+  if (a < 0.015625f) {  // below 2^-6, the smallest normal: multiples of 2^-9
+    const float r = __builtin_rintf(a * 512.0f);  // 0..8 (8 is the smallest normal)
+    code = (unsigned)r;
+    qa = r * 0.001953125f;
+  } else {
+    unsigned au = u & 0x7FFFFFFFu;
+    au = (au + 0x7FFFFu + ((au >> 20) & 1u)) & ~0xFFFFFu;  // 3 fraction bits, ties to even
+    code = (((au >> 23) - 120u) << 3) | ((au >> 20) & 7u);
+    qa = __builtin_bit_cast(float, au);
+  }
+  *q = sign ? -qa : qa;
+  return sign | code;
+}
+
+// The split: one thread per 8 consecutive values, so 4 threads per 32-value block and 16 per
+// 128-value group (n8 = B K / 8 is a multiple of 16, and a group's threads are 16 aligned
+// lanes of one wave).
+__global__ __launch_bounds__(256) void mx_split_kernel(const uint16_t* __restrict__ x,
+                                                       uint8_t* __restrict__ out, int n8,
+                                                       size_t sc_off) {
+  const int i = blockIdx.x * 256 + threadIdx.x;
+  const int lane = threadIdx.x & 63;
+  const bool in = i < n8;
+  const u32x4 raw = in ? *reinterpret_cast<const u32x4*>(x + (size_t)i * 8) : u32x4{0u, 0u, 0u, 0u};
+  float v[8];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    v[2 * j] = __builtin_bit_cast(float, raw[j] << 16);
+    v[2 * j + 1] = __builtin_bit_cast(float, raw[j] & 0xFFFF0000u);
+  }
+  const size_t rec = (size_t)(i >> 4);  // (b K/128 + g): values 8i.. are b K + k
+#pragma unroll
+  for (int t = 0; t < 2; ++t) {
+    float amax = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) amax = fmaxf(amax, __builtin_fabsf(v[j]));
+    amax = fmaxf(amax, __shfl_xor(amax, 1));
+    amax = fmaxf(amax, __shfl_xor(amax, 2));
+    const int e = mx_exponent(amax);
+    unsigned w0 = 0, w1 = 0;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      float q;
+      const unsigned c = e4m3_rne(__builtin_ldexpf(v[j], -e), &q);
+      if (j < 4)
+        w0 |= c << (8 * j);
+      else
+        w1 |= c << (8 * (j - 4));
+      v[j] -= __builtin_ldexpf(q, e);  // exact: what the next term rounds
+    }
+    if (in) *reinterpret_cast<uint2*>(out + rec * 256 + t * 128 + (i & 15) * 8) = uint2{w0, w1};
+    // the group's four block scales, gathered in its first thread
+    const unsigned sb = (unsigned)(e + 127);
+    const unsigned s1 = __shfl(sb, lane + 4), s2 = __shfl(sb, lane + 8), s3 = __shfl(sb, lane + 12);
+    if (in && (i & 15) == 0)
+      *reinterpret_cast<unsigned*>(out + sc_off + rec * 8 + t * 4) = sb | s1 << 8 | s2 << 16 | s3 << 24;
+  }
+}
+
+typedef int i32x8 __attribute__((ext_vector_type(8)));
+template <int C>
+__device__ __forceinline__ f32x4 mfma_mx(const u32x4& a, const u32x4& b0, const u32x4& b1,
+                                         const f32x4& acc, unsigned sa, unsigned sb) {
+  const i32x8 av = {(int)a.x, (int)a.y, (int)a.z, (int)a.w, 0, 0, 0, 0};  // fp4: 4 dwords read
+  const i32x8 bv = {(int)b0.x, (int)b0.y, (int)b0.z, (int)b0.w,
+                    (int)b1.x, (int)b1.y, (int)b1.z, (int)b1.w};
+  // A: E2M1 (cbsz 4), B: E4M3 (blgp 0); byte C of each lane's scale word
+  return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(av, bv, acc, 4, 0, C, (int)sa, C,
+                                                          (int)sb);
+}
+
+// One unit on the FP4 MFMA, 8 MFMAs (4 chunks x 2 terms).  Lane L = n + 16 q gives chunk c
+// of its item q as A (32 codes; scale byte c of its record) -- K-block q of the MFMA.  The
+// MFMA pairs value 16 h + j (j < 16) of K-block g with B byte 16 (g >> 1) + j of B lane
+// group 2 (g & 1) + h, and takes block g's B scale from lane n + 16 g (found by one-hot
+// probes of the instruction on gfx950).  So B lane (n, q) holds values 16 (q & 1) .. +15 of
+// chunk c of items q >> 1 and 2 + (q >> 1), and the scale of its own item's block c.
+// xs: the span's first staged group of batch row n.
+// B operands of chunk C: terms 0 and 1, each 16 bytes from two groups.
+struct MxB {
+  u32x4 t0a, t0b, t1a, t1b;
+};
+template <int C>
+__device__ __forceinline__ void mx_read(const uint8_t* d, MxB& b) {
+  b.t0a = *reinterpret_cast<const u32x4*>(d + C * 32);
+  b.t0b = *reinterpret_cast<const u32x4*>(d + 2 * kSliceBytes + C * 32);
+  b.t1a = *reinterpret_cast<const u32x4*>(d + 128 + C * 32);
+  b.t1b = *reinterpret_cast<const u32x4*>(d + 2 * kSliceBytes + 128 + C * 32);
+}
+// Chunk C's two MFMAs, with chunk C + 1's reads issued first (two buffers of 16 registers
+// instead of all 64 up front, which left the sliced kernels spilling).
+template <int C>
+__device__ __forceinline__ void mx_step(const Rec<kFmtMx>& r, const uint8_t* d, uint2 sx,
+                                        MxB (&b)[2], f32x4& acc0, f32x4& acc1) {
+  if constexpr (C < 3) mx_read<C + 1>(d, b[(C + 1) & 1]);
+  acc0 = mfma_mx<C>(r.nib[C], b[C & 1].t0a, b[C & 1].t0b, acc0, r.t0.x, sx.x);
+  acc1 = mfma_mx<C>(r.nib[C], b[C & 1].t1a, b[C & 1].t1b, acc1, r.t0.x, sx.y);
+  // keeps the MFMAs here: otherwise they sink into the slot write's per-lane branch, after
+  // every read of the unit
+  asm volatile("" : "+v"(acc0), "+v"(acc1));
+  __builtin_amdgcn_sched_barrier(0);
+}
+__device__ __forceinline__ f32x4 unit_partial_mx(const Rec<kFmtMx>& r, const uint8_t* xs, int q) {
+  const uint8_t* d = xs + (q >> 1) * kSliceBytes + (q & 1) * 16;
+  const uint2 sx = *reinterpret_cast<const uint2*>(xs + q * kSliceBytes + 256);
+  f32x4 acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
+  MxB b[2];
+  mx_read<0>(d, b[0]);
+  __builtin_amdgcn_sched_barrier(0);
+  mx_step<0>(r, d, sx, b, acc0, acc1);
+  mx_step<1>(r, d, sx, b, acc0, acc1);
+  mx_step<2>(r, d, sx, b, acc0, acc1);
+  mx_step<3>(r, d, sx, b, acc0, acc1);
+  return acc0 + acc1;
+}
+// LDS of the zero block that MFMA columns past the batch read: the MX unit reads up to
+// 3 groups + 256 + 8 bytes past its span base.
+constexpr int zero_bytes(int fmt) { return fmt == kFmtMx ? 1088 : 256; }
+
+// ---------------------------------------------------------------------------------
 // The GEMV kernel
 // ---------------------------------------------------------------------------------
 // The first 15 argument dwords arrive preloaded in SGPRs and hold everything but the
@@ -643,7 +806,7 @@ template <int FMT, int XDT, int MODE, int NW, int XP>
 __global__ __launch_bounds__(NW * 64) void gemv_kernel(
     const uint8_t* __restrict__ w, const void* __restrict__ x, int K, int Bin, int SPL, int GS,
     int tq, int tr, unsigned spl_m, int S, int fwht_block, int RS, float fwht_scale,
-    void* __restrict__ y, int N, int ydt PH_KPARAM) {
+    void* __restrict__ y, int N, int ydt, const uint8_t* __restrict__ xsc PH_KPARAM) {
   extern __shared__ __align__(16) uint8_t lds[];
   PH_DECL
   PH_MARK(kPhStart);
@@ -681,7 +844,7 @@ __global__ __launch_bounds__(NW * 64) void gemv_kernel(
   // per-tile unit counts
   int* counter = reinterpret_cast<int*>(lds);
   uint8_t* zeros = lds + 16;
-  uint8_t* xst = lds + 16 + 256;
+  uint8_t* xst = lds + 16 + zero_bytes(FMT);
   f32x4* slots = reinterpret_cast<f32x4*>(xst + xbytes);
 
 
@@ -691,7 +854,8 @@ __global__ __launch_bounds__(NW * 64) void gemv_kernel(
   const int q = lane >> 4;    // K-quarter of the span / output row group
   // MFMA columns >= B multiply zeros (read from one 256-byte block whatever the span):
   // their results are not used, and zeros keep the matrix core from switching.
-  const uint8_t* xl = col < B ? xst + col * RS + q * kSliceBytes : zeros;
+  constexpr bool mx = FMT == kFmtMx;  // the native FP4 path reads 3 groups from the span base
+  const uint8_t* xl = col < B ? xst + col * RS + (mx ? 0 : q * kSliceBytes) : zeros;
   const int xspan = col < B ? 4 * kSliceBytes : 0;  // x bytes per span for this lane
 
   // After two fixed units per wave, the waves take units from the workgroup's LDS counter, so a wave that the SIMD's
@@ -735,7 +899,11 @@ __global__ __launch_bounds__(NW * 64) void gemv_kernel(
   auto process = [&](const Rec<FMT>& r, int s, int u) {
     const int lt = tile_of(u);
     const int span = u - lt * sp;
-    const f32x4 acc = unit_partial<FMT, XDT>(r, xl + span * xspan);
+    f32x4 acc;
+    if constexpr (mx)
+      acc = unit_partial_mx(r, xl + span * xspan, q);
+    else
+      acc = unit_partial<FMT, XDT>(r, xl + span * xspan);
     if (col < B) {
       f32x4* sl = slots + ((size_t)(lt * SPL + span) * 4 + q) * B + col;
       if (s == s_begin)
@@ -817,13 +985,28 @@ __global__ __launch_bounds__(NW * 64) void gemv_kernel(
     if (s == s_begin) {
       if (tile_reduce && (int)threadIdx.x < t1 - t0) tile_cnt[threadIdx.x] = 0;
       if (threadIdx.x == 0) *counter = 2 * NW;
-      if (threadIdx.x < 16) reinterpret_cast<u32x4*>(zeros)[threadIdx.x] = u32x4{0u, 0u, 0u, 0u};
+      if (threadIdx.x < zero_bytes(FMT) / 16)
+        reinterpret_cast<u32x4*>(zeros)[threadIdx.x] = u32x4{0u, 0u, 0u, 0u};
     }
     if constexpr (rot)
       stage_fwht<NW>(xst, reinterpret_cast<float*>(xst + B * RS), xr, xrs, K, B, k0, kw, nsl, RS,
                  fwht_block, fwht_scale, tid PH_ARG);
     else
       stage_plain<NT, XP, flat1>(xst, xp, xrs, K, B, k0, nsl, RS, row_of_wave, wv, tid);
+    if constexpr (mx) {
+      // the split's block scales into the pad of each staged group (zeros past K)
+      const int G = K / 128;
+      const rsrc_t srs = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(xsc), (short)0,
+                                                           B * G * 8, kRsrcWord3);
+      for (int i = tid; i < B * nsl; i += NT) {
+        const int b = fdiv(i >> 2, SPL, spl_m);  // i / nsl, nsl = 4 SPL
+        const int it = i - b * nsl;
+        const int gi = k0 / 128 + it;
+        const unsigned off = gi < G ? (unsigned)(b * G + gi) * 8u : kXOutOfRange;
+        const uint2 sc = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(srs, off, 0, 0));
+        *reinterpret_cast<uint2*>(xst + b * RS + it * kSliceBytes + 256) = sc;
+      }
+    }
     __syncthreads();  // x staged, counter set
     PH_MARK(s == 0 ? kPhStaged : s == 1 ? kPhStaged1 : kPhStaged2);
     issue(s, u1, ring[1]);
@@ -1031,7 +1214,7 @@ unsigned div_magic(int d) { return d == 1 ? 0xFFFFFFFFu : (unsigned)((1ull << 32
 size_t plan_lds(const fb_shape_t* s, int tpw, int SPL) {
   // batch 1 adds the per-tile unit counts of the tile-by-tile reduction
   return (size_t)x_lds_bytes(s->B, s->K, SPL, s->fwht_block) + (size_t)tpw * SPL * 64 * s->B +
-         (s->B == 1 ? (size_t)((tpw * 4 + 15) & ~15) : 0) + 16 + 256;
+         (s->B == 1 ? (size_t)((tpw * 4 + 15) & ~15) : 0) + 16 + zero_bytes(s->fmt);
 }
 
 // The fewest K-slices whose LDS fits.  One 16-wave workgroup per CU (up to the number of
@@ -1127,7 +1310,7 @@ int device_cus() {
 
 template <int FMT, int XDT, int MODE, int NW, int XP>
 int launch_gemv(const void* wdev, const void* x, void* y, const fb_shape_t* s, const Plan& pl,
-                hipStream_t stream) {
+                hipStream_t stream, const void* xsc) {
   auto kern = gemv_kernel<FMT, XDT, MODE, NW, XP>;
   // the LDS limit is a per-device attribute of the kernel: set once on each device
   static std::atomic<uint64_t> attr_set{0};
@@ -1143,51 +1326,57 @@ int launch_gemv(const void* wdev, const void* x, void* y, const fb_shape_t* s, c
   hipLaunchKernelGGL(kern, dim3(pl.grid, pl.P ? pl.P : 1), dim3(NW * 64), pl.lds, stream,
                      static_cast<const uint8_t*>(wdev), x, s->K, s->B, pl.SPL, pl.GS, pl.tq,
                      pl.tr, div_magic(pl.SPL), pl.S, s->fwht_block, x_row_stride(pl.SPL * 4),
-                     fwht_scale(s->fwht_block), y,
-                     s->N, s->y_dtype PH_KARG((size_t)pl.grid * NW * 64));
+                     fwht_scale(s->fwht_block), y, s->N, s->y_dtype,
+                     static_cast<const uint8_t*>(xsc) PH_KARG((size_t)pl.grid * NW * 64));
   return hipGetLastError() == hipSuccess ? FB_OK : FB_ERR_HIP;
 }
 
 template <int FMT, int XDT>
 int launch_mode(int mode, const void* wdev, const void* x, void* y, const fb_shape_t* s,
-                const Plan& pl, hipStream_t stream) {
+                const Plan& pl, hipStream_t stream, const void* xsc) {
   const bool deep = pl.xp == 8;
   if (mode == kSplitK)
-    return deep ? launch_gemv<FMT, XDT, kSplitK, kWaves, 8>(wdev, x, y, s, pl, stream)
-                : launch_gemv<FMT, XDT, kSplitK, kWaves, 4>(wdev, x, y, s, pl, stream);
+    return deep ? launch_gemv<FMT, XDT, kSplitK, kWaves, 8>(wdev, x, y, s, pl, stream, xsc)
+                : launch_gemv<FMT, XDT, kSplitK, kWaves, 4>(wdev, x, y, s, pl, stream, xsc);
   if (mode == kFlat1) {
     if (pl.nw == kWaves / 2)
-      return deep ? launch_gemv<FMT, XDT, kFlat1, kWaves / 2, 8>(wdev, x, y, s, pl, stream)
-                  : launch_gemv<FMT, XDT, kFlat1, kWaves / 2, 4>(wdev, x, y, s, pl, stream);
-    return deep ? launch_gemv<FMT, XDT, kFlat1, kWaves, 8>(wdev, x, y, s, pl, stream)
-                : launch_gemv<FMT, XDT, kFlat1, kWaves, 4>(wdev, x, y, s, pl, stream);
+      return deep ? launch_gemv<FMT, XDT, kFlat1, kWaves / 2, 8>(wdev, x, y, s, pl, stream, xsc)
+                  : launch_gemv<FMT, XDT, kFlat1, kWaves / 2, 4>(wdev, x, y, s, pl, stream, xsc);
+    return deep ? launch_gemv<FMT, XDT, kFlat1, kWaves, 8>(wdev, x, y, s, pl, stream, xsc)
+                : launch_gemv<FMT, XDT, kFlat1, kWaves, 4>(wdev, x, y, s, pl, stream, xsc);
   }
   if (mode == kFlat) {
     if (pl.nw == kWaves / 2)
-      return deep ? launch_gemv<FMT, XDT, kFlat, kWaves / 2, 8>(wdev, x, y, s, pl, stream)
-                  : launch_gemv<FMT, XDT, kFlat, kWaves / 2, 4>(wdev, x, y, s, pl, stream);
-    return deep ? launch_gemv<FMT, XDT, kFlat, kWaves, 8>(wdev, x, y, s, pl, stream)
-                : launch_gemv<FMT, XDT, kFlat, kWaves, 4>(wdev, x, y, s, pl, stream);
+      return deep ? launch_gemv<FMT, XDT, kFlat, kWaves / 2, 8>(wdev, x, y, s, pl, stream, xsc)
+                  : launch_gemv<FMT, XDT, kFlat, kWaves / 2, 4>(wdev, x, y, s, pl, stream, xsc);
+    return deep ? launch_gemv<FMT, XDT, kFlat, kWaves, 8>(wdev, x, y, s, pl, stream, xsc)
+                : launch_gemv<FMT, XDT, kFlat, kWaves, 4>(wdev, x, y, s, pl, stream, xsc);
   }
   if (mode == kSliced)
-    return deep ? launch_gemv<FMT, XDT, kSliced, kWaves, 8>(wdev, x, y, s, pl, stream)
-                : launch_gemv<FMT, XDT, kSliced, kWaves, 4>(wdev, x, y, s, pl, stream);
-  // the rotation preloads kXPre 256-value sub-blocks per wave instead
-  if (mode == kRot1) return launch_gemv<FMT, XDT, kRot1, kWaves, 4>(wdev, x, y, s, pl, stream);
-  return launch_gemv<FMT, XDT, kRotated, kWaves, 4>(wdev, x, y, s, pl, stream);
+    return deep ? launch_gemv<FMT, XDT, kSliced, kWaves, 8>(wdev, x, y, s, pl, stream, xsc)
+                : launch_gemv<FMT, XDT, kSliced, kWaves, 4>(wdev, x, y, s, pl, stream, xsc);
+  if constexpr (FMT == kFmtMx) {
+    return FB_ERR_FWHT;  // the split is of unrotated x
+  } else {
+    // the rotation preloads kXPre 256-value sub-blocks per wave instead
+    if (mode == kRot1) return launch_gemv<FMT, XDT, kRot1, kWaves, 4>(wdev, x, y, s, pl, stream, xsc);
+    return launch_gemv<FMT, XDT, kRotated, kWaves, 4>(wdev, x, y, s, pl, stream, xsc);
+  }
 }
 
 int launch_plan(const void* wdev, const void* x, void* y, const fb_shape_t* s, const Plan& pl,
-                hipStream_t hs) {
+                hipStream_t hs, const void* xsc = nullptr) {
   const int mode = s->fwht_block ? (s->B == 1 && pl.S == 1 ? kRot1 : kRotated)
                    : pl.P         ? kSplitK
                    : pl.S > 1     ? kSliced
                    : s->B == 1    ? kFlat1
                                   : kFlat;
-  if (s->fmt == FB_FMT_GF4) return launch_mode<FB_FMT_GF4, FB_DT_F16>(mode, wdev, x, y, s, pl, hs);
+  if (s->fmt == FB_FMT_GF4)
+    return launch_mode<FB_FMT_GF4, FB_DT_F16>(mode, wdev, x, y, s, pl, hs, xsc);
+  if (s->fmt == kFmtMx) return launch_mode<kFmtMx, FB_DT_BF16>(mode, wdev, x, y, s, pl, hs, xsc);
   if (s->x_dtype == FB_DT_BF16)
-    return launch_mode<FB_FMT_E2M1, FB_DT_BF16>(mode, wdev, x, y, s, pl, hs);
-  return launch_mode<FB_FMT_E2M1, FB_DT_F16>(mode, wdev, x, y, s, pl, hs);
+    return launch_mode<FB_FMT_E2M1, FB_DT_BF16>(mode, wdev, x, y, s, pl, hs, xsc);
+  return launch_mode<FB_FMT_E2M1, FB_DT_F16>(mode, wdev, x, y, s, pl, hs, xsc);
 }
 
 // Rotated calls with at least this many activation values (B * K) rotate x once
@@ -1214,20 +1403,20 @@ int launch_rotate(const void* x, void* xo, const fb_shape_t* s, hipStream_t hs) 
 
 // The GEMV of a validated shape: one launch when a plan fits LDS, else row chunks.
 int gemv_planned(const void* wdev, const void* x, void* y, const fb_shape_t* s, int cus,
-                 hipStream_t hs, void* ws, size_t ws_bytes) {
+                 hipStream_t hs, void* ws, size_t ws_bytes, const uint8_t* xsc = nullptr) {
   Plan pl;
   // batch 8-16 on layers of few row tiles: the K-parts side by side, through the workspace
   if (ws && splitk_parts(s, cus, &pl) && ws_bytes >= splitk_bytes(s, pl.P)) {
     fb_shape_t sp = *s;
     sp.y_dtype = FB_DT_F32;  // the parts' sums
-    const int st = launch_plan(wdev, x, ws, &sp, pl, hs);
+    const int st = launch_plan(wdev, x, ws, &sp, pl, hs, xsc);
     if (st != FB_OK) return st;
     const int64_t n = (int64_t)s->B * s->N;
     hipLaunchKernelGGL(splitk_sum, dim3((unsigned)((n + 1023) / 1024)), dim3(256), 0, hs,
                        static_cast<const float*>(ws), pl.P, n, y, s->y_dtype);
     return hipGetLastError() == hipSuccess ? FB_OK : FB_ERR_HIP;
   }
-  if (make_plan(s, cus, pl)) return launch_plan(wdev, x, y, s, pl, hs);
+  if (make_plan(s, cus, pl)) return launch_plan(wdev, x, y, s, pl, hs, xsc);
   // No plan holds the whole batch in LDS (a 4096-wide rotation keeps an fp32 copy of every
   // batch row): the rows run in the largest chunks that fit, each streaming the weights.
   fb_shape_t sc = *s;
@@ -1242,7 +1431,8 @@ int gemv_planned(const void* wdev, const void* x, void* y, const fb_shape_t* s, 
     sc.B = std::min(bc, s->B - b0);
     if (!make_plan(&sc, cus, pl)) return FB_ERR_LDS;
     const int st = launch_plan(wdev, static_cast<const uint8_t*>(x) + (size_t)b0 * s->K * 2,
-                               static_cast<uint8_t*>(y) + (size_t)b0 * s->N * ysize, &sc, pl, hs);
+                               static_cast<uint8_t*>(y) + (size_t)b0 * s->N * ysize, &sc, pl, hs,
+                               xsc ? xsc + (size_t)b0 * (s->K / 128) * 8 : nullptr);
     if (st != FB_OK) return st;
   }
   return FB_OK;
@@ -1282,6 +1472,54 @@ int gemv_impl(const void* wdev, const void* x, void* y, const fb_shape_t* s, voi
                         ws_bytes - need);
   }
   return gemv_planned(wdev, x, y, s, cus, hs, ws, ws_bytes);
+}
+
+// Checks of the native FP4 path's shape: E2M1 weights, bf16 x (8 significant bits, which the
+// two E4M3 terms hold), no rotation.
+int mx_check(const fb_shape_t* s) {
+  const int st = fb_validate(s);
+  if (st != FB_OK) return st;
+  if (s->fmt != FB_FMT_E2M1) return FB_ERR_FORMAT;
+  if (s->x_dtype != FB_DT_BF16) return FB_ERR_DTYPE;
+  if (s->fwht_block) return FB_ERR_FWHT;
+  if (s->B > 16) return FB_ERR_BATCH;
+  return FB_OK;
+}
+
+int launch_mx_split(const void* x, void* out, const fb_shape_t* s, hipStream_t hs) {
+  const int n8 = s->B * (s->K / 8);  // B K < 2^31 (fb_validate)
+  hipLaunchKernelGGL(mx_split_kernel, dim3((n8 + 255) / 256), dim3(256), 0, hs,
+                     static_cast<const uint16_t*>(x), static_cast<uint8_t*>(out), n8,
+                     mx_scale_offset(s->B, s->K));
+  return hipGetLastError() == hipSuccess ? FB_OK : FB_ERR_HIP;
+}
+
+// fb_gemv_mx behind the ABI: the split into the workspace's head, then the GEMV on it (with
+// the split-K parts' sums after the split where the plan runs them side by side).
+int gemv_mx_impl(const void* wdev, const void* x, void* y, const fb_shape_t* s, void* ws,
+                 size_t ws_bytes, hipStream_t hs) {
+  if (!s || !wdev || !x || !y || !ws) return FB_ERR_NULL;
+  int st = mx_check(s);
+  if (st != FB_OK) return st;
+  if (!aligned16(wdev) || !aligned16(x) || (reinterpret_cast<uintptr_t>(y) & 3u) ||
+      (reinterpret_cast<uintptr_t>(ws) & 255u))
+    return FB_ERR_ALIGN;
+  const int cus = device_cus();
+  {
+    // 32-bit offsets from each workgroup's first block (as in gemv_impl)
+    const int64_t T = (s->N + 15) / 16, GS = (s->K / 128 + 3) / 4;
+    const int64_t grid = std::min<int64_t>(T, cus);
+    if ((T + grid - 1) / grid * GS * fb::kE2m1BlockBytes > INT32_MAX) return FB_ERR_SHAPE;
+  }
+  const size_t need = mx_split_bytes(s->B, s->K);
+  if (ws_bytes < need) return FB_ERR_WORKSPACE;
+  st = launch_mx_split(x, ws, s, hs);
+  if (st != FB_OK) return st;
+  fb_shape_t u = *s;
+  u.fmt = kFmtMx;
+  uint8_t* w8 = static_cast<uint8_t*>(ws);
+  return gemv_planned(wdev, w8, y, &u, cus, hs, w8 + need, ws_bytes - need,
+                      w8 + mx_scale_offset(s->B, s->K));
 }
 
 // Scratch of the allocation-free entry point: a file-scope device array (one per GPU the
@@ -1356,6 +1594,31 @@ int fb_dequant(const void* wdev, void* w_out, int32_t out_dtype, const fb_shape_
     hipLaunchKernelGGL(dequant_kernel<FB_FMT_E2M1>, dim3(grid), dim3(256), 0, hs,
                        static_cast<const uint8_t*>(wdev), w_out, s->N, s->K, out_dtype);
   return hipGetLastError() == hipSuccess ? FB_OK : FB_ERR_HIP;
+}
+
+size_t fb_mx_split_bytes(const fb_shape_t* s) {
+  if (!s || mx_check(s) != FB_OK) return 0;
+  return mx_split_bytes(s->B, s->K);
+}
+
+int fb_mx_split(const void* x, void* out, const fb_shape_t* s, void* stream) {
+  if (!s || !x || !out) return FB_ERR_NULL;
+  const int st = mx_check(s);
+  if (st != FB_OK) return st;
+  if (!aligned16(x) || (reinterpret_cast<uintptr_t>(out) & 255u)) return FB_ERR_ALIGN;
+  return launch_mx_split(x, out, s, static_cast<hipStream_t>(stream));
+}
+
+size_t fb_mx_workspace_bytes(const fb_shape_t* s) {
+  if (!s || mx_check(s) != FB_OK) return 0;
+  fb_shape_t u = *s;
+  u.fmt = kFmtMx;
+  return mx_split_bytes(s->B, s->K) + splitk_bytes(&u, splitk_parts(&u, device_cus(), nullptr));
+}
+
+int fb_gemv_mx(const void* wdev, const void* x, void* y, const fb_shape_t* s, void* ws,
+               size_t ws_bytes, void* stream) {
+  return gemv_mx_impl(wdev, x, y, s, ws, ws_bytes, static_cast<hipStream_t>(stream));
 }
 
 #ifdef FB_PHASE_TRACE

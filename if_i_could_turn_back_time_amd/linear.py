@@ -79,19 +79,23 @@ def _fwht_last_dim(t: torch.Tensor, block: int) -> torch.Tensor:
     return (v.reshape(*lead, K) / float(block) ** 0.5)
 
 
-def _gemv_chunks(wdev, N, kp, fmt, fwht_block, xk, y):
+def _gemv_chunks(wdev, N, kp, fmt, fwht_block, xk, y, fp4_mfma=False):
     f = C.FMT_BY_NAME[fmt]
     for b0 in range(0, xk.shape[0], MAX_GEMV_BATCH):
         b1 = min(b0 + MAX_GEMV_BATCH, xk.shape[0])
         shape = C.make_shape(N, kp, b1 - b0, f, fwht_block, C.DTYPE_CODE[xk.dtype],
                              C.DTYPE_CODE[y.dtype])
-        C.gemv(wdev, xk[b0:b1], y[b0:b1], shape, C.new_workspace(shape, xk.device))
+        if fp4_mfma:
+            C.gemv_mx(wdev, xk[b0:b1], y[b0:b1], shape)
+        else:
+            C.gemv(wdev, xk[b0:b1], y[b0:b1], shape, C.new_workspace(shape, xk.device))
 
 
 def _kernel_input(x2: torch.Tensor, K: int, fmt: str, fwht_block: int, range_check: bool,
-                  f16_exact: bool) -> torch.Tensor:
+                  f16_exact: bool, fp4_mfma: bool = False) -> torch.Tensor:
     """x [M, K] -> the kernel's activation: fp16 for GF4 and every rotation (E2M1 keeps
-    fp16 / bf16, fp32 becomes bf16), zero-padded to ``packed_k(K)``.  ``range_check``
+    fp16 / bf16, fp32 becomes bf16; on the native FP4 path every dtype becomes bf16),
+    zero-padded to ``packed_k(K)``.  ``range_check``
     raises where the fp16 staging would overflow: values beyond +-65504 in a wider x, and
     for a rotation any block of L2 norm >= 65504 (a rotated value is at most its block's
     norm).  It costs one reduction and a host sync per call."""
@@ -107,6 +111,8 @@ def _kernel_input(x2: torch.Tensor, K: int, fmt: str, fwht_block: int, range_che
                 if bool(norm >= FP16_MAX):
                     raise ValueError("packed linear: a rotation block of x has L2 norm >= 65504, "
                                      "so its rotated values may overflow fp16")
+    elif fp4_mfma:
+        xk = x2.to(torch.bfloat16)
     else:
         xk = x2 if x2.dtype in (torch.float16, torch.bfloat16) else x2.to(torch.bfloat16)
     if fmt == "e2m1" and xk.dtype == torch.float16 and not f16_exact:
@@ -126,11 +132,11 @@ class _PackedLinearFn(torch.autograd.Function):
     rotated weight W' = W H, rotated back: ``grad_x = (grad_y W') H``."""
 
     @staticmethod
-    def forward(ctx, x2, wdev, N, K, fmt, fwht_block, range_check, f16_exact):
-        xk = _kernel_input(x2, K, fmt, fwht_block, range_check, f16_exact)
+    def forward(ctx, x2, wdev, N, K, fmt, fwht_block, range_check, f16_exact, fp4_mfma=False):
+        xk = _kernel_input(x2, K, fmt, fwht_block, range_check, f16_exact, fp4_mfma)
         ydt = x2.dtype if x2.dtype in C.DTYPE_CODE else torch.float32
         y = torch.empty(x2.shape[0], N, dtype=ydt, device=x2.device)
-        _gemv_chunks(wdev, N, packed_k(K), fmt, fwht_block, xk, y)
+        _gemv_chunks(wdev, N, packed_k(K), fmt, fwht_block, xk, y, fp4_mfma)
         ctx.save_for_backward(wdev)
         ctx.cfg = (N, K, fmt, fwht_block, x2.dtype)
         return y
@@ -144,12 +150,13 @@ class _PackedLinearFn(torch.autograd.Function):
         gx = gy.float() @ W
         if fwht_block:
             gx = _fwht_last_dim(gx, fwht_block)
-        return gx[:, :K].to(xdt), None, None, None, None, None, None, None
+        return gx[:, :K].to(xdt), None, None, None, None, None, None, None, None
 
 
 def packed_linear(wdev: torch.Tensor, N: int, K: int, fmt: str, fwht_block: int,
                   x: torch.Tensor, bias: torch.Tensor | None = None, *,
-                  range_check: bool = True, f16_exact: bool = True) -> torch.Tensor:
+                  range_check: bool = True, f16_exact: bool = True,
+                  fp4_mfma: bool = False) -> torch.Tensor:
     """``F.linear(x, W, bias)`` for a packed 4-bit ``W [N, K]`` (device stream ``wdev``
     of a ``packed_k(K)``-wide weight), through fb_gemv in chunks of 16 rows of x.
 
@@ -158,24 +165,30 @@ def packed_linear(wdev: torch.Tensor, N: int, K: int, fmt: str, fwht_block: int,
     has x's dtype (fp32 for other dtypes).  Differentiable in x (and bias): the weight is
     frozen, as the reference's committed weight is.  ``range_check`` (see
     ``_kernel_input``) raises instead of letting fp16 staging overflow; ``f16_exact``
-    (E2M1 only) says whether the weight's scales decode exactly to fp16.  No CPU path: x
-    must be on the GPU."""
+    (E2M1 only) says whether the weight's scales decode exactly to fp16.  ``fp4_mfma``
+    (unrotated E2M1 only) runs the matrix cores' native FP4 path (fb_gemv_mx): x as bf16,
+    split into two MX-E4M3 terms, which hold a bf16 value exactly unless its 32-value block
+    spans more than E4M3's exponent range (fp16 and fp32 x are rounded to bf16 first).  No
+    CPU path: x must be on the GPU."""
     if x.dim() == 0 or x.shape[-1] != K:
         raise RuntimeError(f"packed linear: input of shape {tuple(x.shape)} does not end in "
                            f"in_features={K}")
     if not x.is_cuda:
         raise RuntimeError("the packed 4-bit linear runs the HIP kernel: move the module and "
                            "input to a ROCm GPU")
+    if fp4_mfma and (fmt != "e2m1" or fwht_block):
+        raise ValueError("the native FP4 path (fp4_mfma) takes unrotated E2M1 weights")
     lead = x.shape[:-1]
     x2 = x.reshape(-1, K)
     if torch.is_grad_enabled() and x.requires_grad:
-        y = _PackedLinearFn.apply(x2, wdev, N, K, fmt, fwht_block, range_check, f16_exact)
+        y = _PackedLinearFn.apply(x2, wdev, N, K, fmt, fwht_block, range_check, f16_exact,
+                                  fp4_mfma)
         if bias is not None:
             y = y + bias.to(y.dtype)
         return y.reshape(*lead, N)
     with torch.no_grad():
         y = _PackedLinearFn.forward(_NoCtx(), x2, wdev, N, K, fmt, fwht_block, range_check,
-                                    f16_exact)
+                                    f16_exact, fp4_mfma)
     if bias is not None:
         if torch.is_grad_enabled() and bias.requires_grad:
             y = y + bias.to(y.dtype)
@@ -277,6 +290,22 @@ class PackedWeight:
         shape = self.shape(B, x.dtype, ydt)
         return C.gemv(self.wdev, x, out, shape, self.workspace(shape, x.device))
 
+    def gemv_mx(self, x: torch.Tensor, out: torch.Tensor | None = None,
+                out_dtype: torch.dtype | None = None) -> torch.Tensor:
+        """x [B,K] (bf16, B <= 16) on the GPU -> y [B,N] on the native FP4 path
+        (fb_gemv_mx; unrotated E2M1 only)."""
+        B = x.shape[0]
+        ydt = out.dtype if out is not None else (out_dtype or x.dtype)
+        if out is None:
+            out = torch.empty(B, self.N, dtype=ydt, device=x.device)
+        shape = self.shape(B, x.dtype, ydt)
+        need = C.mx_workspace_bytes(shape)
+        key = ("mx", str(x.device), need)
+        ws = self._ws.get(key)
+        if ws is None and need:
+            ws = self._ws[key] = torch.empty(need, dtype=torch.uint8, device=x.device)
+        return C.gemv_mx(self.wdev, x, out, shape, ws)
+
     def dequant_device(self, out_dtype=torch.float32) -> torch.Tensor:
         return C.dequant_device(self.wdev, C.make_shape(self.N, self.K, 1, self.fmt), out_dtype)
 
@@ -298,7 +327,7 @@ class QuantLinear(nn.Linear):
 
     def __init__(self, linear_module: nn.Linear, bitwidth: int = 4, mask=None, *,
                  fmt: str = "gf4", hadamard=False, nthreads: int | None = None,
-                 pack: bool = True, packer: str = "host"):
+                 pack: bool = True, packer: str = "host", fp4_mfma: bool = False):
         super().__init__(linear_module.in_features, linear_module.out_features,
                          bias=(linear_module.bias is not None))
         if bitwidth != 4:
@@ -325,6 +354,10 @@ class QuantLinear(nn.Linear):
              self.fwht_block], dtype=torch.int32))
         self.register_buffer("wdev", torch.empty(0, dtype=torch.uint8), persistent=False)
         self.hard_quant = False
+        # unrotated E2M1 only: the matrix cores' native FP4 path (x as two MX-E4M3 terms)
+        if fp4_mfma and (fmt != "e2m1" or self.fwht_block):
+            raise ValueError("fp4_mfma needs fmt='e2m1' without a rotation")
+        self.fp4_mfma = fp4_mfma
         # raise instead of letting fp16 activation staging overflow (one host sync per
         # call for bf16 / fp32 inputs and for rotated layers); set False to skip
         self.range_check = True
@@ -477,7 +510,8 @@ class QuantLinear(nn.Linear):
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         return packed_linear(self.wdev, self.out_features, self.in_features, self.fmt,
                              self.fwht_block, x, self.bias, range_check=self.range_check,
-                             f16_exact=self._f16_exact)
+                             f16_exact=self._f16_exact,
+                             fp4_mfma=self.fp4_mfma)
 
     def extra_repr(self) -> str:
         return (f"in_features={self.in_features}, out_features={self.out_features}, "

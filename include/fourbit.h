@@ -180,6 +180,43 @@ int fb_gemv(const void* wdev, const void* x, void* y, const fb_shape_t* s, void*
 int fb_gemv_noalloc(const void* wdev, const void* x, void* y, const fb_shape_t* s,
                     void* stream);
 
+/* The E2M1 GEMV on the matrix cores' native FP4 path, an opt-in alternative to fb_gemv for
+ * unrotated E2M1 weights with BF16 x, batch 1..16 (others: FB_ERR_FORMAT / FB_ERR_DTYPE /
+ * FB_ERR_FWHT / FB_ERR_BATCH).  Same operands and result layout as fb_gemv and the same
+ * reference interface (QuantLinear.forward's dequantize + F.linear, layers.py:33-38, and
+ * linear_kernel_batch, layers.h:9828-9839); the reference has no FP4 mode of its own.
+ * x is split once per call (one small kernel, into ws) into two MX-E4M3 terms, each E4M3
+ * values times a power of two per 32-value block; v_mfma_scale_f32_16x16x128_f8f6f4 then
+ * multiplies the stored E2M1 codes and E8M0 scales by both terms, with no decode.  The two
+ * terms hold a bf16 value exactly unless its 32-value block spans more than E4M3's exponent
+ * range (values 2^14 or more below the block's largest lose low bits), so y differs from
+ * fb_gemv's by the accumulation order, plus that loss where it occurs.  E8M0 byte 0 is
+ * 2^-127 here (fb_dequant_host's value; fb_gemv decodes it to 0).
+ * ws: device workspace, 256-byte aligned, of at least fb_mx_workspace_bytes(s) bytes
+ * (required: FB_ERR_NULL / FB_ERR_ALIGN / FB_ERR_WORKSPACE otherwise): the split, then the
+ * split-K parts' sums where the plan runs them side by side.  Calls that share a workspace
+ * must not overlap. */
+int fb_gemv_mx(const void* wdev, const void* x, void* y, const fb_shape_t* s, void* ws,
+               size_t ws_bytes, void* stream);
+
+/* Workspace bytes of fb_gemv_mx for this shape on the current device (0 for shapes it
+ * does not take). */
+size_t fb_mx_workspace_bytes(const fb_shape_t* s);
+
+/* The split fb_gemv_mx makes of x (BF16 [B,K] on the device), into out (device, 256-byte
+ * aligned, fb_mx_split_bytes(s) bytes), asynchronous on the stream.  Layout: for batch row
+ * b and 128-value group g, 256 bytes at (b*K/128 + g)*256 -- the 128 E4M3 codes (OCP
+ * e4m3fn) of term 0, then the 128 of term 1, in K order; from byte offset B*K*2 rounded up
+ * to 256, 8 bytes per (b, g) -- the E8M0 scales of the group's four 32-value blocks for
+ * term 0, then for term 1.  Term t rounds (nearest, ties to even) what the earlier terms
+ * left of x, in units of its block's scale 2^e, e the smallest with the block's largest
+ * magnitude <= 448 * 2^e (clamped to [-127, 127]; 0 for a block of zeros).  For callers
+ * that reuse one split across layers that share their input. */
+int fb_mx_split(const void* x, void* out, const fb_shape_t* s, void* stream);
+
+/* Bytes of fb_mx_split's output (0 for shapes fb_gemv_mx does not take). */
+size_t fb_mx_split_bytes(const fb_shape_t* s);
+
 /* GF4 packer on the GPU: the same arithmetic as fb_quantize_gf4 (keep == NULL) and
  * fb_quantize_gf4_masked, one wavefront per (row, 128-group), fp64; the outputs are
  * bit-identical to the host packers.  w fp32 [N,K], keep uint8 [N,K] or NULL, codes uint8

@@ -345,6 +345,88 @@ def e2m1_dequant(codes: np.ndarray, scales: np.ndarray, group: int = E2M1_GROUP)
 
 
 # --------------------------------------------------------------------------------------
+# Activations as two MX-E4M3 terms (the B operand of the native FP4 MFMA path)
+# --------------------------------------------------------------------------------------
+E4M3_MAX = 448.0
+MX_BLOCK = 32
+
+
+def e4m3_round(v: np.ndarray):
+    """Round |v| <= 448 (float64) to OCP E4M3 (e4m3fn: exponent bias 7, 3 fraction bits,
+    subnormal step 2**-9, largest finite 448), nearest with ties to even.  Returns
+    ``(codes uint8, values float64)``; the sign bit follows signbit(v).  No counterpart in
+    the reference (OCP 8-bit Floating Point Specification v1.0, E4M3)."""
+    v = np.asarray(v, np.float64)
+    a = np.abs(v)
+    if (a > E4M3_MAX).any():
+        raise ValueError("e4m3_round takes |v| <= 448")
+    _, ex = np.frexp(a)                          # a = m 2**ex, m in [0.5, 1)
+    e = np.maximum(ex.astype(np.int64) - 1, -6)  # binade; below 2**-6 the subnormal step
+    step = np.ldexp(1.0, e - 3)
+    r = np.round(a / step) * step                # np.round: half to even
+    _, ex2 = np.frexp(r)
+    e2 = np.where(r >= 2.0 ** -6, ex2.astype(np.int64) - 1, -7)  # -7: subnormal / zero
+    frac = np.where(e2 >= -6, r / np.ldexp(1.0, e2) - 1.0, r / 2.0 ** -9 / 8.0)
+    code = ((e2 + 7) << 3) | np.round(frac * 8).astype(np.int64)
+    code = np.where(r == 0, 0, code) | (np.signbit(v).astype(np.int64) << 7)
+    return code.astype(np.uint8), np.where(np.signbit(v), -r, r)
+
+
+def e4m3_decode(codes: np.ndarray) -> np.ndarray:
+    """E4M3 code -> float64 (codes 0x7F / 0xFF are NaN)."""
+    c = np.asarray(codes, np.int64)
+    e, m = (c >> 3) & 15, c & 7
+    mag = np.where(e > 0, np.ldexp(1.0 + m / 8.0, e - 7), np.ldexp(m / 8.0, -6))
+    mag = np.where((c & 0x7F) == 0x7F, np.nan, mag)
+    return np.where(c & 0x80, -mag, mag)
+
+
+def mx_exponent(amax: np.ndarray) -> np.ndarray:
+    """The smallest e with amax <= 448 * 2**e, clamped to the E8M0 range [-127, 127];
+    amax == 0 gives -127.  (Unlike OCP MX's floor(log2 amax) - 8, no value saturates.)"""
+    amax = np.asarray(amax, np.float64)
+    m, ex = np.frexp(amax)
+    e = ex.astype(np.int64) - 9 + (m > 0.875)
+    return np.clip(np.where(amax > 0, e, -127), -127, 127)
+
+
+def mx_split_x(x, terms: int = 2):
+    """x [B, K] (float values, e.g. bf16) -> ``(codes uint8 [terms, B, K], scales uint8
+    [terms, B, K/32])``.  Term t rounds to E4M3, per 32-value block with its own E8M0 scale
+    2**mx_exponent(block max), what the earlier terms left of x (float64, exact).  The
+    native FP4 path's split (fb_gemv_mx, fb_mx_split).  No counterpart in the reference."""
+    x = np.asarray(x, np.float64)
+    B, K = x.shape
+    if K % MX_BLOCK:
+        raise ValueError("K must be a multiple of 32")
+    rem = x.reshape(B, K // MX_BLOCK, MX_BLOCK).copy()
+    codes, scales = [], []
+    for _ in range(terms):
+        e = mx_exponent(np.abs(rem).max(-1))
+        c, val = e4m3_round(np.ldexp(rem, -e[..., None]))
+        rem = rem - np.ldexp(val, e[..., None])
+        codes.append(c.reshape(B, K))
+        scales.append((e + 127).astype(np.uint8))
+    return np.stack(codes), np.stack(scales)
+
+
+def mx_terms_value(codes: np.ndarray, scales: np.ndarray) -> np.ndarray:
+    """Sum of the terms of mx_split_x (float64 [B, K])."""
+    T, B, K = codes.shape
+    v = e4m3_decode(codes).reshape(T, B, K // MX_BLOCK, MX_BLOCK)
+    e = scales.astype(np.int64)[..., None] - 127
+    return np.ldexp(v, e).sum(0).reshape(B, K)
+
+
+def y_ref_mx(codes, scales_w, x, terms: int = 2):
+    """E2M1 W (exact decode) times the MX split of x, float64 [B, N]: what the native FP4
+    MFMA computes, up to its fp32 accumulation."""
+    W = e2m1_dequant(codes, scales_w).astype(np.float64)
+    c, s = mx_split_x(np.asarray(x, np.float64), terms)
+    return mx_terms_value(c, s) @ W.T
+
+
+# --------------------------------------------------------------------------------------
 # Nibble packing
 # --------------------------------------------------------------------------------------
 def pack_nibbles(codes: np.ndarray) -> np.ndarray:

@@ -1,0 +1,186 @@
+"""The native FP4 path (fb_gemv_mx): E2M1 weights on v_mfma_scale_f32_16x16x128_f8f6f4, with
+x split into two MX-E4M3 terms.  No counterpart in the reference, whose product is F.linear
+on the dequantized weight (layers.py:36-38); the path is the matrix cores' native FP4 mode
+for the small-batch contraction.
+
+- The split (fb_mx_split) against the oracle's mx_split_x, byte for byte.
+- The GEMV against the product of the device-decoded weight (bit-identical to the host and
+  oracle decodes, checked on sampled rows) with the oracle's split of x, in fp64: the
+  MFMA's fp32 accumulation is the only difference allowed, |err| <= 2^-16 sum |w x|.
+- The GEMV against the exact product (bf16 x, unsplit) within the north star's tolerance,
+  |y - y_ref| <= 1e-2 + 1e-3 |y_ref|: config 5a's shapes and generator (Student-t weights,
+  bf16 x with 20x outliers), the split-K and sliced plans, ragged rows, every output dtype.
+"""
+import ctypes
+import sys
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import fourbit_oracle as O
+from if_i_could_turn_back_time_amd import _capi as C
+from if_i_could_turn_back_time_amd import PackedWeight, QuantLinear
+from if_i_could_turn_back_time_amd import workloads as WL
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda:0"
+ATOL, RTOL = 1e-2, 1e-3
+ACC_REL = 2.0 ** -16  # fp32 accumulation against fp64, relative to sum |w x|
+
+
+def say(*a):
+    print(*a, flush=True)
+    sys.stdout.flush()
+
+
+def _x_cases(B, K, kind, seed):
+    g = torch.Generator().manual_seed(seed)
+    x = WL.synth_x("cfg2", B, K, g).float()
+    if kind == "edges":
+        x[0, :32] = 0.0                                   # an all-zero block
+        x[0, 32:64] *= 1e-30                              # tiny values
+        if B > 1:
+            x[1, :64] *= 1e30                             # huge values
+            x[1, 64:96] = torch.linspace(-3e4, 3e4, 32)   # a wide block
+            x[1, 96] = -3.0e38
+        x[0, 128:160] = torch.tensor(2.0) ** torch.arange(-20, 12).float()  # 31 binades
+    return x.to(torch.bfloat16)
+
+
+@pytest.mark.parametrize("B,K,kind", [(1, 128, "plain"), (3, 1024, "edges"), (16, 4096, "edges"),
+                                      (16, 11008, "plain"), (8, 8192, "plain")],
+                         ids=lambda v: str(v))
+def test_mx_split_bit_exact_vs_oracle(B, K, kind):
+    say("mx split", B, K, kind)
+    x = _x_cases(B, K, kind, B * 7 + K)
+    shape = C.make_shape(64, K, B, C.FMT_E2M1, 0, C.DT_BF16, C.DT_F32)
+    codes, scales = C.mx_split(x.to(DEV), shape)
+    torch.cuda.synchronize()
+    oc, osc = O.mx_split_x(x.float().numpy())
+    assert np.array_equal(scales.cpu().numpy(), osc)
+    assert np.array_equal(codes.cpu().numpy(), oc)
+
+
+_PW = {}
+
+
+def _packed(N, K):
+    key = (N, K)
+    if key not in _PW:
+        _PW.clear()
+        torch.cuda.empty_cache()
+        w = WL.synth_weight("cfg2", N, K, torch.Generator().manual_seed(N + K))
+        pw = PackedWeight.quantize(w, "e2m1", device=DEV, packer="gpu")
+        W = pw.dequant_device(torch.float32)
+        rows = torch.randint(0, N, (16,), generator=torch.Generator().manual_seed(N))
+        host = torch.stack([torch.from_numpy(pw.dequant_host_row(int(r))) for r in rows])
+        assert torch.equal(W[rows].cpu().view(torch.int32), host.view(torch.int32))
+        _PW[key] = (pw, W, rows)
+    return _PW[key]
+
+
+def _check_mx(N, K, B, kind="plain"):
+    pw, W, rows = _packed(N, K)
+    x = _x_cases(B, K, kind, 1000 + B)
+    xd = x.to(DEV)
+    y = pw.gemv_mx(xd, out_dtype=torch.float32)
+    # the oracle's split in fp64, times the decoded weight in fp64 (on the GPU)
+    oc, osc = O.mx_split_x(x.float().numpy())
+    xs = torch.from_numpy(O.mx_terms_value(oc, osc)).to(DEV)
+    W64 = W.double()
+    y_mx = xs @ W64.t()
+    mag = xs.abs() @ W64.abs().t()
+    y_exact = xd.double() @ W64.t()
+    torch.cuda.synchronize()
+    ratio = float(((y.double() - y_mx).abs() / (mag + 1e-300)).max())
+    say(f"  max |y - y_mx| / sum|w x| = {ratio:.3g} (2^{np.log2(max(ratio, 1e-300)):.1f})")
+    assert bool(((y.double() - y_mx).abs() <= ACC_REL * mag + 1e-30).all()), ratio
+    err = (y.double() - y_exact).abs()
+    assert bool((err <= ATOL + RTOL * y_exact.abs()).all()), float(err.max())
+    # sampled rows: the oracle's own decode of the packed codes and its split product
+    codes = O.unpack_nibbles(pw.codes[rows].numpy())
+    y_o = torch.from_numpy(O.y_ref_mx(codes, pw.meta[rows].numpy(), x.float().numpy()))
+    mag_o = torch.from_numpy(np.abs(O.mx_terms_value(oc, osc)) @
+                             np.abs(O.e2m1_dequant(codes, pw.meta[rows].numpy())).astype(np.float64).T)
+    assert bool(((y[:, rows].double().cpu() - y_o).abs() <= ACC_REL * mag_o + 1e-30).all())
+    # the same call again gives the same bits; narrower outputs are y rounded
+    assert torch.equal(pw.gemv_mx(xd, out_dtype=torch.float32), y)
+    for dt, ulp in ((torch.bfloat16, 2.0 ** -8), (torch.float16, 2.0 ** -11)):
+        yn = pw.gemv_mx(xd, out_dtype=dt).double()
+        ok = (yn - y.double()).abs() <= ulp * y.double().abs() + 1e-7
+        assert bool((ok | ~torch.isfinite(y.to(dt).double())).all()), dt
+
+
+@pytest.mark.parametrize("N,K,B,kind", [
+    (96, 128, 1, "plain"), (100, 1024, 3, "edges"), (4096, 4096, 1, "plain"),
+    (4096, 4096, 8, "edges"), (130, 28672, 4, "plain"),
+    # config 5a: E2M1 with bf16 x at batch 8 / 16 (one slice, K-slices), and the split-K plan
+    (8192, 8192, 8, "plain"), (8192, 8192, 16, "plain"), (28672, 8192, 8, "plain"),
+    (28672, 8192, 16, "plain"), (4096, 11008, 16, "plain"),
+], ids=lambda v: str(v))
+def test_gemv_mx_vs_oracle(N, K, B, kind):
+    say("gemv mx", N, K, B, kind)
+    _check_mx(N, K, B, kind)
+
+
+def test_gemv_mx_against_the_bf16_path():
+    """The native FP4 path and the exact-decode bf16 path agree within the tolerance on
+    config 5a's layer, and their difference is the split's (zero where the split is exact)."""
+    pw, W, _ = _packed(8192, 8192)
+    x = _x_cases(16, 8192, "plain", 5).to(DEV)
+    y_mx = pw.gemv_mx(x, out_dtype=torch.float32)
+    y_bf = pw.gemv(x, out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    err = (y_mx - y_bf).abs()
+    assert bool((err <= ATOL + RTOL * y_bf.abs()).all()), float(err.max())
+    say(f"  fp4 mfma vs bf16 mfma: max abs diff {float(err.max()):.3g}")
+
+
+def test_quantlinear_fp4_mfma():
+    """QuantLinear(..., fp4_mfma=True): forward on any leading shape and dtype against the
+    default path, backward through the decoded weight, and the formats it refuses."""
+    torch.manual_seed(0)
+    lin = torch.nn.Linear(1000, 300)
+    q = QuantLinear(lin, fmt="e2m1", fp4_mfma=True).to(DEV)
+    ref = QuantLinear(lin, fmt="e2m1").to(DEV)
+    x = torch.randn(3, 7, 1000, device=DEV)
+    for dt in (torch.bfloat16, torch.float32):
+        y = q(x.to(dt))
+        y0 = ref(x.to(torch.bfloat16).to(dt))
+        assert y.shape == (3, 7, 300) and y.dtype == dt
+        err = (y.float() - y0.float()).abs()
+        assert bool((err <= ATOL + 2e-2 * y0.float().abs()).all()), float(err.max())
+    xg = x.to(torch.bfloat16).requires_grad_(True)
+    q(xg).float().sum().backward()
+    xg0 = x.to(torch.bfloat16).requires_grad_(True)
+    ref(xg0).float().sum().backward()
+    assert torch.equal(xg.grad, xg0.grad)
+    with pytest.raises(ValueError):
+        QuantLinear(lin, fmt="gf4", fp4_mfma=True)
+    with pytest.raises(ValueError):
+        QuantLinear(torch.nn.Linear(1024, 64), fmt="e2m1", hadamard=True, fp4_mfma=True)
+
+
+def test_gemv_mx_workspace_contract():
+    """fb_gemv_mx refuses a missing, short or misaligned workspace with its error code and
+    writes nothing; a larger one is fine."""
+    pw, W, _ = _packed(96, 128)
+    x = torch.randn(2, 128).to(torch.bfloat16).to(DEV)
+    y = torch.full((2, 96), 7.0, device=DEV)
+    shape = pw.shape(2, torch.bfloat16, torch.float32)
+    need = C.mx_workspace_bytes(shape)
+    assert need == (2 * 128 * 2 + 255) // 256 * 256 + 256
+    L = C.lib()
+    ws = torch.empty(need + 512, dtype=torch.uint8, device=DEV)
+    args = (C._ptr(pw.wdev), C._ptr(x), C._ptr(y), ctypes.byref(shape))
+    st = C._stream(x.device)
+    assert L.fb_gemv_mx(*args, None, need, st) == -1                     # FB_ERR_NULL
+    assert L.fb_gemv_mx(*args, C._ptr(ws), need - 1, st) == -8           # FB_ERR_WORKSPACE
+    assert L.fb_gemv_mx(*args, C._ptr(ws) + 16, need, st) == -7          # FB_ERR_ALIGN
+    torch.cuda.synchronize()
+    assert bool((y == 7.0).all())
+    assert L.fb_gemv_mx(*args, C._ptr(ws), need + 512, st) == 0
+    torch.cuda.synchronize()
+    yref = x.double() @ W.double().t()
+    assert bool(((y.double() - yref).abs() <= ATOL + RTOL * yref.abs()).all())

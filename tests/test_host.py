@@ -682,3 +682,30 @@ def test_gemv_noalloc_validation_needs_no_gpu():
     assert L.fb_gemv_noalloc(buf, buf, buf, None, None) == -1
     bad = C.make_shape(64, 100, 1)
     assert L.fb_gemv_noalloc(buf, buf, buf, ctypes.byref(bad), None) == -2
+
+
+def test_gemv_mx_validation_needs_no_gpu():
+    """fb_gemv_mx checks the shape, pointers and workspace before any device call, and the
+    workspace is the split (B*K*2 + 8*B*K/128, each rounded up to 256) plus the split-K
+    parts' sums of the same plan as fb_gemv's."""
+    L = C.lib()
+    arena = np.zeros(1 << 16, np.uint8)
+    base = arena.ctypes.data
+    p = base + (-base) % 256  # 256-byte aligned host addresses: never dereferenced here
+    s = C.make_shape(4096, 11008, 16, C.FMT_E2M1, 0, C.DT_BF16, C.DT_F32)
+    split = 16 * 11008 * 2 + (16 * 86 * 8 + 255) // 256 * 256
+    assert L.fb_mx_split_bytes(ctypes.byref(s)) == split
+    assert L.fb_mx_workspace_bytes(ctypes.byref(s)) == split + L.fb_workspace_bytes(ctypes.byref(s))
+    assert L.fb_workspace_bytes(ctypes.byref(s)) == 4 * 16 * 4096 * 4  # split-K, P = 4
+    call = lambda sh, ws, n: L.fb_gemv_mx(p, p, p, ctypes.byref(sh), ws, n, None)
+    assert call(s, p, split - 1) == -8                                   # FB_ERR_WORKSPACE
+    assert call(s, None, split) == -1                                    # FB_ERR_NULL
+    assert call(s, p + 16, 1 << 30) == -7                                # FB_ERR_ALIGN
+    for kw, code in (({"x_dtype": C.DT_F16}, -5), ({"fmt": C.FMT_GF4, "x_dtype": C.DT_F16}, -4),
+                     ({"fwht_block": 256}, -6), ({"B": 17}, -9), ({"K": 100}, -2)):
+        sh = C.make_shape(**{**dict(N=4096, K=11008, B=16, fmt=C.FMT_E2M1, fwht_block=0,
+                                    x_dtype=C.DT_BF16, y_dtype=C.DT_F32), **kw})
+        assert call(sh, p, 1 << 30) == code, kw
+        assert L.fb_mx_workspace_bytes(ctypes.byref(sh)) == 0
+        assert L.fb_mx_split(p, p, ctypes.byref(sh), None) == code
+    assert L.fb_mx_split(p, p + 16, ctypes.byref(s), None) == -7

@@ -518,3 +518,120 @@ def test_jenks2_degenerate_inputs():
     assert split == 4 and not keep[:4].any() and keep[4:].all()
     keep, split, gvf, _ = O.jenks2(np.array([2.5], np.float32))
     assert split == 0 and keep.all()
+
+
+# ----------------------------------------------------------------- MX-E4M3 activation split
+def test_e4m3_round_matches_torch_float8_e4m3fn():
+    """The E4M3 rounding against torch's own float8_e4m3fn conversion (an independent
+    implementation of the OCP format): uniform values, values near zero (subnormals) and
+    every midpoint between neighbouring codes (ties to even)."""
+    codes = np.array([c for c in range(128) if c != 0x7F], np.uint8)
+    vals = O.e4m3_decode(codes)
+    mids = (vals[:-1] + vals[1:]) / 2
+    a = np.concatenate([RNG.uniform(-448, 448, 20000), RNG.uniform(-0.03, 0.03, 20000),
+                        mids, -mids, vals, -vals, [0.0, -0.0, 448.0, -448.0]])
+    a = a.astype(np.float32).astype(np.float64)  # exactly the values torch converts
+    c, v = O.e4m3_round(a)
+    t = torch.from_numpy(a.astype(np.float32)).to(torch.float8_e4m3fn)
+    assert np.array_equal(c, t.view(torch.uint8).numpy())
+    assert np.array_equal(v, t.float().double().numpy())
+
+
+def test_e4m3_codes_round_trip_and_table():
+    """Every finite code decodes to the OCP value (closed form 2**(e-7) (1 + m/8), and
+    m/8 2**-6 for e = 0) and encodes back to itself."""
+    for c in range(256):
+        if c & 0x7F == 0x7F:
+            assert np.isnan(O.e4m3_decode(np.array([c]))[0])
+            continue
+        e, m = (c >> 3) & 15, c & 7
+        want = (2.0 ** (e - 7)) * (1 + m / 8) if e else (m / 8) * 2.0 ** -6
+        want = -want if c & 0x80 else want
+        got = O.e4m3_decode(np.array([c], np.uint8))[0]
+        assert got == want and np.signbit(got) == bool(c & 0x80)
+        c2, _ = O.e4m3_round(np.array([got]))
+        assert c2[0] == c
+    assert O.e4m3_decode(np.array([0x7E]))[0] == 448.0
+
+
+def test_mx_exponent_is_the_smallest_unsaturated_scale():
+    a = np.concatenate([np.exp(RNG.uniform(-80, 80, 5000)), [448.0, 449.0, 447.99, 1.0, 0.875]])
+    e = O.mx_exponent(a)
+    assert (a <= 448.0 * np.exp2(e.astype(np.float64))).all()
+    assert (a > 448.0 * np.exp2(e.astype(np.float64) - 1)).all()
+    assert list(O.mx_exponent(np.array([448.0, 449.0, 1.0, 0.0, 1e-45, 3e38]))) == \
+        [0, 1, -8, -127, -127, 120]  # 3e38 = 451 x 2**119
+
+
+def _bf16(a):
+    return torch.from_numpy(np.asarray(a, np.float32)).to(torch.bfloat16).float().double().numpy()
+
+
+def test_mx_split_known_answers():
+    """A block of ones: t0 = 256 x 2**-8 (code 0x78, scale byte 119) and t1 = 0 (the
+    all-zero block's scale byte 0); 1 + 2**-7 (a bf16 value with 8 significant bits) puts
+    2**-7 into t1 with its own scale."""
+    x = np.ones((1, 32))
+    c, s = O.mx_split_x(x)
+    assert (c[0] == 0x78).all() and (s[0] == 119).all()
+    assert (c[1] == 0).all() and (s[1] == 0).all()
+    x[0, 3] = 1 + 2.0 ** -7
+    c, s = O.mx_split_x(x)
+    assert s[0, 0, 0] == 119 and c[0, 0, 3] == 0x78
+    # t1: only element 3 is left, 2**-7 = 256 x 2**-15 -> scale byte 112, code 0x78
+    assert s[1, 0, 0] == 112 and c[1, 0, 3] == 0x78 and (np.delete(c[1, 0], 3) == 0).all()
+    assert np.array_equal(O.mx_terms_value(c, s), x)
+
+
+def test_mx_split_holds_bf16_exactly():
+    """Two terms hold bf16 x exactly when a block spans less than E4M3's exponent range
+    (8 significant bits = 4 + 4): normal activations with 20x outliers, and large / small
+    magnitudes.  The sum of the terms is compared with x itself."""
+    x = RNG.standard_normal((16, 4096))
+    x[RNG.random(x.shape) < 1e-3] *= 20
+    x[3] *= 1e30
+    x[4] *= 1e-30
+    x = _bf16(x)
+    c, s = O.mx_split_x(x)
+    v = O.mx_terms_value(c, s)
+    ok = v == x
+    # the only values allowed to differ: those 2**14 or more below their block's largest
+    blk = np.abs(x).reshape(16, -1, 32).max(-1).repeat(32, 1)
+    assert ok[np.abs(x) * 2.0 ** 13 >= blk].all()
+    assert ok.mean() > 0.9999
+
+
+def test_mx_split_error_bound_wide_blocks():
+    """Blocks spanning more than E4M3's range lose only what the last term rounds away:
+    per element at most half the E4M3 spacing at what t0 left, r, in t1's scale 2**e1 --
+    2**(b - 4) for r in binade b >= e1 - 6, and 2**(e1 - 10) below (subnormal step)."""
+    x = np.concatenate([RNG.standard_normal((4, 32)) * 1e-6,
+                        RNG.standard_normal((4, 32))], 1).reshape(8, 32)
+    x[:, 0] = 3.0e4  # one large value per block
+    x = _bf16(x)
+    c, s = O.mx_split_x(x)
+    err = np.abs(O.mx_terms_value(c, s) - x)
+    r = x - O.mx_terms_value(c[:1], s[:1])
+    e1 = (s[1].astype(np.int64) - 127).repeat(32, 1)
+    _, ex = np.frexp(np.abs(r))
+    b = np.maximum(ex - 1, e1 - 6)
+    assert (err <= np.exp2(b - 4.0)).all()
+    assert err.max() > 0  # the case is a lossy one
+
+
+def test_y_ref_mx_matches_the_exact_product():
+    """Config 5a's weights and activations (Student-t weights, bf16 x with outliers): the
+    MX-split product differs from the exact one by no more than the split's own error
+    carried through |W|, and is far inside the GEMV tolerance."""
+    from if_i_could_turn_back_time_amd import workloads as WL
+    g = torch.Generator().manual_seed(3)
+    w = WL.synth_weight("cfg2", 64, 1024, g).numpy()
+    codes, sc = O.e2m1_quantize(w)
+    x = WL.synth_x("cfg2", 8, 1024, g).to(torch.bfloat16).float().numpy()
+    y = O.y_ref_mx(codes, sc, x)
+    W = O.e2m1_dequant(codes, sc).astype(np.float64)
+    y_exact = x.astype(np.float64) @ W.T
+    c, s = O.mx_split_x(x)
+    dx = np.abs(O.mx_terms_value(c, s) - x)
+    assert (np.abs(y - y_exact) <= dx @ np.abs(W).T + 1e-12).all()
+    assert np.abs(y - y_exact).max() <= 1e-6
