@@ -56,7 +56,7 @@ def n_copies(nbytes: int, cold: bool) -> int:
 
 
 def time_gpu(pw: PackedWeight, x: torch.Tensor, y: torch.Tensor, steps: int, warmup: int,
-             cold: bool = True, windows: int = 0, mx: bool = False):
+             cold: bool = True, windows: int = 0, mx: str = ""):
     """Back-to-back launches on the current stream, timed with HIP events on that stream
     (the stream fb_gemv launches on).  cold: cycle through weight copies that together
     exceed the Infinity Cache.
@@ -66,8 +66,10 @@ def time_gpu(pw: PackedWeight, x: torch.Tensor, y: torch.Tensor, steps: int, war
     event is stamped on a busy GPU: the host's first launch latency (argument checks,
     plan, ctypes) would otherwise land inside the region.  ``windows`` more regions of
     the same length follow for the median.  Returns (mean ms per call of the first
-    region, number of weight copies, [ms per call of each extra region]).  mx: time
-    fb_gemv_mx (the native FP4 path, its x split included) instead of fb_gemv."""
+    region, number of weight copies, [ms per call of each extra region]).  mx: "split" times
+    fb_gemv_mx (the native FP4 path, its x split included) instead of fb_gemv; "presplit"
+    times fb_gemv_mx_presplit on one split made beforehand (what each further layer with the
+    same input costs)."""
     L = C.lib()
     shape = pw.shape(x.shape[0], x.dtype, y.dtype)
     sref = ctypes.byref(shape)
@@ -75,9 +77,15 @@ def time_gpu(pw: PackedWeight, x: torch.Tensor, y: torch.Tensor, steps: int, war
     copies = [pw.wdev] + [pw.wdev.clone() for _ in range(ncp - 1)]
     wps = [c.data_ptr() for c in copies]
     xp, yp = x.data_ptr(), y.data_ptr()
-    if mx:
+    if mx == "split":
         ws = torch.empty(C.mx_workspace_bytes(shape), dtype=torch.uint8, device=x.device)
         gemv = L.fb_gemv_mx
+    elif mx == "presplit":
+        xsplit = C.mx_split_raw(x, shape)
+        xp = xsplit.data_ptr()
+        nws = L.fb_mx_presplit_workspace_bytes(sref)
+        ws = torch.empty(nws, dtype=torch.uint8, device=x.device) if nws else None
+        gemv = L.fb_gemv_mx_presplit
     else:
         ws = C.new_workspace(shape, x.device)
         gemv = L.fb_gemv
@@ -254,10 +262,10 @@ def time_gpu_pack(w: torch.Tensor, pw: PackedWeight, reps: int = 3):
 def run_workload(name: str, steps: int, warmup: int, want_cpu: bool, check: bool = True,
                  warm: bool = False, cache: dict | None = None, pack_check: bool = False,
                  packer: str = "host", windows: int = 0, cpu_budget_s: float = 12.0,
-                 mx: bool = False):
+                 mx: str = ""):
     """cache: packed weights by (fmt, K, N, kind, rotation), reused across batch sizes (the
-    weights are drawn before the activations, so they do not depend on the batch).  mx: the
-    native FP4 path (fb_gemv_mx; unrotated E2M1 workloads)."""
+    weights are drawn before the activations, so they do not depend on the batch).  mx:
+    "split" / "presplit", the native FP4 path (unrotated E2M1 workloads; see time_gpu)."""
     fmt, K, N, B, kind, fwht = WORKLOADS[name]
     if mx and (fmt != "e2m1" or fwht):
         raise ValueError(f"{name}: the native FP4 path takes unrotated E2M1 layers")
@@ -294,7 +302,7 @@ def run_workload(name: str, steps: int, warmup: int, want_cpu: bool, check: bool
     gbs = nbytes / (ms * 1e-3) / 1e9
     rec = {
         "workload": name, "fmt": fmt, "K": K, "N": N, "B": B, "fwht_block": fb,
-        "path": "fp4_mfma" if mx else "exact_decode",
+        "path": {"split": "fp4_mfma", "presplit": "fp4_mfma_presplit"}.get(mx, "exact_decode"),
         "bytes_per_call": nbytes, "weight_stream_bytes": N * K // 2,
         "us_per_call": ms * 1e3, "GBps": gbs, "frac_of_8TBps": gbs / PEAK_GBS,
         "weight_copies_cycled": ncp, "warmup_calls_run": warm_calls,
@@ -308,8 +316,11 @@ def run_workload(name: str, steps: int, warmup: int, want_cpu: bool, check: bool
     }
     if check:  # spot parity: sampled rows vs exact host decode + F.linear (fp32)
         yk = torch.empty(B, N, dtype=torch.float32, device="cuda:0")
-        if mx:
+        if mx == "split":
             pw.gemv_mx(xd, out=yk)
+        elif mx == "presplit":
+            sh = pw.shape(B, xd.dtype, torch.float32)
+            C.gemv_mx_presplit(pw.wdev, C.mx_split_raw(xd, sh), yk, sh)
         else:
             pw.gemv(xd, out=yk)
         rows = torch.randint(0, N, (64,), generator=torch.Generator().manual_seed(1))
@@ -623,7 +634,7 @@ def main():
             names = [args.workload]
         cache = {}
         for name in names:
-            for mx in (False, True):
+            for mx in ("", "split", "presplit"):
                 rec, pw = run_workload(name, args.steps, args.warmup, False, cache=cache,
                                        windows=MEDIAN_WINDOWS, mx=mx)
                 del pw

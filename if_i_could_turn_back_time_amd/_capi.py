@@ -36,6 +36,7 @@ EXPORTED = (
     "fb_quantize_e2m1_gpu", "fb_jenks2_host", "fb_jenks2_workspace", "fb_jenks2_gpu",
     "fb_jenks2_filters_host", "fb_jenks2_filters_gpu", "fb_gemv_noalloc",
     "fb_mx_split_bytes", "fb_mx_split", "fb_mx_workspace_bytes", "fb_gemv_mx",
+    "fb_gemv_mx_presplit", "fb_mx_presplit_workspace_bytes",
 )
 
 
@@ -89,6 +90,8 @@ def lib() -> ctypes.CDLL:
         "fb_mx_split": (ctypes.c_int, [vp, vp, sp, vp]),
         "fb_mx_workspace_bytes": (sz, [sp]),
         "fb_gemv_mx": (ctypes.c_int, [vp, vp, vp, sp, vp, sz, vp]),
+        "fb_gemv_mx_presplit": (ctypes.c_int, [vp, vp, vp, sp, vp, sz, vp]),
+        "fb_mx_presplit_workspace_bytes": (sz, [sp]),
     }
     for name, (res, args) in sigs.items():
         fn = getattr(L, name)
@@ -310,20 +313,51 @@ def gemv_mx(wdev: torch.Tensor, x: torch.Tensor, y: torch.Tensor, shape: FbShape
     return y
 
 
-def mx_split(x: torch.Tensor, shape: FbShape):
-    """The split fb_gemv_mx makes of x (bf16 [B, K] on the GPU): (codes uint8 [2, B, K],
-    scales uint8 [2, B, K/32]) -- term t of value (b, k) and of its 32-value block."""
+def mx_split_raw(x: torch.Tensor, shape: FbShape) -> torch.Tensor:
+    """fb_mx_split of x (bf16 [B, K] on the GPU): the split in its device layout (uint8),
+    the input of gemv_mx_presplit."""
     if not x.is_cuda or x.dtype != torch.bfloat16 or not x.is_contiguous():
         raise ValueError("x must be a contiguous bfloat16 device tensor")
     if tuple(x.shape) != (shape.B, shape.K):
         raise ValueError("x does not match the shape")
-    B, K = shape.B, shape.K
     nbytes = lib().fb_mx_split_bytes(ctypes.byref(shape))
     if not nbytes:
         _mx_refuse(shape)
     out = torch.empty(nbytes, dtype=torch.uint8, device=x.device)
     with torch.cuda.device(x.device):
         check(lib().fb_mx_split(_ptr(x), _ptr(out), ctypes.byref(shape), _stream(x.device)))
+    return out
+
+
+def gemv_mx_presplit(wdev: torch.Tensor, xs: torch.Tensor, y: torch.Tensor, shape: FbShape,
+                     workspace: torch.Tensor | None = None) -> torch.Tensor:
+    """gemv_mx on a split made by mx_split_raw (one split for several layers with the same
+    input)."""
+    if not (wdev.is_cuda and xs.is_cuda and y.is_cuda):
+        raise RuntimeError("fb_gemv_mx_presplit needs device tensors (ROCm GPU)")
+    if not (wdev.device == xs.device == y.device):
+        raise ValueError("fb_gemv_mx_presplit operands are on different devices")
+    if xs.numel() < lib().fb_mx_split_bytes(ctypes.byref(shape)):
+        raise ValueError("xs is smaller than fb_mx_split_bytes(shape)")
+    if tuple(y.shape) != (shape.B, shape.N) or DTYPE_CODE.get(y.dtype) != shape.y_dtype:
+        raise ValueError("y does not match the shape")
+    if wdev.numel() < device_bytes(shape):
+        raise ValueError("weight stream is smaller than fb_device_bytes(shape)")
+    need = lib().fb_mx_presplit_workspace_bytes(ctypes.byref(shape))
+    if need and (workspace is None or workspace.numel() < need):
+        workspace = torch.empty(need, dtype=torch.uint8, device=y.device)
+    wp = _ptr(workspace) if need else None
+    with torch.cuda.device(y.device):
+        check(lib().fb_gemv_mx_presplit(_ptr(wdev), _ptr(xs), _ptr(y), ctypes.byref(shape), wp,
+                                        need, _stream(y.device)))
+    return y
+
+
+def mx_split(x: torch.Tensor, shape: FbShape):
+    """The split fb_gemv_mx makes of x (bf16 [B, K] on the GPU): (codes uint8 [2, B, K],
+    scales uint8 [2, B, K/32]) -- term t of value (b, k) and of its 32-value block."""
+    out = mx_split_raw(x, shape)
+    B, K = shape.B, shape.K
     soff = (B * K * 2 + 255) // 256 * 256
     terms = out[:B * K * 2].view(B, K // 128, 2, 128).permute(2, 0, 1, 3).reshape(2, B, K)
     sc = out[soff:soff + B * (K // 128) * 8].view(B, K // 128, 2, 4).permute(2, 0, 1, 3)

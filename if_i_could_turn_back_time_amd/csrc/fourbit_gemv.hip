@@ -937,6 +937,22 @@ __global__ __launch_bounds__(NW * 64) void gemv_kernel(
   // x through a buffer resource (out-of-range offsets read zeros)
   const rsrc_t xrs = __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(x), (short)0, B * K * 2,
                                                        kRsrcWord3);
+  // MX path: the split's block scales, 8 bytes per (batch row, 128-value group), staged into
+  // the pad of each staged group (zeros past K).  Entry i of a slice is row i / nsl, group
+  // k0 / 128 + i % nsl.
+  const int G = K / 128;
+  const rsrc_t srs = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(xsc), (short)0,
+                                                       mx ? B * G * 8 : 0, kRsrcWord3);
+  auto sc_load = [&](int i, int k0) -> uint2 {
+    const int b = fdiv(i >> 2, SPL, spl_m);  // i / nsl, nsl = 4 SPL
+    const int gi = k0 / 128 + i - b * nsl;
+    const unsigned off = gi < G ? (unsigned)(b * G + gi) * 8u : kXOutOfRange;
+    return __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(srs, off, 0, 0));
+  };
+  auto sc_store = [&](int i, uint2 v) {
+    const int b = fdiv(i >> 2, SPL, spl_m);
+    *reinterpret_cast<uint2*>(xst + b * RS + (i - b * nsl) * kSliceBytes + 256) = v;
+  };
   // Each wave's first two units are static (wave, wave + NW); the counter hands out
   // the rest.
   constexpr bool rot = MODE == kRotated || rot1;
@@ -961,6 +977,11 @@ __global__ __launch_bounds__(NW * 64) void gemv_kernel(
       rot_preload<NW>(xr, xrs, K, B, k0, kw, fwht_block, tid);
     else
       x_preload<NT, XP, flat1>(xp, xrs, K, k0, per_row, B * per_row, row_of_wave, wv, tid);
+    // MX: the thread's first scale entry is requested with its x (a slice has at most
+    // kLdsLimit / 272 < NT entries whenever its x fits LDS, so this is usually all of them)
+    uint2 sc_first = {0u, 0u};
+    if constexpr (mx)
+      if (tid < B * nsl) sc_first = sc_load(tid, k0);
     if (s == 0) PH_MARK(kPhXIssued);
     if constexpr (MODE != kFlat && !rot1 && !flat1) {
       if (s == nslices - 1 && spl_last != SPL) {  // a last slice with fewer spans
@@ -994,18 +1015,8 @@ __global__ __launch_bounds__(NW * 64) void gemv_kernel(
     else
       stage_plain<NT, XP, flat1>(xst, xp, xrs, K, B, k0, nsl, RS, row_of_wave, wv, tid);
     if constexpr (mx) {
-      // the split's block scales into the pad of each staged group (zeros past K)
-      const int G = K / 128;
-      const rsrc_t srs = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(xsc), (short)0,
-                                                           B * G * 8, kRsrcWord3);
-      for (int i = tid; i < B * nsl; i += NT) {
-        const int b = fdiv(i >> 2, SPL, spl_m);  // i / nsl, nsl = 4 SPL
-        const int it = i - b * nsl;
-        const int gi = k0 / 128 + it;
-        const unsigned off = gi < G ? (unsigned)(b * G + gi) * 8u : kXOutOfRange;
-        const uint2 sc = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(srs, off, 0, 0));
-        *reinterpret_cast<uint2*>(xst + b * RS + it * kSliceBytes + 256) = sc;
-      }
+      if (tid < B * nsl) sc_store(tid, sc_first);
+      for (int i = tid + NT; i < B * nsl; i += NT) sc_store(i, sc_load(i, k0));
     }
     __syncthreads();  // x staged, counter set
     PH_MARK(s == 0 ? kPhStaged : s == 1 ? kPhStaged1 : kPhStaged2);
@@ -1494,32 +1505,44 @@ int launch_mx_split(const void* x, void* out, const fb_shape_t* s, hipStream_t h
   return hipGetLastError() == hipSuccess ? FB_OK : FB_ERR_HIP;
 }
 
+// Checks shared by the native FP4 entry points: shape, then the 32-bit block offsets from
+// each workgroup's first block (as in gemv_impl).
+int mx_gemv_check(const fb_shape_t* s, int cus) {
+  const int st = mx_check(s);
+  if (st != FB_OK) return st;
+  const int64_t T = (s->N + 15) / 16, GS = (s->K / 128 + 3) / 4;
+  const int64_t grid = std::min<int64_t>(T, cus);
+  if ((T + grid - 1) / grid * GS * fb::kE2m1BlockBytes > INT32_MAX) return FB_ERR_SHAPE;
+  return FB_OK;
+}
+
+// The GEMV on a split of x (fb_mx_split's layout at xs); ws / ws_bytes may hold the split-K
+// parts' sums (without them the K-slices run in turn).
+int gemv_mx_split_run(const void* wdev, const void* xs, void* y, const fb_shape_t* s, int cus,
+                      void* ws, size_t ws_bytes, hipStream_t hs) {
+  fb_shape_t u = *s;
+  u.fmt = kFmtMx;
+  const uint8_t* x8 = static_cast<const uint8_t*>(xs);
+  return gemv_planned(wdev, x8, y, &u, cus, hs, ws, ws_bytes, x8 + mx_scale_offset(s->B, s->K));
+}
+
 // fb_gemv_mx behind the ABI: the split into the workspace's head, then the GEMV on it (with
 // the split-K parts' sums after the split where the plan runs them side by side).
 int gemv_mx_impl(const void* wdev, const void* x, void* y, const fb_shape_t* s, void* ws,
                  size_t ws_bytes, hipStream_t hs) {
   if (!s || !wdev || !x || !y || !ws) return FB_ERR_NULL;
-  int st = mx_check(s);
+  const int cus = device_cus();
+  int st = mx_gemv_check(s, cus);
   if (st != FB_OK) return st;
   if (!aligned16(wdev) || !aligned16(x) || (reinterpret_cast<uintptr_t>(y) & 3u) ||
       (reinterpret_cast<uintptr_t>(ws) & 255u))
     return FB_ERR_ALIGN;
-  const int cus = device_cus();
-  {
-    // 32-bit offsets from each workgroup's first block (as in gemv_impl)
-    const int64_t T = (s->N + 15) / 16, GS = (s->K / 128 + 3) / 4;
-    const int64_t grid = std::min<int64_t>(T, cus);
-    if ((T + grid - 1) / grid * GS * fb::kE2m1BlockBytes > INT32_MAX) return FB_ERR_SHAPE;
-  }
   const size_t need = mx_split_bytes(s->B, s->K);
   if (ws_bytes < need) return FB_ERR_WORKSPACE;
   st = launch_mx_split(x, ws, s, hs);
   if (st != FB_OK) return st;
-  fb_shape_t u = *s;
-  u.fmt = kFmtMx;
   uint8_t* w8 = static_cast<uint8_t*>(ws);
-  return gemv_planned(wdev, w8, y, &u, cus, hs, w8 + need, ws_bytes - need,
-                      w8 + mx_scale_offset(s->B, s->K));
+  return gemv_mx_split_run(wdev, w8, y, s, cus, w8 + need, ws_bytes - need, hs);
 }
 
 // Scratch of the allocation-free entry point: a file-scope device array (one per GPU the
@@ -1619,6 +1642,27 @@ size_t fb_mx_workspace_bytes(const fb_shape_t* s) {
 int fb_gemv_mx(const void* wdev, const void* x, void* y, const fb_shape_t* s, void* ws,
                size_t ws_bytes, void* stream) {
   return gemv_mx_impl(wdev, x, y, s, ws, ws_bytes, static_cast<hipStream_t>(stream));
+}
+
+int fb_gemv_mx_presplit(const void* wdev, const void* xs, void* y, const fb_shape_t* s,
+                        void* ws, size_t ws_bytes, void* stream) {
+  if (!s || !wdev || !xs || !y) return FB_ERR_NULL;
+  const int cus = device_cus();
+  const int st = mx_gemv_check(s, cus);
+  if (st != FB_OK) return st;
+  if (!aligned16(wdev) || (reinterpret_cast<uintptr_t>(xs) & 255u) ||
+      (reinterpret_cast<uintptr_t>(y) & 3u))
+    return FB_ERR_ALIGN;
+  if (ws && (reinterpret_cast<uintptr_t>(ws) & 255u)) ws = nullptr;  // misaligned: unused
+  if (!ws) ws_bytes = 0;
+  return gemv_mx_split_run(wdev, xs, y, s, cus, ws, ws_bytes, static_cast<hipStream_t>(stream));
+}
+
+size_t fb_mx_presplit_workspace_bytes(const fb_shape_t* s) {
+  if (!s || mx_check(s) != FB_OK) return 0;
+  fb_shape_t u = *s;
+  u.fmt = kFmtMx;
+  return splitk_bytes(&u, splitk_parts(&u, device_cus(), nullptr));
 }
 
 #ifdef FB_PHASE_TRACE

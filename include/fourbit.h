@@ -211,11 +211,23 @@ size_t fb_mx_workspace_bytes(const fb_shape_t* s);
  * term 0, then for term 1.  Term t rounds (nearest, ties to even) what the earlier terms
  * left of x, in units of its block's scale 2^e, e the smallest with the block's largest
  * magnitude <= 448 * 2^e (clamped to [-127, 127]; 0 for a block of zeros).  For callers
- * that reuse one split across layers that share their input. */
+ * that reuse one split across layers that share their input (fb_gemv_mx_presplit). */
 int fb_mx_split(const void* x, void* out, const fb_shape_t* s, void* stream);
 
 /* Bytes of fb_mx_split's output (0 for shapes fb_gemv_mx does not take). */
 size_t fb_mx_split_bytes(const fb_shape_t* s);
+
+/* fb_gemv_mx on a split made by fb_mx_split (xs: device, 256-byte aligned), for layers that
+ * share their input (q/k/v or gate/up projections): one split, then one of these per layer.
+ * Same results as fb_gemv_mx on the same x when given a workspace of
+ * fb_mx_presplit_workspace_bytes(s) bytes (the split-K parts' sums; 256-byte aligned); with
+ * NULL such shapes run their K-slices in turn, within the tolerance of that result.  Calls
+ * that share a workspace must not overlap.  The reference interface replaced is fb_gemv_mx's. */
+int fb_gemv_mx_presplit(const void* wdev, const void* xs, void* y, const fb_shape_t* s,
+                        void* ws, size_t ws_bytes, void* stream);
+
+/* Workspace bytes of fb_gemv_mx_presplit (0: none used, or a shape it does not take). */
+size_t fb_mx_presplit_workspace_bytes(const fb_shape_t* s);
 
 /* GF4 packer on the GPU: the same arithmetic as fb_quantize_gf4 (keep == NULL) and
  * fb_quantize_gf4_masked, one wavefront per (row, 128-group), fp64; the outputs are

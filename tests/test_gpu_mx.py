@@ -184,3 +184,32 @@ def test_gemv_mx_workspace_contract():
     torch.cuda.synchronize()
     yref = x.double() @ W.double().t()
     assert bool(((y.double() - yref).abs() <= ATOL + RTOL * yref.abs()).all())
+
+
+@pytest.mark.parametrize("N,K,B", [(8192, 8192, 8), (4096, 11008, 16), (100, 1024, 3)],
+                         ids=lambda v: str(v))
+def test_gemv_mx_presplit_equals_gemv_mx(N, K, B):
+    """One split (fb_mx_split), then fb_gemv_mx_presplit: the bits of fb_gemv_mx with a
+    workspace; without one (split-K shapes run their K-slices in turn) within the tolerance
+    of the exact product.  Two layers on the same split each give their own result."""
+    say("presplit", N, K, B)
+    pw, W, _ = _packed(N, K)
+    x = _x_cases(B, K, "plain", 77).to(DEV)
+    shape = pw.shape(B, torch.bfloat16, torch.float32)
+    xs = C.mx_split_raw(x, shape)
+    y_mx = pw.gemv_mx(x, out_dtype=torch.float32)
+    y_ps = C.gemv_mx_presplit(pw.wdev, xs, torch.empty(B, N, device=DEV), shape)
+    torch.cuda.synchronize()
+    assert torch.equal(y_ps, y_mx)
+    y_nows = torch.empty(B, N, device=DEV)
+    C.check(C.lib().fb_gemv_mx_presplit(C._ptr(pw.wdev), C._ptr(xs), C._ptr(y_nows),
+                                        ctypes.byref(shape), None, 0, C._stream(x.device)))
+    yref = x.double() @ W.double().t()
+    torch.cuda.synchronize()
+    assert bool(((y_nows.double() - yref).abs() <= ATOL + RTOL * yref.abs()).all())
+    # a second layer on the same split (64 rows of another weight)
+    w2 = WL.synth_weight("cfg2", 64, K, torch.Generator().manual_seed(9))
+    pw2 = PackedWeight.quantize(w2, "e2m1", device=DEV, packer="gpu")
+    sh2 = pw2.shape(B, torch.bfloat16, torch.float32)
+    y2 = C.gemv_mx_presplit(pw2.wdev, xs, torch.empty(B, 64, device=DEV), sh2)
+    assert torch.equal(y2, pw2.gemv_mx(x, out_dtype=torch.float32))

@@ -709,3 +709,23 @@ def test_gemv_mx_validation_needs_no_gpu():
         assert L.fb_mx_workspace_bytes(ctypes.byref(sh)) == 0
         assert L.fb_mx_split(p, p, ctypes.byref(sh), None) == code
     assert L.fb_mx_split(p, p + 16, ctypes.byref(s), None) == -7
+
+
+def test_gemv_mx_presplit_validation_needs_no_gpu():
+    """fb_gemv_mx_presplit: the shape checks of fb_gemv_mx, a 256-byte aligned split, and an
+    optional workspace (the split-K parts' sums only)."""
+    L = C.lib()
+    arena = np.zeros(1 << 16, np.uint8)
+    base = arena.ctypes.data
+    p = base + (-base) % 256
+    s = C.make_shape(4096, 11008, 16, C.FMT_E2M1, 0, C.DT_BF16, C.DT_F32)
+    assert L.fb_mx_presplit_workspace_bytes(ctypes.byref(s)) == L.fb_workspace_bytes(ctypes.byref(s))
+    s8 = C.make_shape(4096, 8192, 8, C.FMT_E2M1, 0, C.DT_BF16, C.DT_F32)
+    assert L.fb_mx_presplit_workspace_bytes(ctypes.byref(s8)) == 0
+    call = lambda sh, xs: L.fb_gemv_mx_presplit(p, xs, p, ctypes.byref(sh), None, 0, None)
+    assert call(s, None) == -1
+    assert call(s, p + 16) == -7
+    sh = C.make_shape(4096, 11008, 16, C.FMT_E2M1, 0, C.DT_F16, C.DT_F32)
+    assert call(sh, p) == -5
+    sh = C.make_shape(4096, 11008, 16, C.FMT_E2M1, 256, C.DT_BF16, C.DT_F32)
+    assert call(sh, p) == -6
