@@ -518,6 +518,55 @@ class QuantLinear(nn.Linear):
                 f"fmt={self.fmt}, fwht_block={self.fwht_block}, bias={self.bias is not None}")
 
 
+def fp4_mfma_shared(layers, x: torch.Tensor):
+    """Runs several E2M1 ``QuantLinear`` layers that take the same input x (the q/k/v or
+    gate/up projections of one activation) on the native FP4 path with one split of x per
+    16 rows (fb_mx_split, then fb_gemv_mx_presplit per layer): ``(y_0, y_1, ...)``, each
+    what ``layer(x)`` gives with ``fp4_mfma=True``.  When autograd needs x's gradient each
+    layer runs on its own (the split is not differentiable; every layer's backward is).
+    No counterpart in the reference, whose layers each run their own ``F.linear``."""
+    layers = list(layers)
+    if not layers:
+        return ()
+    K = layers[0].in_features
+    for q in layers:
+        if not isinstance(q, QuantLinear) or q.fmt != "e2m1" or q.fwht_block:
+            raise ValueError("fp4_mfma_shared takes unrotated E2M1 QuantLinear layers")
+        if q.in_features != K:
+            raise ValueError("fp4_mfma_shared: the layers differ in in_features")
+    if x.dim() == 0 or x.shape[-1] != K:
+        raise RuntimeError(f"fp4_mfma_shared: input of shape {tuple(x.shape)} does not end in "
+                           f"in_features={K}")
+    if not x.is_cuda:
+        raise RuntimeError("the packed 4-bit linear runs the HIP kernel: move the modules and "
+                           "input to a ROCm GPU")
+    if torch.is_grad_enabled() and (x.requires_grad or any(
+            q.bias is not None and q.bias.requires_grad for q in layers)):
+        return tuple(packed_linear(q.wdev, q.out_features, K, "e2m1", 0, x, q.bias,
+                                   range_check=q.range_check, f16_exact=q._f16_exact,
+                                   fp4_mfma=True) for q in layers)
+    lead = x.shape[:-1]
+    x2 = x.reshape(-1, K)
+    kp = packed_k(K)
+    xk = _kernel_input(x2, K, "e2m1", 0, False, True, fp4_mfma=True)
+    ydt = x2.dtype if x2.dtype in C.DTYPE_CODE else torch.float32
+    ys = [torch.empty(x2.shape[0], q.out_features, dtype=ydt, device=x.device) for q in layers]
+    with torch.no_grad():
+        for b0 in range(0, xk.shape[0], MAX_GEMV_BATCH):
+            b1 = min(b0 + MAX_GEMV_BATCH, xk.shape[0])
+            sh0 = C.make_shape(layers[0].out_features, kp, b1 - b0, C.FMT_E2M1, 0, C.DT_BF16,
+                               C.DTYPE_CODE[ydt])
+            xs = C.mx_split_raw(xk[b0:b1], sh0)
+            for q, y in zip(layers, ys):
+                sh = C.make_shape(q.out_features, kp, b1 - b0, C.FMT_E2M1, 0, C.DT_BF16,
+                                  C.DTYPE_CODE[ydt])
+                C.gemv_mx_presplit(q.wdev, xs, y[b0:b1], sh)
+        for q, y in zip(layers, ys):
+            if q.bias is not None:
+                y.add_(q.bias.to(y.dtype))
+    return tuple(y.reshape(*lead, q.out_features) for q, y in zip(layers, ys))
+
+
 def quantize_module(module, bitwidth: int = 4, **kw):
     """Recursively swaps every ``nn.Linear`` for a ``QuantLinear`` (reference:
     ``Quantization_Experiments/utils.py:1498-1524``; masks come from existing zero

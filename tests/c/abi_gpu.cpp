@@ -5,7 +5,9 @@
 // rounded as the kernel reads them.  Bound: |err| <= 1e-2 + 1e-3 |ref|, plus half an
 // output ulp for an fp16 y.
 // Cases: GF4, fp16 x, fp32 y, batch 3, N = 300 (the last row tile is partial);
-//        E2M1, bf16 x, fp16 y, batch 16, K = 2048 (the MFMA columns are all live).
+//        E2M1, bf16 x, fp16 y, batch 16, K = 2048 (the MFMA columns are all live);
+//        E2M1, bf16 x, fp32 y, batch 8, on the native FP4 path (fb_gemv_mx, with its
+//        workspace from hipMalloc).
 // Built by if_i_could_turn_back_time_amd/build_lib.py next to libfourbit.so; run by
 // tests/test_gpu.py::test_c_abi_gpu_caller.  Prints one line per case and "ok".
 #include <hip/hip_runtime.h>
@@ -62,7 +64,8 @@ static float from_f16(uint16_t b) {
 }
 
 // Returns the number of outputs outside the bound.
-static int run_case(int fmt, int N, int K, int B, int x_dtype, int y_dtype, hipStream_t st) {
+static int run_case(int fmt, int N, int K, int B, int x_dtype, int y_dtype, hipStream_t st,
+                    bool mx = false) {
   std::mt19937 gen(1234 + fmt * 100 + B);
   std::normal_distribution<float> nd(0.0f, 1.0f);
   std::vector<float> w((size_t)N * K);
@@ -98,13 +101,25 @@ static int run_case(int fmt, int N, int K, int B, int x_dtype, int y_dtype, hipS
   HIP_OK(hipMalloc(&d_y, (size_t)B * N * ysize));
   HIP_OK(hipMemcpyAsync(d_w, stream_bytes.data(), stream_bytes.size(), hipMemcpyHostToDevice, st));
   HIP_OK(hipMemcpyAsync(d_x, xb.data(), xb.size() * 2, hipMemcpyHostToDevice, st));
-  FB_OK_OR_DIE(fb_gemv(d_w, d_x, d_y, &s, nullptr, 0, st));
+  void* d_ws = nullptr;
+  const size_t ws_bytes = mx ? fb_mx_workspace_bytes(&s) : 0;
+  if (mx) {
+    if (!ws_bytes) {
+      std::fprintf(stderr, "fb_mx_workspace_bytes: 0 for this shape\n");
+      std::exit(2);
+    }
+    HIP_OK(hipMalloc(&d_ws, ws_bytes));  // hipMalloc gives 256-byte alignment
+    FB_OK_OR_DIE(fb_gemv_mx(d_w, d_x, d_y, &s, d_ws, ws_bytes, st));
+  } else {
+    FB_OK_OR_DIE(fb_gemv(d_w, d_x, d_y, &s, nullptr, 0, st));
+  }
   std::vector<uint8_t> yb((size_t)B * N * ysize);
   HIP_OK(hipMemcpyAsync(yb.data(), d_y, yb.size(), hipMemcpyDeviceToHost, st));
   HIP_OK(hipStreamSynchronize(st));
   HIP_OK(hipFree(d_w));
   HIP_OK(hipFree(d_x));
   HIP_OK(hipFree(d_y));
+  if (d_ws) HIP_OK(hipFree(d_ws));
 
   int bad = 0;
   double emax = 0.0;
@@ -128,8 +143,8 @@ static int run_case(int fmt, int N, int K, int B, int x_dtype, int y_dtype, hipS
       if (!(err <= bound)) ++bad;
       if (err > emax) emax = err;
     }
-  std::printf("%s N=%d K=%d B=%d: max abs err %.3g, %d outside the bound\n",
-              fmt == FB_FMT_GF4 ? "gf4" : "e2m1", N, K, B, emax, bad);
+  std::printf("%s%s N=%d K=%d B=%d: max abs err %.3g, %d outside the bound\n",
+              fmt == FB_FMT_GF4 ? "gf4" : "e2m1", mx ? " (fp4 mfma)" : "", N, K, B, emax, bad);
   return bad;
 }
 
@@ -144,6 +159,7 @@ int main() {
   HIP_OK(hipStreamCreate(&st));
   int bad = run_case(FB_FMT_GF4, 300, 1024, 3, FB_DT_F16, FB_DT_F32, st);
   bad += run_case(FB_FMT_E2M1, 256, 2048, 16, FB_DT_BF16, FB_DT_F16, st);
+  bad += run_case(FB_FMT_E2M1, 200, 4096, 8, FB_DT_BF16, FB_DT_F32, st, true);
   HIP_OK(hipStreamDestroy(st));
   if (bad) return 1;
   std::printf("ok\n");

@@ -258,7 +258,8 @@ def test_c_abi_gpu_caller():
     """The C ABI from a native C++ caller with no Python or torch (tests/c/abi_gpu.cpp,
     built by build_lib): hipMalloc'd buffers, its own stream, weights packed by the host
     packers, fb_gemv, and y checked against an fp64 host product of the exact decode
-    (GF4 fp16 x batch 3 with a partial row tile; E2M1 bf16 x batch 16)."""
+    (GF4 fp16 x batch 3 with a partial row tile; E2M1 bf16 x batch 16; E2M1 batch 8 on the
+    native FP4 path, fb_gemv_mx, with a hipMalloc'd workspace)."""
     say("native C++ caller")
     exe = Path(__file__).resolve().parent / "c" / "abi_gpu"
     if not exe.exists():  # build() makes it with the library (and fails loudly if it cannot)

@@ -213,3 +213,81 @@ def test_gemv_mx_presplit_equals_gemv_mx(N, K, B):
     sh2 = pw2.shape(B, torch.bfloat16, torch.float32)
     y2 = C.gemv_mx_presplit(pw2.wdev, xs, torch.empty(B, 64, device=DEV), sh2)
     assert torch.equal(y2, pw2.gemv_mx(x, out_dtype=torch.float32))
+
+
+def test_fp4_mfma_shared_matches_each_layer():
+    """Three E2M1 layers on one input (q/k/v-like), one split per 16 rows: each output has
+    the bits of the layer's own fp4_mfma forward; with autograd on x it runs each layer on
+    its own and the gradients are the layers' own."""
+    from if_i_could_turn_back_time_amd import fp4_mfma_shared
+    torch.manual_seed(1)
+    lins = [torch.nn.Linear(1024, n) for n in (512, 256, 256)]
+    qs = [QuantLinear(l, fmt="e2m1", fp4_mfma=True).to(DEV) for l in lins]
+    x = torch.randn(2, 19, 1024, device=DEV).to(torch.bfloat16)  # 38 rows: 3 chunks
+    ys = fp4_mfma_shared(qs, x)
+    for q, y in zip(qs, ys):
+        assert torch.equal(y, q(x))
+    xg = x.clone().requires_grad_(True)
+    outs = fp4_mfma_shared(qs, xg)
+    sum(o.float().sum() for o in outs).backward()
+    xg0 = x.clone().requires_grad_(True)
+    sum(q(xg0).float().sum() for q in qs).backward()
+    assert torch.equal(xg.grad, xg0.grad)
+    with pytest.raises(ValueError):
+        fp4_mfma_shared([qs[0], QuantLinear(torch.nn.Linear(1024, 64), fmt="gf4").to(DEV)], x)
+
+
+def test_gemv_mx_in_hip_graph_replays_match_eager():
+    """fb_gemv_mx captured in a HIP graph (its split and GEMV kernels; the workspace is cached
+    by the PackedWeight before capture, and no memset is recorded): several replays with
+    eager work between them, each equal to the eager result bit for bit."""
+    for N, K, B in ((4096, 2048, 8), (4096, 11008, 16)):
+        say("mx graph", N, K, B)
+        pw, W, _ = _packed(N, K)
+        x = _x_cases(B, K, "plain", 3).to(DEV)
+        y = torch.empty(B, N, dtype=torch.float32, device=DEV)
+        pw.gemv_mx(x, out=y)
+        torch.cuda.synchronize()
+        eager = y.clone()
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.stream(s):
+            pw.gemv_mx(x, out=y)
+            torch.cuda.synchronize()
+            with torch.cuda.graph(graph, stream=s):
+                pw.gemv_mx(x, out=y)
+        torch.cuda.synchronize()
+        for rep in range(4):
+            y.fill_(float("nan"))
+            x2 = (x.float() * 3).to(torch.bfloat16)
+            torch.cuda.synchronize()
+            graph.replay()
+            torch.cuda.synchronize()
+            assert torch.equal(y, eager), (N, K, B, rep)
+            assert x2.shape == x.shape
+
+
+def test_gemv_mx_two_streams_match_serial():
+    """Two layers' fb_gemv_mx calls interleaved on two streams, each layer with its own
+    workspace, give the bits of the same calls one after the other."""
+    g = torch.Generator().manual_seed(5)
+    layers = []
+    for N, K in ((4096, 4096), (3000, 8192)):
+        pw = PackedWeight.quantize(WL.synth_weight("cfg2", N, K, g), "e2m1", device=DEV,
+                                   packer="gpu")
+        xs = [_x_cases(4, K, "plain", 50 + i).to(DEV) for i in range(5)]
+        layers.append((pw, xs))
+    serial = [[pw.gemv_mx(x, out_dtype=torch.float32) for x in xs] for pw, xs in layers]
+    torch.cuda.synchronize()
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+    outs = [[None] * 5 for _ in layers]
+    for i in range(5):
+        for j, ((pw, xs), s) in enumerate(zip(layers, streams)):
+            s.wait_stream(torch.cuda.current_stream())
+            with torch.cuda.stream(s):  # a layer's calls (and its workspace) stay on one stream
+                outs[j][i] = pw.gemv_mx(xs[i], out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    for j in range(2):
+        for i in range(5):
+            assert torch.equal(outs[j][i], serial[j][i]), (j, i)
