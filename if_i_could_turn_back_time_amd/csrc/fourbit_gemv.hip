@@ -806,7 +806,7 @@ template <int FMT, int XDT, int MODE, int NW, int XP>
 __global__ __launch_bounds__(NW * 64) void gemv_kernel(
     const uint8_t* __restrict__ w, const void* __restrict__ x, int K, int Bin, int SPL, int GS,
     int tq, int tr, unsigned spl_m, int S, int fwht_block, int RS, float fwht_scale,
-    void* __restrict__ y, int N, int ydt, const uint8_t* __restrict__ xsc PH_KPARAM) {
+    void* __restrict__ y, int N, int ydt PH_KPARAM) {
   extern __shared__ __align__(16) uint8_t lds[];
   PH_DECL
   PH_MARK(kPhStart);
@@ -939,8 +939,10 @@ __global__ __launch_bounds__(NW * 64) void gemv_kernel(
                                                        kRsrcWord3);
   // MX path: the split's block scales, 8 bytes per (batch row, 128-value group), staged into
   // the pad of each staged group (zeros past K).  Entry i of a slice is row i / nsl, group
-  // k0 / 128 + i % nsl.
+  // k0 / 128 + i % nsl.  They follow the codes in the split's layout, so no argument is
+  // needed for them.
   const int G = K / 128;
+  const uint8_t* xsc = static_cast<const uint8_t*>(x) + mx_scale_offset(Bin, K);
   const rsrc_t srs = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(xsc), (short)0,
                                                        mx ? B * G * 8 : 0, kRsrcWord3);
   auto sc_load = [&](int i, int k0) -> uint2 {
@@ -1321,7 +1323,7 @@ int device_cus() {
 
 template <int FMT, int XDT, int MODE, int NW, int XP>
 int launch_gemv(const void* wdev, const void* x, void* y, const fb_shape_t* s, const Plan& pl,
-                hipStream_t stream, const void* xsc) {
+                hipStream_t stream) {
   auto kern = gemv_kernel<FMT, XDT, MODE, NW, XP>;
   // the LDS limit is a per-device attribute of the kernel: set once on each device
   static std::atomic<uint64_t> attr_set{0};
@@ -1337,57 +1339,56 @@ int launch_gemv(const void* wdev, const void* x, void* y, const fb_shape_t* s, c
   hipLaunchKernelGGL(kern, dim3(pl.grid, pl.P ? pl.P : 1), dim3(NW * 64), pl.lds, stream,
                      static_cast<const uint8_t*>(wdev), x, s->K, s->B, pl.SPL, pl.GS, pl.tq,
                      pl.tr, div_magic(pl.SPL), pl.S, s->fwht_block, x_row_stride(pl.SPL * 4),
-                     fwht_scale(s->fwht_block), y, s->N, s->y_dtype,
-                     static_cast<const uint8_t*>(xsc) PH_KARG((size_t)pl.grid * NW * 64));
+                     fwht_scale(s->fwht_block), y, s->N, s->y_dtype
+                     PH_KARG((size_t)pl.grid * NW * 64));
   return hipGetLastError() == hipSuccess ? FB_OK : FB_ERR_HIP;
 }
 
 template <int FMT, int XDT>
 int launch_mode(int mode, const void* wdev, const void* x, void* y, const fb_shape_t* s,
-                const Plan& pl, hipStream_t stream, const void* xsc) {
+                const Plan& pl, hipStream_t stream) {
   const bool deep = pl.xp == 8;
   if (mode == kSplitK)
-    return deep ? launch_gemv<FMT, XDT, kSplitK, kWaves, 8>(wdev, x, y, s, pl, stream, xsc)
-                : launch_gemv<FMT, XDT, kSplitK, kWaves, 4>(wdev, x, y, s, pl, stream, xsc);
+    return deep ? launch_gemv<FMT, XDT, kSplitK, kWaves, 8>(wdev, x, y, s, pl, stream)
+                : launch_gemv<FMT, XDT, kSplitK, kWaves, 4>(wdev, x, y, s, pl, stream);
   if (mode == kFlat1) {
     if (pl.nw == kWaves / 2)
-      return deep ? launch_gemv<FMT, XDT, kFlat1, kWaves / 2, 8>(wdev, x, y, s, pl, stream, xsc)
-                  : launch_gemv<FMT, XDT, kFlat1, kWaves / 2, 4>(wdev, x, y, s, pl, stream, xsc);
-    return deep ? launch_gemv<FMT, XDT, kFlat1, kWaves, 8>(wdev, x, y, s, pl, stream, xsc)
-                : launch_gemv<FMT, XDT, kFlat1, kWaves, 4>(wdev, x, y, s, pl, stream, xsc);
+      return deep ? launch_gemv<FMT, XDT, kFlat1, kWaves / 2, 8>(wdev, x, y, s, pl, stream)
+                  : launch_gemv<FMT, XDT, kFlat1, kWaves / 2, 4>(wdev, x, y, s, pl, stream);
+    return deep ? launch_gemv<FMT, XDT, kFlat1, kWaves, 8>(wdev, x, y, s, pl, stream)
+                : launch_gemv<FMT, XDT, kFlat1, kWaves, 4>(wdev, x, y, s, pl, stream);
   }
   if (mode == kFlat) {
     if (pl.nw == kWaves / 2)
-      return deep ? launch_gemv<FMT, XDT, kFlat, kWaves / 2, 8>(wdev, x, y, s, pl, stream, xsc)
-                  : launch_gemv<FMT, XDT, kFlat, kWaves / 2, 4>(wdev, x, y, s, pl, stream, xsc);
-    return deep ? launch_gemv<FMT, XDT, kFlat, kWaves, 8>(wdev, x, y, s, pl, stream, xsc)
-                : launch_gemv<FMT, XDT, kFlat, kWaves, 4>(wdev, x, y, s, pl, stream, xsc);
+      return deep ? launch_gemv<FMT, XDT, kFlat, kWaves / 2, 8>(wdev, x, y, s, pl, stream)
+                  : launch_gemv<FMT, XDT, kFlat, kWaves / 2, 4>(wdev, x, y, s, pl, stream);
+    return deep ? launch_gemv<FMT, XDT, kFlat, kWaves, 8>(wdev, x, y, s, pl, stream)
+                : launch_gemv<FMT, XDT, kFlat, kWaves, 4>(wdev, x, y, s, pl, stream);
   }
   if (mode == kSliced)
-    return deep ? launch_gemv<FMT, XDT, kSliced, kWaves, 8>(wdev, x, y, s, pl, stream, xsc)
-                : launch_gemv<FMT, XDT, kSliced, kWaves, 4>(wdev, x, y, s, pl, stream, xsc);
+    return deep ? launch_gemv<FMT, XDT, kSliced, kWaves, 8>(wdev, x, y, s, pl, stream)
+                : launch_gemv<FMT, XDT, kSliced, kWaves, 4>(wdev, x, y, s, pl, stream);
   if constexpr (FMT == kFmtMx) {
     return FB_ERR_FWHT;  // the split is of unrotated x
   } else {
     // the rotation preloads kXPre 256-value sub-blocks per wave instead
-    if (mode == kRot1) return launch_gemv<FMT, XDT, kRot1, kWaves, 4>(wdev, x, y, s, pl, stream, xsc);
-    return launch_gemv<FMT, XDT, kRotated, kWaves, 4>(wdev, x, y, s, pl, stream, xsc);
+    if (mode == kRot1) return launch_gemv<FMT, XDT, kRot1, kWaves, 4>(wdev, x, y, s, pl, stream);
+    return launch_gemv<FMT, XDT, kRotated, kWaves, 4>(wdev, x, y, s, pl, stream);
   }
 }
 
 int launch_plan(const void* wdev, const void* x, void* y, const fb_shape_t* s, const Plan& pl,
-                hipStream_t hs, const void* xsc = nullptr) {
+                hipStream_t hs) {
   const int mode = s->fwht_block ? (s->B == 1 && pl.S == 1 ? kRot1 : kRotated)
                    : pl.P         ? kSplitK
                    : pl.S > 1     ? kSliced
                    : s->B == 1    ? kFlat1
                                   : kFlat;
-  if (s->fmt == FB_FMT_GF4)
-    return launch_mode<FB_FMT_GF4, FB_DT_F16>(mode, wdev, x, y, s, pl, hs, xsc);
-  if (s->fmt == kFmtMx) return launch_mode<kFmtMx, FB_DT_BF16>(mode, wdev, x, y, s, pl, hs, xsc);
+  if (s->fmt == FB_FMT_GF4) return launch_mode<FB_FMT_GF4, FB_DT_F16>(mode, wdev, x, y, s, pl, hs);
+  if (s->fmt == kFmtMx) return launch_mode<kFmtMx, FB_DT_BF16>(mode, wdev, x, y, s, pl, hs);
   if (s->x_dtype == FB_DT_BF16)
-    return launch_mode<FB_FMT_E2M1, FB_DT_BF16>(mode, wdev, x, y, s, pl, hs, xsc);
-  return launch_mode<FB_FMT_E2M1, FB_DT_F16>(mode, wdev, x, y, s, pl, hs, xsc);
+    return launch_mode<FB_FMT_E2M1, FB_DT_BF16>(mode, wdev, x, y, s, pl, hs);
+  return launch_mode<FB_FMT_E2M1, FB_DT_F16>(mode, wdev, x, y, s, pl, hs);
 }
 
 // Rotated calls with at least this many activation values (B * K) rotate x once
@@ -1414,20 +1415,23 @@ int launch_rotate(const void* x, void* xo, const fb_shape_t* s, hipStream_t hs) 
 
 // The GEMV of a validated shape: one launch when a plan fits LDS, else row chunks.
 int gemv_planned(const void* wdev, const void* x, void* y, const fb_shape_t* s, int cus,
-                 hipStream_t hs, void* ws, size_t ws_bytes, const uint8_t* xsc = nullptr) {
+                 hipStream_t hs, void* ws, size_t ws_bytes) {
   Plan pl;
   // batch 8-16 on layers of few row tiles: the K-parts side by side, through the workspace
   if (ws && splitk_parts(s, cus, &pl) && ws_bytes >= splitk_bytes(s, pl.P)) {
     fb_shape_t sp = *s;
     sp.y_dtype = FB_DT_F32;  // the parts' sums
-    const int st = launch_plan(wdev, x, ws, &sp, pl, hs, xsc);
+    const int st = launch_plan(wdev, x, ws, &sp, pl, hs);
     if (st != FB_OK) return st;
     const int64_t n = (int64_t)s->B * s->N;
     hipLaunchKernelGGL(splitk_sum, dim3((unsigned)((n + 1023) / 1024)), dim3(256), 0, hs,
                        static_cast<const float*>(ws), pl.P, n, y, s->y_dtype);
     return hipGetLastError() == hipSuccess ? FB_OK : FB_ERR_HIP;
   }
-  if (make_plan(s, cus, pl)) return launch_plan(wdev, x, y, s, pl, hs, xsc);
+  if (make_plan(s, cus, pl)) return launch_plan(wdev, x, y, s, pl, hs);
+  // (an unrotated batch always has a plan: one span per slice fits LDS; the MX kernels find
+  // their scales after the whole split, which row chunks would not keep)
+  if (s->fmt == kFmtMx) return FB_ERR_LDS;
   // No plan holds the whole batch in LDS (a 4096-wide rotation keeps an fp32 copy of every
   // batch row): the rows run in the largest chunks that fit, each streaming the weights.
   fb_shape_t sc = *s;
@@ -1442,8 +1446,7 @@ int gemv_planned(const void* wdev, const void* x, void* y, const fb_shape_t* s, 
     sc.B = std::min(bc, s->B - b0);
     if (!make_plan(&sc, cus, pl)) return FB_ERR_LDS;
     const int st = launch_plan(wdev, static_cast<const uint8_t*>(x) + (size_t)b0 * s->K * 2,
-                               static_cast<uint8_t*>(y) + (size_t)b0 * s->N * ysize, &sc, pl, hs,
-                               xsc ? xsc + (size_t)b0 * (s->K / 128) * 8 : nullptr);
+                               static_cast<uint8_t*>(y) + (size_t)b0 * s->N * ysize, &sc, pl, hs);
     if (st != FB_OK) return st;
   }
   return FB_OK;
@@ -1522,8 +1525,7 @@ int gemv_mx_split_run(const void* wdev, const void* xs, void* y, const fb_shape_
                       void* ws, size_t ws_bytes, hipStream_t hs) {
   fb_shape_t u = *s;
   u.fmt = kFmtMx;
-  const uint8_t* x8 = static_cast<const uint8_t*>(xs);
-  return gemv_planned(wdev, x8, y, &u, cus, hs, ws, ws_bytes, x8 + mx_scale_offset(s->B, s->K));
+  return gemv_planned(wdev, xs, y, &u, cus, hs, ws, ws_bytes);
 }
 
 // fb_gemv_mx behind the ABI: the split into the workspace's head, then the GEMV on it (with
