@@ -1070,15 +1070,33 @@ __global__ __launch_bounds__(NW * 64) void gemv_kernel(
 // ---------------------------------------------------------------------------------
 // The split-K sum: y[i] = ((part_0[i] + part_1[i]) + ...) + part_{P-1}[i], fp32, in part
 // order whichever workgroup finished first; four outputs per thread, 16-byte reads where
-// the batch-by-rows count allows.
-__global__ __launch_bounds__(256) void splitk_sum(const float* __restrict__ part, int P,
-                                                  int64_t n, void* __restrict__ y, int ydt) {
+// the batch-by-rows count allows.  P (2, 4 or 8) is a template argument so that the P reads
+// of a thread are issued back to back before the first add waits for them.
+template <int P>
+__global__ __launch_bounds__(256) void splitk_sum(const float* __restrict__ part, int64_t n,
+                                                  void* __restrict__ y, int ydt) {
   const int64_t i0 = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4;
   if (i0 >= n) return;
   if (i0 + 4 <= n && (n & 3) == 0) {
-    f32x4 a = *reinterpret_cast<const f32x4*>(part + i0);
-    for (int p = 1; p < P; ++p) a += *reinterpret_cast<const f32x4*>(part + (int64_t)p * n + i0);
-    for (int j = 0; j < 4; ++j) store_y(y, i0 + j, a[j], ydt);
+    f32x4 v[P];
+#pragma unroll
+    for (int p = 0; p < P; ++p)
+      v[p] = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(part + (int64_t)p * n + i0));
+    f32x4 a = v[0];
+#pragma unroll
+    for (int p = 1; p < P; ++p) a += v[p];
+    if (ydt == FB_DT_F32) {
+      *reinterpret_cast<f32x4*>(static_cast<float*>(y) + i0) = a;
+    } else {  // two 4-byte stores: y is only known to be 4-byte aligned
+      unsigned h[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        h[j] = ydt == FB_DT_F16 ? __builtin_bit_cast(unsigned short, (_Float16)a[j])
+                                : __builtin_bit_cast(unsigned short, (__bf16)a[j]);
+      unsigned* yo = reinterpret_cast<unsigned*>(static_cast<uint16_t*>(y) + i0);
+      yo[0] = h[0] | (h[1] << 16);
+      yo[1] = h[2] | (h[3] << 16);
+    }
   } else {
     for (int64_t i = i0; i < min(n, i0 + 4); ++i) {
       float a = part[i];
@@ -1424,8 +1442,14 @@ int gemv_planned(const void* wdev, const void* x, void* y, const fb_shape_t* s, 
     const int st = launch_plan(wdev, x, ws, &sp, pl, hs);
     if (st != FB_OK) return st;
     const int64_t n = (int64_t)s->B * s->N;
-    hipLaunchKernelGGL(splitk_sum, dim3((unsigned)((n + 1023) / 1024)), dim3(256), 0, hs,
-                       static_cast<const float*>(ws), pl.P, n, y, s->y_dtype);
+    const dim3 grid((unsigned)((n + 1023) / 1024));
+    const float* part = static_cast<const float*>(ws);
+    if (pl.P == 2)
+      hipLaunchKernelGGL(splitk_sum<2>, grid, dim3(256), 0, hs, part, n, y, s->y_dtype);
+    else if (pl.P == 4)
+      hipLaunchKernelGGL(splitk_sum<4>, grid, dim3(256), 0, hs, part, n, y, s->y_dtype);
+    else
+      hipLaunchKernelGGL(splitk_sum<8>, grid, dim3(256), 0, hs, part, n, y, s->y_dtype);
     return hipGetLastError() == hipSuccess ? FB_OK : FB_ERR_HIP;
   }
   if (make_plan(s, cus, pl)) return launch_plan(wdev, x, y, s, pl, hs);
