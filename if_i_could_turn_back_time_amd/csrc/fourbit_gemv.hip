@@ -1070,7 +1070,7 @@ __global__ __launch_bounds__(NW * 64) void gemv_kernel(
 // ---------------------------------------------------------------------------------
 // The split-K sum: y[i] = ((part_0[i] + part_1[i]) + ...) + part_{P-1}[i], fp32, in part
 // order whichever workgroup finished first; four outputs per thread, 16-byte reads where
-// the batch-by-rows count allows.  P (2, 4 or 8) is a template argument so that the P reads
+// the batch-by-rows count allows.  P (4 or 8) is a template argument so that the P reads
 // of a thread are issued back to back before the first add waits for them.
 template <int P>
 __global__ __launch_bounds__(256) void splitk_sum(const float* __restrict__ part, int64_t n,
@@ -1444,9 +1444,9 @@ int gemv_planned(const void* wdev, const void* x, void* y, const fb_shape_t* s, 
     const int64_t n = (int64_t)s->B * s->N;
     const dim3 grid((unsigned)((n + 1023) / 1024));
     const float* part = static_cast<const float*>(ws);
-    if (pl.P == 2)
-      hipLaunchKernelGGL(splitk_sum<2>, grid, dim3(256), 0, hs, part, n, y, s->y_dtype);
-    else if (pl.P == 4)
+    // P is 4 or 8: splitk_parts takes the sliced plan's slice count (3 or more) rounded up
+    // to a power of two, at most 8
+    if (pl.P == 4)
       hipLaunchKernelGGL(splitk_sum<4>, grid, dim3(256), 0, hs, part, n, y, s->y_dtype);
     else
       hipLaunchKernelGGL(splitk_sum<8>, grid, dim3(256), 0, hs, part, n, y, s->y_dtype);

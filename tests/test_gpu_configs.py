@@ -293,17 +293,23 @@ def test_rotated_batch_with_and_without_workspace(N, K, B, block):
     assert ok, emax
 
 
-@pytest.mark.parametrize("fmt,N,ydt", [("gf4", 4096, torch.float16), ("e2m1", 4096, torch.bfloat16),
-                                       ("gf4", 1000, torch.float32), ("e2m1", 72, torch.float16)])
-def test_splitk_against_slices_and_oracle(fmt, N, ydt):
+@pytest.mark.parametrize("fmt,N,ydt,K", [("gf4", 4096, torch.float16, 11008),
+                                         ("e2m1", 4096, torch.bfloat16, 11008),
+                                         ("gf4", 1000, torch.float32, 11008),
+                                         ("e2m1", 72, torch.float16, 11008),
+                                         ("gf4", 200, torch.bfloat16, 28672),
+                                         ("e2m1", 512, torch.float32, 28672)])
+def test_splitk_against_slices_and_oracle(fmt, N, ydt, K):
     """Batch 16 at K = 11008 (22 spans: parts of 6, 6, 6 and 4) runs its K-parts side by side
-    through the workspace and adds their fp32 sums in part order: within tolerance of the
-    sliced plan (no workspace) and of the device-decoded weight x fp32 torch on all rows,
-    the same bits on a second call (the last part sums only its own spans), and sampled rows
-    against the oracle's exact decode.  The reference's batched product it replaces is
+    through the workspace and adds their fp32 sums in part order; at K = 28672 (56 spans,
+    x of 917 KB in 6 slices) in eight parts of 7.  Checked: within tolerance of the sliced
+    plan (no workspace) and of the device-decoded weight x fp32 torch on all rows, the same
+    bits on a second call (the last part sums only its own spans), and sampled rows against
+    the oracle's exact decode.  The reference's batched product it replaces is
     layers.h:9828-9839 / layers.py:36-38."""
     import ctypes
-    K, B = 11008, 16
+    B = 16
+    P = 4 if K == 11008 else 8
     say("split-K", fmt, N, K, B, ydt)
     g = torch.Generator().manual_seed(N + 7)
     w = torch.randn(N, K, generator=g) * 0.02
@@ -312,7 +318,7 @@ def test_splitk_against_slices_and_oracle(fmt, N, ydt):
     x = (torch.randn(B, K, generator=g) * 0.5).to(xdt).to(DEV)
     shape = pw.shape(B, xdt, ydt)
     need = C.workspace_bytes(shape)
-    assert need == 4 * B * N * 4   # four parts
+    assert need == P * B * N * 4   # the parts' fp32 sums
     ws = torch.full((need,), 0xFF, dtype=torch.uint8, device=DEV)   # no zero-fill needed
     L = C.lib()
     sp = torch.cuda.current_stream().cuda_stream
