@@ -65,20 +65,26 @@ def build(verbose: bool = False) -> Path:
     inc = [f"-I{INCLUDE}", f"-I{CSRC}"]
     host_o = BUILD / "fourbit_host.o"
     gemv_o = BUILD / "fourbit_gemv.o"
+    ilp_o = BUILD / "fourbit_gemv_ilp.o"
     pack_o = BUILD / "fourbit_pack.o"
     jenks2_o = BUILD / "fourbit_jenks2.o"
     trace_o = BUILD / "fourbit_gemv_trace.o"
     steps = [
         ["g++", *HOST_FLAGS, *inc, "-c", str(CSRC / "fourbit_host.cpp"), "-o", str(host_o)],
         [_hipcc(), *HIP_FLAGS, *inc, "-c", str(CSRC / "fourbit_gemv.hip"), "-o", str(gemv_o)],
+        # the batch-1 rotated and the 8-wave short-preload batch-1 kernels: max-ILP scheduling
+        # (measured faster for them, and slower for the large layers' kernels)
+        [_hipcc(), *HIP_FLAGS, "-mllvm", "-amdgpu-sched-strategy=max-ilp", *inc, "-c",
+         str(CSRC / "fourbit_gemv_ilp.hip"), "-o", str(ilp_o)],
         # the GPU packer must round every fp64 operation as the host packer does
         [_hipcc(), *HIP_FLAGS, "-ffp-contract=off", *inc, "-c", str(CSRC / "fourbit_pack.hip"),
          "-o", str(pack_o)],
         # the two-class Jenks rounds every fp64 operation as its host twin does
         [_hipcc(), *HIP_FLAGS, "-ffp-contract=off", *inc, "-c", str(CSRC / "fourbit_jenks2.hip"),
          "-o", str(jenks2_o)],
-        [_hipcc(), *HIP_FLAGS, "-DFB_PHASE_TRACE", *inc, "-c", str(CSRC / "fourbit_gemv.hip"),
-         "-o", str(trace_o)],
+        # the diagnostic build keeps every kernel in one unit, default scheduling
+        [_hipcc(), *HIP_FLAGS, "-DFB_PHASE_TRACE", "-DFB_GEMV_ONE_TU", *inc, "-c",
+         str(CSRC / "fourbit_gemv.hip"), "-o", str(trace_o)],
     ]
     for cmd in steps:
         if verbose:
@@ -87,10 +93,10 @@ def build(verbose: bool = False) -> Path:
     with ThreadPoolExecutor(max_workers=len(steps)) as ex:
         for f in [ex.submit(_run, cmd) for cmd in steps]:
             f.result()
-    for lib, kern_o in ((LIB, gemv_o), (TRACE_LIB, trace_o)):
+    for lib, kern_os in ((LIB, (gemv_o, ilp_o)), (TRACE_LIB, (trace_o,))):
         tmp = lib.with_suffix(".so.tmp")
-        link = [_hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", str(host_o), str(kern_o),
-                str(pack_o), str(jenks2_o), "-o", str(tmp), "-lpthread"]
+        link = [_hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", str(host_o),
+                *map(str, kern_os), str(pack_o), str(jenks2_o), "-o", str(tmp), "-lpthread"]
         if verbose:
             print(" ".join(link), flush=True)
         _run(link)

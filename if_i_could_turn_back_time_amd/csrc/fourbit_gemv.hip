@@ -28,6 +28,21 @@
 #include "fourbit.h"
 #include "fourbit_layout.h"
 
+// The library's GEMV is two translation units.  fourbit_gemv_ilp.hip includes this file with
+// FB_GEMV_ILP_TU defined and is compiled with the compiler's max-ILP instruction scheduling;
+// it holds copies of two kernels that run faster that way, the batch-1 rotated one (kRot1)
+// and the 8-wave batch-1 one with the short x preload (kFlat1, used there only where each
+// workgroup has a CU to itself), and fb_ilp::launch starts them.  Every other kernel (the
+// large batch-1 layers among them, which are 1-2 us slower with that scheduling) stays here.
+// FB_GEMV_ONE_TU keeps all of them in this unit (the diagnostic build).
+namespace fb_ilp {
+// A plan's fields are passed one by one: the plan type is local to each unit.  Not part of
+// the library's ABI.
+__attribute__((visibility("hidden"))) int launch(int fmt, int xdt, int mode, const void* wdev, const void* x, void* y,
+           const fb_shape_t* s, int grid, int SPL, int GS, int tq, int tr, int S, size_t lds,
+           hipStream_t stream);
+}  // namespace fb_ilp
+
 namespace {
 
 typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
@@ -1231,6 +1246,7 @@ struct Plan {
   int xp = 4;    // x chunks each thread preloads per slice: 4, or 8 for larger slices
   size_t lds = 0;
   int P = 0;     // kSplitK: K-parts run side by side (grid grid x P); 0: slices in turn
+  bool cu_shared = false;  // two 8-wave workgroups per CU (more workgroups than CUs)
 };
 
 // The rotation's normalisation 1 / sqrt(b), rounded as fp32 (correctly rounded sqrt and
@@ -1282,6 +1298,7 @@ bool make_plan(const fb_shape_t* s, int cus, Plan& pl) {
       pl.nw = nw;
       pl.xp = (s->B * SPL + nw - 1) / nw <= 4 ? 4 : 8;  // 16-byte chunks per thread
       pl.lds = lds;
+      pl.cu_shared = grid > cus;
       return true;
     }
   }
@@ -1362,10 +1379,27 @@ int launch_gemv(const void* wdev, const void* x, void* y, const fb_shape_t* s, c
   return hipGetLastError() == hipSuccess ? FB_OK : FB_ERR_HIP;
 }
 
+// Whether fb_ilp::launch starts the batch-1 rotated kernel and the 8-wave batch-1 kernel with
+// the short x preload (instantiated in the max-ILP unit, not here).
+#if !defined(FB_GEMV_ONE_TU) && !defined(FB_GEMV_ILP_TU)
+constexpr bool kIlpSplit = true;
+#else
+constexpr bool kIlpSplit = false;
+#endif
+
 template <int FMT, int XDT>
 int launch_mode(int mode, const void* wdev, const void* x, void* y, const fb_shape_t* s,
                 const Plan& pl, hipStream_t stream) {
   const bool deep = pl.xp == 8;
+  constexpr bool ilp = kIlpSplit && FMT != kFmtMx;
+  // the max-ILP copies: the rotated batch-1 kernel, and the 8-wave short-preload batch-1 one
+  // where each workgroup has a CU to itself (with two per CU that copy was 0.9-1.4 us slower:
+  // GF4 8192^2, 4096 -> 11008, 4096 -> 14336)
+  if constexpr (ilp) {
+    if (mode == kRot1 || (mode == kFlat1 && pl.nw == kWaves / 2 && !deep && !pl.cu_shared))
+      return fb_ilp::launch(FMT, XDT, mode, wdev, x, y, s, pl.grid, pl.SPL, pl.GS, pl.tq, pl.tr,
+                            pl.S, pl.lds, stream);
+  }
   if (mode == kSplitK)
     return deep ? launch_gemv<FMT, XDT, kSplitK, kWaves, 8>(wdev, x, y, s, pl, stream)
                 : launch_gemv<FMT, XDT, kSplitK, kWaves, 4>(wdev, x, y, s, pl, stream);
@@ -1390,7 +1424,10 @@ int launch_mode(int mode, const void* wdev, const void* x, void* y, const fb_sha
     return FB_ERR_FWHT;  // the split is of unrotated x
   } else {
     // the rotation preloads kXPre 256-value sub-blocks per wave instead
-    if (mode == kRot1) return launch_gemv<FMT, XDT, kRot1, kWaves, 4>(wdev, x, y, s, pl, stream);
+    if (mode == kRot1) {
+      if constexpr (!ilp) return launch_gemv<FMT, XDT, kRot1, kWaves, 4>(wdev, x, y, s, pl, stream);
+      return FB_ERR_HIP;  // not reached: started by fb_ilp::launch above
+    }
     return launch_gemv<FMT, XDT, kRotated, kWaves, 4>(wdev, x, y, s, pl, stream);
   }
 }
@@ -1571,6 +1608,7 @@ int gemv_mx_impl(const void* wdev, const void* x, void* y, const fb_shape_t* s, 
   return gemv_mx_split_run(wdev, w8, y, s, cus, w8 + need, ws_bytes - need, hs);
 }
 
+#ifndef FB_GEMV_ILP_TU
 // Scratch of the allocation-free entry point: a file-scope device array (one per GPU the
 // library runs on, alive until the process ends).  Host code never uses the array's name as
 // an address: the device address comes from hipGetSymbolAddress, once per device.
@@ -1588,8 +1626,40 @@ void* scratch_ptr(int dev) {
   g_scratch[dev].store(q, std::memory_order_release);
   return q;
 }
+#endif  // FB_GEMV_ILP_TU
 
 }  // namespace
+
+#ifdef FB_GEMV_ILP_TU
+namespace fb_ilp {
+int launch(int fmt, int xdt, int mode, const void* wdev, const void* x, void* y,
+           const fb_shape_t* s, int grid, int SPL, int GS, int tq, int tr, int S, size_t lds,
+           hipStream_t stream) {
+  Plan pl;
+  pl.grid = grid;
+  pl.SPL = SPL;
+  pl.GS = GS;
+  pl.tq = tq;
+  pl.tr = tr;
+  pl.S = S;
+  pl.lds = lds;
+  pl.xp = 4;
+  if (mode == kRot1) {  // a rotation takes fp16 x
+    pl.nw = kWaves;
+    if (xdt != FB_DT_F16) return FB_ERR_DTYPE;
+    return fmt == FB_FMT_GF4
+               ? launch_gemv<FB_FMT_GF4, FB_DT_F16, kRot1, kWaves, 4>(wdev, x, y, s, pl, stream)
+               : launch_gemv<FB_FMT_E2M1, FB_DT_F16, kRot1, kWaves, 4>(wdev, x, y, s, pl, stream);
+  }
+  pl.nw = kWaves / 2;  // kFlat1: GF4 with fp16 x, E2M1 with fp16 or bf16 x
+  if (fmt == FB_FMT_GF4)
+    return launch_gemv<FB_FMT_GF4, FB_DT_F16, kFlat1, kWaves / 2, 4>(wdev, x, y, s, pl, stream);
+  if (xdt == FB_DT_BF16)
+    return launch_gemv<FB_FMT_E2M1, FB_DT_BF16, kFlat1, kWaves / 2, 4>(wdev, x, y, s, pl, stream);
+  return launch_gemv<FB_FMT_E2M1, FB_DT_F16, kFlat1, kWaves / 2, 4>(wdev, x, y, s, pl, stream);
+}
+}  // namespace fb_ilp
+#else
 
 extern "C" {
 
@@ -1719,3 +1789,4 @@ int fb_phase_plan(const fb_shape_t* s, int* grid, int* waves, int* slices, int* 
 #endif
 
 }  // extern "C"
+#endif  // FB_GEMV_ILP_TU
