@@ -69,6 +69,7 @@ def build(verbose: bool = False) -> Path:
     pack_o = BUILD / "fourbit_pack.o"
     jenks2_o = BUILD / "fourbit_jenks2.o"
     trace_o = BUILD / "fourbit_gemv_trace.o"
+    trace_ilp_o = BUILD / "fourbit_gemv_ilp_trace.o"
     steps = [
         ["g++", *HOST_FLAGS, *inc, "-c", str(CSRC / "fourbit_host.cpp"), "-o", str(host_o)],
         [_hipcc(), *HIP_FLAGS, *inc, "-c", str(CSRC / "fourbit_gemv.hip"), "-o", str(gemv_o)],
@@ -82,9 +83,10 @@ def build(verbose: bool = False) -> Path:
         # the two-class Jenks rounds every fp64 operation as its host twin does
         [_hipcc(), *HIP_FLAGS, "-ffp-contract=off", *inc, "-c", str(CSRC / "fourbit_jenks2.hip"),
          "-o", str(jenks2_o)],
-        # the diagnostic build keeps every kernel in one unit, default scheduling
-        [_hipcc(), *HIP_FLAGS, "-DFB_PHASE_TRACE", "-DFB_GEMV_ONE_TU", *inc, "-c",
-         str(CSRC / "fourbit_gemv.hip"), "-o", str(trace_o)],
+        [_hipcc(), *HIP_FLAGS, "-DFB_PHASE_TRACE", *inc, "-c", str(CSRC / "fourbit_gemv.hip"),
+         "-o", str(trace_o)],
+        [_hipcc(), *HIP_FLAGS, "-mllvm", "-amdgpu-sched-strategy=max-ilp", "-DFB_PHASE_TRACE",
+         *inc, "-c", str(CSRC / "fourbit_gemv_ilp.hip"), "-o", str(trace_ilp_o)],
     ]
     for cmd in steps:
         if verbose:
@@ -93,7 +95,7 @@ def build(verbose: bool = False) -> Path:
     with ThreadPoolExecutor(max_workers=len(steps)) as ex:
         for f in [ex.submit(_run, cmd) for cmd in steps]:
             f.result()
-    for lib, kern_os in ((LIB, (gemv_o, ilp_o)), (TRACE_LIB, (trace_o,))):
+    for lib, kern_os in ((LIB, (gemv_o, ilp_o)), (TRACE_LIB, (trace_o, trace_ilp_o))):
         tmp = lib.with_suffix(".so.tmp")
         link = [_hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", str(host_o),
                 *map(str, kern_os), str(pack_o), str(jenks2_o), "-o", str(tmp), "-lpthread"]

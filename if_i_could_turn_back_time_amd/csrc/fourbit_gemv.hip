@@ -30,17 +30,16 @@
 
 // The library's GEMV is two translation units.  fourbit_gemv_ilp.hip includes this file with
 // FB_GEMV_ILP_TU defined and is compiled with the compiler's max-ILP instruction scheduling;
-// it holds copies of two kernels that run faster that way, the batch-1 rotated one (kRot1)
-// and the 8-wave batch-1 one with the short x preload (kFlat1, used there only where each
-// workgroup has a CU to itself), and fb_ilp::launch starts them.  Every other kernel (the
-// large batch-1 layers among them, which are 1-2 us slower with that scheduling) stays here.
-// FB_GEMV_ONE_TU keeps all of them in this unit (the diagnostic build).
+// it holds the kernels that run faster that way, the batch-1 rotated one (kRot1) and the
+// 8-wave batch-1 one (kFlat1, one workgroup per CU), and fb_ilp::launch starts them.  Every
+// other kernel stays here: with max-ILP scheduling the 16-wave batch-1 kernel ran the large
+// layers 1.4-1.8 us slower.
 namespace fb_ilp {
 // A plan's fields are passed one by one: the plan type is local to each unit.  Not part of
 // the library's ABI.
 __attribute__((visibility("hidden"))) int launch(int fmt, int xdt, int mode, const void* wdev, const void* x, void* y,
            const fb_shape_t* s, int grid, int SPL, int GS, int tq, int tr, int S, size_t lds,
-           hipStream_t stream);
+           bool xp8, hipStream_t stream);
 }  // namespace fb_ilp
 
 namespace {
@@ -316,9 +315,21 @@ struct Phases {
     if (buf) buf[i] = ((unsigned long long)hi << 32) | lo;
   }
 };
-// Host side: the buffer the next launches write to (fb_phase_trace_set), and its size.
-unsigned long long* g_phase_host = nullptr;
-size_t g_phase_entries = 0;
+}  // namespace
+// Host side: the buffer the next launches write to (fb_phase_trace_set), and its size; one
+// copy for both units of the diagnostic library.
+namespace fb_trace {
+#ifdef FB_GEMV_ILP_TU
+extern unsigned long long* g_phase_host;
+extern size_t g_phase_entries;
+#else
+__attribute__((visibility("hidden"))) unsigned long long* g_phase_host = nullptr;
+__attribute__((visibility("hidden"))) size_t g_phase_entries = 0;
+#endif
+}  // namespace fb_trace
+using fb_trace::g_phase_entries;
+using fb_trace::g_phase_host;
+namespace {
 // The marks are macros so that the product build's code is exactly what it is without them.
 #define PH_DECL Phases ph;
 #define PH_PARAM , Phases& ph
@@ -1246,7 +1257,6 @@ struct Plan {
   int xp = 4;    // x chunks each thread preloads per slice: 4, or 8 for larger slices
   size_t lds = 0;
   int P = 0;     // kSplitK: K-parts run side by side (grid grid x P); 0: slices in turn
-  bool cu_shared = false;  // two 8-wave workgroups per CU (more workgroups than CUs)
 };
 
 // The rotation's normalisation 1 / sqrt(b), rounded as fp32 (correctly rounded sqrt and
@@ -1264,20 +1274,25 @@ size_t plan_lds(const fb_shape_t* s, int tpw, int SPL) {
          (s->B == 1 ? (size_t)((tpw * 4 + 15) & ~15) : 0) + 16 + zero_bytes(s->fmt);
 }
 
-// The fewest K-slices whose LDS fits.  One 16-wave workgroup per CU (up to the number of
-// row tiles), or, for unrotated batch-1 layers with few row tiles per CU (GF4 at most 4,
-// E2M1 at most 2) and LDS that fits twice in a CU, two 8-wave workgroups per CU (measured
-// 0.3-1.4 us faster there; slower on larger layers, at batch 2 and 4, and with a rotation,
-// which each workgroup would then compute with half the waves).
+// The fewest K-slices whose LDS fits.
+// - Unrotated batch-1 GF4 / E2M1 layers whose x fits one slice: one 8-wave workgroup per CU
+//   (up to the number of row tiles), run by the max-ILP copy of the kernel, which holds 183
+//   VGPRs (GF4) so that only one such workgroup fits a CU.  Measured against 16 waves with
+//   the default scheduling, same box, median us: GF4 8192 -> 28672 29.79 -> 28.93,
+//   28672 -> 8192 30.16 -> 29.31, 4096 -> 28672 17.47 -> 16.55, 4096 -> 14336 10.80 -> 9.96,
+//   4096 -> 11008 8.77 -> 8.19; E2M1 8192 -> 28672 20.58 -> 20.28; the rest within 0.1.
+// - The native FP4 path's batch-1 layers with few row tiles per CU (at most 2) and LDS that
+//   fits twice in a CU: two 8-wave workgroups per CU.
+// - Otherwise one 16-wave workgroup per CU.
 bool make_plan(const fb_shape_t* s, int cus, Plan& pl) {
   const int GS = (s->K / 128 + 3) / 4;
   const int T = (s->N + 15) / 16;
-  const int half_tiles = (s->fmt == FB_FMT_GF4 ? 4 : 2) * cus;
-  const bool half = !s->fwht_block && s->B == 1 && T <= half_tiles;
+  const bool one8 = !s->fwht_block && s->B == 1 && s->fmt != kFmtMx;
+  const bool half = one8 || (!s->fwht_block && s->B == 1 && T <= 2 * cus);
   for (int pass = half ? 0 : 1; pass < 2; ++pass) {
     const int nw = pass == 0 ? kWaves / 2 : kWaves;
-    const size_t limit = pass == 0 ? (size_t)kLdsLimit / 2 : (size_t)kLdsLimit;
-    const int grid = std::max(1, std::min(T, pass == 0 ? 2 * cus : cus));
+    const size_t limit = pass == 0 && !one8 ? (size_t)kLdsLimit / 2 : (size_t)kLdsLimit;
+    const int grid = std::max(1, std::min(T, pass == 0 && !one8 ? 2 * cus : cus));
     const int tpw = (T + grid - 1) / grid;  // most tiles a workgroup owns
     for (int S = 1; S <= GS; ++S) {
       int SPL = (GS + S - 1) / S;  // spans per slice; the last slice may have fewer
@@ -1286,7 +1301,7 @@ bool make_plan(const fb_shape_t* s, int cus, Plan& pl) {
         SPL = (SPL + bs - 1) / bs * bs;
       }
       if ((S - 1) * SPL >= GS) continue;  // the last slice would have no span
-      if (pass == 0 && S > 1) break;  // two workgroups per CU only with one K-slice
+      if (pass == 0 && S > 1) break;  // 8-wave workgroups only with one K-slice
       const size_t lds = plan_lds(s, tpw, SPL);
       if (lds > limit) continue;
       pl.S = S;
@@ -1298,7 +1313,6 @@ bool make_plan(const fb_shape_t* s, int cus, Plan& pl) {
       pl.nw = nw;
       pl.xp = (s->B * SPL + nw - 1) / nw <= 4 ? 4 : 8;  // 16-byte chunks per thread
       pl.lds = lds;
-      pl.cu_shared = grid > cus;
       return true;
     }
   }
@@ -1381,7 +1395,7 @@ int launch_gemv(const void* wdev, const void* x, void* y, const fb_shape_t* s, c
 
 // Whether fb_ilp::launch starts the batch-1 rotated kernel and the 8-wave batch-1 kernel with
 // the short x preload (instantiated in the max-ILP unit, not here).
-#if !defined(FB_GEMV_ONE_TU) && !defined(FB_GEMV_ILP_TU)
+#ifndef FB_GEMV_ILP_TU
 constexpr bool kIlpSplit = true;
 #else
 constexpr bool kIlpSplit = false;
@@ -1392,21 +1406,23 @@ int launch_mode(int mode, const void* wdev, const void* x, void* y, const fb_sha
                 const Plan& pl, hipStream_t stream) {
   const bool deep = pl.xp == 8;
   constexpr bool ilp = kIlpSplit && FMT != kFmtMx;
-  // the max-ILP copies: the rotated batch-1 kernel, and the 8-wave short-preload batch-1 one
-  // where each workgroup has a CU to itself (with two per CU that copy was 0.9-1.4 us slower:
-  // GF4 8192^2, 4096 -> 11008, 4096 -> 14336)
+  // the max-ILP copies: the rotated batch-1 kernel and the 8-wave batch-1 one (one workgroup
+  // per CU: the GF4 copy's registers leave room for no second one)
   if constexpr (ilp) {
-    if (mode == kRot1 || (mode == kFlat1 && pl.nw == kWaves / 2 && !deep && !pl.cu_shared))
+    if (mode == kRot1 || (mode == kFlat1 && pl.nw == kWaves / 2))
       return fb_ilp::launch(FMT, XDT, mode, wdev, x, y, s, pl.grid, pl.SPL, pl.GS, pl.tq, pl.tr,
-                            pl.S, pl.lds, stream);
+                            pl.S, pl.lds, deep, stream);
   }
   if (mode == kSplitK)
     return deep ? launch_gemv<FMT, XDT, kSplitK, kWaves, 8>(wdev, x, y, s, pl, stream)
                 : launch_gemv<FMT, XDT, kSplitK, kWaves, 4>(wdev, x, y, s, pl, stream);
   if (mode == kFlat1) {
-    if (pl.nw == kWaves / 2)
-      return deep ? launch_gemv<FMT, XDT, kFlat1, kWaves / 2, 8>(wdev, x, y, s, pl, stream)
-                  : launch_gemv<FMT, XDT, kFlat1, kWaves / 2, 4>(wdev, x, y, s, pl, stream);
+    if (pl.nw == kWaves / 2) {
+      if constexpr (!ilp)
+        return deep ? launch_gemv<FMT, XDT, kFlat1, kWaves / 2, 8>(wdev, x, y, s, pl, stream)
+                    : launch_gemv<FMT, XDT, kFlat1, kWaves / 2, 4>(wdev, x, y, s, pl, stream);
+      return FB_ERR_HIP;  // not reached: started by fb_ilp::launch above
+    }
     return deep ? launch_gemv<FMT, XDT, kFlat1, kWaves, 8>(wdev, x, y, s, pl, stream)
                 : launch_gemv<FMT, XDT, kFlat1, kWaves, 4>(wdev, x, y, s, pl, stream);
   }
@@ -1634,7 +1650,7 @@ void* scratch_ptr(int dev) {
 namespace fb_ilp {
 int launch(int fmt, int xdt, int mode, const void* wdev, const void* x, void* y,
            const fb_shape_t* s, int grid, int SPL, int GS, int tq, int tr, int S, size_t lds,
-           hipStream_t stream) {
+           bool xp8, hipStream_t stream) {
   Plan pl;
   pl.grid = grid;
   pl.SPL = SPL;
@@ -1643,8 +1659,8 @@ int launch(int fmt, int xdt, int mode, const void* wdev, const void* x, void* y,
   pl.tr = tr;
   pl.S = S;
   pl.lds = lds;
-  pl.xp = 4;
-  if (mode == kRot1) {  // a rotation takes fp16 x
+  pl.xp = xp8 ? 8 : 4;
+  if (mode == kRot1) {  // a rotation takes fp16 x (and preloads its own way)
     pl.nw = kWaves;
     if (xdt != FB_DT_F16) return FB_ERR_DTYPE;
     return fmt == FB_FMT_GF4
@@ -1652,6 +1668,13 @@ int launch(int fmt, int xdt, int mode, const void* wdev, const void* x, void* y,
                : launch_gemv<FB_FMT_E2M1, FB_DT_F16, kRot1, kWaves, 4>(wdev, x, y, s, pl, stream);
   }
   pl.nw = kWaves / 2;  // kFlat1: GF4 with fp16 x, E2M1 with fp16 or bf16 x
+  if (xp8) {
+    if (fmt == FB_FMT_GF4)
+      return launch_gemv<FB_FMT_GF4, FB_DT_F16, kFlat1, kWaves / 2, 8>(wdev, x, y, s, pl, stream);
+    if (xdt == FB_DT_BF16)
+      return launch_gemv<FB_FMT_E2M1, FB_DT_BF16, kFlat1, kWaves / 2, 8>(wdev, x, y, s, pl, stream);
+    return launch_gemv<FB_FMT_E2M1, FB_DT_F16, kFlat1, kWaves / 2, 8>(wdev, x, y, s, pl, stream);
+  }
   if (fmt == FB_FMT_GF4)
     return launch_gemv<FB_FMT_GF4, FB_DT_F16, kFlat1, kWaves / 2, 4>(wdev, x, y, s, pl, stream);
   if (xdt == FB_DT_BF16)
