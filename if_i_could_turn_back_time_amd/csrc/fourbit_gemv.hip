@@ -1393,19 +1393,16 @@ int launch_gemv(const void* wdev, const void* x, void* y, const fb_shape_t* s, c
   return hipGetLastError() == hipSuccess ? FB_OK : FB_ERR_HIP;
 }
 
-// Whether fb_ilp::launch starts the batch-1 rotated kernel and the 8-wave batch-1 kernel with
-// the short x preload (instantiated in the max-ILP unit, not here).
+// The host side from here to the end of the file is compiled in the default unit only, so
+// that the max-ILP unit instantiates no kernel but its own two.
 #ifndef FB_GEMV_ILP_TU
-constexpr bool kIlpSplit = true;
-#else
-constexpr bool kIlpSplit = false;
-#endif
 
 template <int FMT, int XDT>
 int launch_mode(int mode, const void* wdev, const void* x, void* y, const fb_shape_t* s,
                 const Plan& pl, hipStream_t stream) {
   const bool deep = pl.xp == 8;
-  constexpr bool ilp = kIlpSplit && FMT != kFmtMx;
+  // fb_ilp::launch starts these two kernels (instantiated in the max-ILP unit, not here)
+  constexpr bool ilp = FMT != kFmtMx;
   // the max-ILP copies: the rotated batch-1 kernel and the 8-wave batch-1 one (one workgroup
   // per CU: the GF4 copy's registers leave room for no second one)
   if constexpr (ilp) {
@@ -1624,7 +1621,6 @@ int gemv_mx_impl(const void* wdev, const void* x, void* y, const fb_shape_t* s, 
   return gemv_mx_split_run(wdev, w8, y, s, cus, w8 + need, ws_bytes - need, hs);
 }
 
-#ifndef FB_GEMV_ILP_TU
 // Scratch of the allocation-free entry point: a file-scope device array (one per GPU the
 // library runs on, alive until the process ends).  Host code never uses the array's name as
 // an address: the device address comes from hipGetSymbolAddress, once per device.
