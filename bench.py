@@ -45,6 +45,7 @@ MIN_WARM_S = 0.25  # least wall time of back-to-back warm-up calls before a time
 LAST_WARMUP_CALLS = 0  # warm-up calls the last time_gpu ran (>= the requested warm-up)
 PRE_CALLS = 3  # untimed calls enqueued before each start event (busy GPU at the stamp)
 MEDIAN_WINDOWS = 9  # timed regions of --steps calls whose median is reported beside value
+SWEEP_WINDOWS = 6  # further regions per --sweep line (its median over 7 regions is reported)
 
 
 def n_copies(nbytes: int, cold: bool) -> int:
@@ -658,12 +659,14 @@ def main():
                 if name == args.workload:
                     continue
                 rec, pw = run_workload(name, max(50, args.steps // 2), args.warmup, False,
-                                       warm=args.warm, cache=cache, packer=args.packer)
+                                       warm=args.warm, cache=cache, packer=args.packer,
+                                       windows=SWEEP_WINDOWS)
                 del pw
                 torch.cuda.empty_cache()
                 f.write(json.dumps(rec) + "\n")
                 f.flush()
-                print(f"[sweep] {name}: {rec['us_per_call']:.2f} us, {rec['GBps']:.0f} GB/s, "
+                print(f"[sweep] {name}: {rec['us_per_call_median']:.2f} us (median), "
+                      f"{rec['GBps']:.0f} GB/s (first region), "
                       f"parity {rec.get('parity_ok')}", file=sys.stderr, flush=True)
 
     rec, pw = run_workload(args.workload, args.steps, args.warmup, not args.no_cpu,
