@@ -30,8 +30,8 @@
 
 // The library's GEMV is two translation units.  fourbit_gemv_ilp.hip includes this file with
 // FB_GEMV_ILP_TU defined and is compiled with the compiler's max-ILP instruction scheduling;
-// it holds the kernels that run faster that way, the batch-1 rotated one (kRot1) and the
-// 8-wave batch-1 one (kFlat1, one workgroup per CU), and fb_ilp::launch starts them.  Every
+// it holds the kernels that run faster that way, the 8-wave batch-1 ones (kFlat1 and the
+// rotated kRot1, one workgroup per CU), and fb_ilp::launch starts them.  Every
 // other kernel stays here: with max-ILP scheduling the 16-wave batch-1 kernel ran the large
 // layers 1.4-1.8 us slower.
 namespace fb_ilp {
@@ -1275,19 +1275,21 @@ size_t plan_lds(const fb_shape_t* s, int tpw, int SPL) {
 }
 
 // The fewest K-slices whose LDS fits.
-// - Unrotated batch-1 GF4 / E2M1 layers whose x fits one slice: one 8-wave workgroup per CU
-//   (up to the number of row tiles), run by the max-ILP copy of the kernel, which holds 183
-//   VGPRs (GF4) so that only one such workgroup fits a CU.  Measured against 16 waves with
+// - Batch-1 GF4 / E2M1 layers whose x fits one slice, rotated or not: one 8-wave workgroup
+//   per CU (up to the number of row tiles), run by the max-ILP copy of the kernel, which holds
+//   183 VGPRs (GF4, unrotated) so that only one such workgroup fits a CU.  Measured against 16 waves with
 //   the default scheduling, same box, median us: GF4 8192 -> 28672 29.79 -> 28.93,
 //   28672 -> 8192 30.16 -> 29.31, 4096 -> 28672 17.47 -> 16.55, 4096 -> 14336 10.80 -> 9.96,
 //   4096 -> 11008 8.77 -> 8.19; E2M1 8192 -> 28672 20.58 -> 20.28; the rest within 0.1.
+//   Rotated, against 16 waves on the rotated kernel's max-ILP copy: 4096^2 7.27 -> 6.96,
+//   4096 -> 11008 10.58 -> 10.06, 11008 -> 4096 10.35 -> 9.60, 8192^2 14.45 -> 13.95.
 // - The native FP4 path's batch-1 layers with few row tiles per CU (at most 2) and LDS that
 //   fits twice in a CU: two 8-wave workgroups per CU.
 // - Otherwise one 16-wave workgroup per CU.
 bool make_plan(const fb_shape_t* s, int cus, Plan& pl) {
   const int GS = (s->K / 128 + 3) / 4;
   const int T = (s->N + 15) / 16;
-  const bool one8 = !s->fwht_block && s->B == 1 && s->fmt != kFmtMx;
+  const bool one8 = s->B == 1 && s->fmt != kFmtMx;
   const bool half = one8 || (!s->fwht_block && s->B == 1 && T <= 2 * cus);
   for (int pass = half ? 0 : 1; pass < 2; ++pass) {
     const int nw = pass == 0 ? kWaves / 2 : kWaves;
@@ -1406,7 +1408,7 @@ int launch_mode(int mode, const void* wdev, const void* x, void* y, const fb_sha
   // the max-ILP copies: the rotated batch-1 kernel and the 8-wave batch-1 one (one workgroup
   // per CU: the GF4 copy's registers leave room for no second one)
   if constexpr (ilp) {
-    if (mode == kRot1 || (mode == kFlat1 && pl.nw == kWaves / 2))
+    if ((mode == kRot1 || mode == kFlat1) && pl.nw == kWaves / 2)
       return fb_ilp::launch(FMT, XDT, mode, wdev, x, y, s, pl.grid, pl.SPL, pl.GS, pl.tq, pl.tr,
                             pl.S, pl.lds, deep, stream);
   }
@@ -1437,8 +1439,10 @@ int launch_mode(int mode, const void* wdev, const void* x, void* y, const fb_sha
     return FB_ERR_FWHT;  // the split is of unrotated x
   } else {
     // the rotation preloads kXPre 256-value sub-blocks per wave instead
-    if (mode == kRot1) {
-      if constexpr (!ilp) return launch_gemv<FMT, XDT, kRot1, kWaves, 4>(wdev, x, y, s, pl, stream);
+    if (mode == kRot1) {  // 16 waves: a plan that would not fit 8-wave staging (not met)
+      if (pl.nw == kWaves) return launch_gemv<FMT, XDT, kRot1, kWaves, 4>(wdev, x, y, s, pl, stream);
+      if constexpr (!ilp)
+        return launch_gemv<FMT, XDT, kRot1, kWaves / 2, 4>(wdev, x, y, s, pl, stream);
       return FB_ERR_HIP;  // not reached: started by fb_ilp::launch above
     }
     return launch_gemv<FMT, XDT, kRotated, kWaves, 4>(wdev, x, y, s, pl, stream);
@@ -1656,14 +1660,14 @@ int launch(int fmt, int xdt, int mode, const void* wdev, const void* x, void* y,
   pl.S = S;
   pl.lds = lds;
   pl.xp = xp8 ? 8 : 4;
+  pl.nw = kWaves / 2;
   if (mode == kRot1) {  // a rotation takes fp16 x (and preloads its own way)
-    pl.nw = kWaves;
     if (xdt != FB_DT_F16) return FB_ERR_DTYPE;
     return fmt == FB_FMT_GF4
-               ? launch_gemv<FB_FMT_GF4, FB_DT_F16, kRot1, kWaves, 4>(wdev, x, y, s, pl, stream)
-               : launch_gemv<FB_FMT_E2M1, FB_DT_F16, kRot1, kWaves, 4>(wdev, x, y, s, pl, stream);
+               ? launch_gemv<FB_FMT_GF4, FB_DT_F16, kRot1, kWaves / 2, 4>(wdev, x, y, s, pl, stream)
+               : launch_gemv<FB_FMT_E2M1, FB_DT_F16, kRot1, kWaves / 2, 4>(wdev, x, y, s, pl, stream);
   }
-  pl.nw = kWaves / 2;  // kFlat1: GF4 with fp16 x, E2M1 with fp16 or bf16 x
+  // kFlat1: GF4 with fp16 x, E2M1 with fp16 or bf16 x
   if (xp8) {
     if (fmt == FB_FMT_GF4)
       return launch_gemv<FB_FMT_GF4, FB_DT_F16, kFlat1, kWaves / 2, 8>(wdev, x, y, s, pl, stream);

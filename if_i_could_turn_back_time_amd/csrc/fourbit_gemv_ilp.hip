@@ -1,6 +1,6 @@
 // The GEMV kernels that build faster with the compiler's max-ILP instruction scheduling
 // (-mllvm -amdgpu-sched-strategy=max-ilp, set for this file alone by build_lib.py): the
-// batch-1 rotated kernel and the 8-wave batch-1 kernel (one workgroup per CU).  The code is
+// 8-wave batch-1 kernels, rotated and not (one workgroup per CU).  The code is
 // fourbit_gemv.hip's; this unit instantiates only those kernels and fb_ilp::launch.
 #define FB_GEMV_ILP_TU
 #include "fourbit_gemv.hip"
