@@ -1032,7 +1032,9 @@ __global__ __launch_bounds__(NW * 64) void gemv_kernel(
       if (threadIdx.x == 0) *counter = 2 * NW;
     }
     if (s == s_begin) {
-      if (tile_reduce && (int)threadIdx.x < t1 - t0) tile_cnt[threadIdx.x] = 0;
+      // a workgroup may own more row tiles than it has threads (a long N over a short K)
+      if constexpr (tile_reduce)
+        for (int i = threadIdx.x; i < t1 - t0; i += NT) tile_cnt[i] = 0;
       if (threadIdx.x == 0) *counter = 2 * NW;
       if (threadIdx.x < zero_bytes(FMT) / 16)
         reinterpret_cast<u32x4*>(zeros)[threadIdx.x] = u32x4{0u, 0u, 0u, 0u};

@@ -116,6 +116,105 @@ def test_config2_student_t(K, N):
     check_layer("e2m1", K, N, 1, "cfg2")
 
 
+# Config 1: the GF4 4096 x 4096 layer at batch 1 (the CPU baseline's configuration).
+def test_config1_gf4_full_size():
+    say("config 1", 4096, 4096)
+    check_layer("gf4", 4096, 4096, 1, "cfg1")
+
+
+def check_layer_rot(fmt, K, N, block, kind):
+    """A rotated layer at full size, batch 1: every row against the device-decoded weight
+    W' (rotated basis) times x' = H_b x / sqrt(b) (the oracle's fp64 rotation, as fp32) in
+    fp32 torch; sampled rows against the oracle's own decode; the same bits twice."""
+    g = torch.Generator().manual_seed(0)
+    w = WL.synth_weight(kind, N, K, g)
+    x = WL.synth_x(kind, 1, K, g).half()      # rotations take fp16 x
+    pw = PackedWeight.quantize(w, fmt, fwht_block=block, device=DEV,
+                               packer="gpu" if fmt == "gf4" else "host")
+    assert pw.f16_exact
+    W = pw.dequant_device(torch.float32)
+    xr = O.rotate_x(x, block)
+    xd = x.to(DEV)
+    y = pw.gemv(xd, out_dtype=torch.float32)
+    y16 = pw.gemv(xd, out_dtype=torch.float16)
+    yref = xr.to(DEV) @ W.t()
+    torch.cuda.synchronize()
+    ok, emax = within_tol(y, yref)
+    assert ok, f"all rows vs device decode: max abs err {emax}"
+    ok, emax = within_tol(y16, yref, 2.0 ** -11)
+    assert ok, f"fp16 output: max abs err {emax}"
+    rows = torch.randint(0, N, (24,), generator=torch.Generator().manual_seed(N + K))
+    codes = O.unpack_nibbles(pw.codes[rows].numpy())
+    meta = pw.meta[rows].numpy()
+    meta = meta.view(np.uint16) if fmt == "gf4" else meta
+    Wo = O.dequant_f32(fmt, codes, meta)
+    assert torch.equal(W[rows].cpu().view(torch.int32), Wo.view(torch.int32))
+    ok, emax = within_tol(y[:, rows], O.y_ref(fmt, codes, meta, x, block))
+    assert ok, f"oracle rows: max abs err {emax}"
+    assert torch.equal(pw.gemv(xd, out_dtype=torch.float32), y)
+
+
+# Config 3: the Llama-7B shapes in GF4 with the fused Walsh-Hadamard rotation, at full size
+# (4096 -> 11008 runs the 8-wave rotated batch-1 plan with 2-3 row tiles per workgroup), and
+# one E2M1 layer through the same rotated kernel.
+@pytest.mark.parametrize("fmt,K,N,block,kind", [
+    ("gf4", 4096, 4096, 4096, "cfg1"), ("gf4", 4096, 11008, 4096, "cfg1"),
+    ("gf4", 11008, 4096, 256, "cfg1"), ("e2m1", 4096, 11008, 4096, "cfg2"),
+], ids=lambda v: str(v))
+def test_config3_rotated_full_size(fmt, K, N, block, kind):
+    say("config 3", fmt, K, N, block)
+    check_layer_rot(fmt, K, N, block, kind)
+
+
+def _random_packed(fmt, N, K, seed):
+    """A packed weight of random codes and random codebooks / scale bytes (no packing
+    run: the shape is too large for the Jenks packer to be quick)."""
+    g = torch.Generator().manual_seed(seed)
+    codes = torch.randint(0, 256, (N, K // 2), dtype=torch.uint8, generator=g)
+    if fmt == "gf4":
+        meta = (torch.randn(N, K // 128, 16, generator=g) * 0.02).half().view(torch.int16)
+    else:
+        meta = torch.randint(118, 124, (N, K // 32), dtype=torch.uint8, generator=g)
+    return PackedWeight(fmt, N, K, codes, meta, 0, DEV)
+
+
+@pytest.mark.parametrize("fmt", ["gf4", "e2m1"])
+def test_batch1_more_row_tiles_than_threads(fmt):
+    """Batch 1 over a short K and a very long N: each 8-wave (512-thread) workgroup owns
+    more row tiles than it has threads (N = 2,200,000, K = 512: 137,500 tiles, 538 per
+    workgroup on 256 CUs), so the per-tile unit counters are cleared by a strided loop.
+    Every row is checked against the device-decoded weight times x in fp32 torch, sampled
+    rows against the oracle's decode, and the same call twice gives the same bits."""
+    N, K = 2_200_000, 512
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    T = (N + 15) // 16
+    say("tiles > threads", fmt, N, K, "tiles per workgroup", -(-T // min(T, cus)))
+    pw = _random_packed(fmt, N, K, 17)
+    xdt = torch.float16 if fmt == "gf4" else torch.bfloat16
+    x = torch.randn(1, K, generator=torch.Generator().manual_seed(3)).to(xdt)
+    xd = x.to(DEV)
+    y = torch.full((1, N), float("nan"), device=DEV)
+    pw.gemv(xd, out=y)
+    W = pw.dequant_device(torch.float32)
+    yref = xd.float() @ W.t()
+    torch.cuda.synchronize()
+    del W
+    assert bool(torch.isfinite(y).all()), "outputs left unwritten"
+    ok, emax = within_tol(y, yref)
+    assert ok, f"all rows vs device decode: max abs err {emax}"
+    rows = torch.randint(0, N, (32,), generator=torch.Generator().manual_seed(4))
+    rows[0], rows[1] = N - 1, (T - 1) * 16 - 1       # the last tile and the one before
+    codes = O.unpack_nibbles(pw.codes[rows].numpy())
+    meta = pw.meta[rows].numpy()
+    Wo = O.dequant_f32(fmt, codes, meta.view(np.uint16) if fmt == "gf4" else meta)
+    ok, emax = within_tol(y[:, rows], torch.nn.functional.linear(x.float(), Wo))
+    assert ok, f"oracle rows: max abs err {emax}"
+    y2 = torch.full((1, N), float("nan"), device=DEV)
+    pw.gemv(xd, out=y2)
+    torch.cuda.synchronize()
+    assert torch.equal(y, y2)
+
+
 @pytest.mark.parametrize("N", [11008, 14336])
 def test_gf4_batch1_several_tiles_per_8wave_workgroup(N):
     """GF4 batch 1 at K = 4096 with more row tiles T than CUs: the plan runs one 8-wave
@@ -205,26 +304,71 @@ def test_e2m1_scale_bytes_at_fp16_limits():
 
 
 def test_fp16_range_checks():
-    """GF4 and rotated layers stage x in fp16: a bf16 activation beyond 65504 raises, as
-    does a rotation block whose L2 norm reaches 65504; range_check=False skips the check."""
+    """GF4 and rotated layers stage x in fp16.  With range_check on, a bf16 activation
+    beyond 65504 raises, as does a rotation block whose L2 norm reaches 65504; by default
+    (no host sync) such an overflow shows as non-finite outputs."""
     say("fp16 range")
     lin = torch.nn.Linear(4096, 32)
     q = QuantLinear(lin).to(DEV)
+    assert q.range_check is False
     x = torch.randn(2, 4096, device=DEV, dtype=torch.bfloat16)
     q(x)
     x[1, 7] = 70000.0
+    assert not torch.isfinite(q(x)).all()
+    q.range_check = True
     with pytest.raises(ValueError, match="fp16 range"):
         q(x)
-    q.range_check = False
-    assert not torch.isfinite(q(x)).all()
     qr = QuantLinear(lin, hadamard=True).to(DEV)
+    qr.range_check = True
     xh = torch.randn(1, 4096, device=DEV, dtype=torch.float16)
     qr(xh)
     xh[0, :4] = 40000.0                                     # block norm 80000
     with pytest.raises(ValueError, match="norm"):
         qr(xh)
     qe = QuantLinear(lin, fmt="e2m1").to(DEV)
+    qe.range_check = True
     qe(x)                                                   # bf16 x: no fp16 staging
+
+
+@pytest.mark.parametrize("K,N,hadamard", [(4096, 4096, True), (11008, 4096, True),
+                                          (8192, 1024, False)])
+def test_quantlinear_graph_capture_replays(K, N, hadamard):
+    """QuantLinear's forward captured in a HIP graph at batch 8 and replayed: a rotated
+    layer (x rotated once into the module's cached workspace, then the GEMV) and a plain
+    one.  Every replay, with the program's own eager work and synchronisations between
+    them, gives the eager forward's bits for the input then in the static buffer; the
+    graph records no allocation or memset of the workspace (the module caches an
+    uninitialised one, and the forward makes no host sync)."""
+    say("graph capture", K, N, hadamard)
+    B = 8
+    g = torch.Generator().manual_seed(K + N)
+    q = QuantLinear(torch.nn.Linear(K, N), hadamard=hadamard, packer="gpu").to(DEV)
+    xs = [torch.randn(B, K, generator=g).half().to(DEV) for _ in range(4)]
+    eager = []
+    for x in xs:
+        eager.append(q(x))
+    torch.cuda.synchronize()
+    static_x = xs[0].clone()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        q(static_x)                                        # the stream's own workspace
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=s):               # s's workspace, made above
+        static_y = q(static_x)
+    for rep in range(3):
+        for i, x in enumerate(xs):
+            static_x.copy_(x)
+            graph.replay()
+            torch.cuda.synchronize()
+            assert torch.equal(static_y, eager[i]), f"replay {rep}, input {i}"
+            # eager work of the program's own between replays (on the default stream,
+            # with that stream's workspace)
+            junk = q(xs[(i + 1) % len(xs)])
+            assert torch.equal(junk, eager[(i + 1) % len(xs)])
+            torch.cuda.synchronize()
 
 
 @pytest.mark.parametrize("fmt,K,hadamard", [("gf4", 1024, False), ("e2m1", 1024, False),

@@ -48,6 +48,38 @@ def test_diagnostic_trace_library_exports():
             getattr(C.lib(), name)
 
 
+def test_batch1_plans_over_a_shape_sweep():
+    """The GEMV's launch plan (fb_phase_plan of the diagnostic library, host-side: without a
+    GPU it plans for 256 CUs, an MI355X's count) over batch-1 shapes up to N = 4.2M: every
+    valid shape gets a plan, batch-1 layers that fit one K-slice run one 8-wave workgroup
+    per CU (the largest fall back to 16 waves or K-slices), and the row tiles are split
+    evenly (tq or tq + 1 per workgroup, covering every tile once).  Shapes of short K and
+    long N give workgroups more row tiles than threads, whose per-tile unit counters the
+    kernel clears with a strided loop; the GPU suite runs such a shape (N = 2,200,000,
+    K = 512: 538 tiles per 512-thread workgroup)."""
+    T_lib = ctypes.CDLL(str(Path(C.__file__).resolve().parent / "libfourbit_trace.so"))
+    ip = ctypes.POINTER(ctypes.c_int)
+    T_lib.fb_phase_plan.argtypes = [ctypes.POINTER(C.FbShape), ip, ip, ip, ip, ip]
+    over = []
+    for fmt in (C.FMT_GF4, C.FMT_E2M1):
+        xdt = C.DT_F16 if fmt == C.FMT_GF4 else C.DT_BF16
+        for K in (128, 512, 2048, 4096, 8192):
+            for N in (1, 16, 4095, 65536, 2_200_000, 4_200_000):
+                s = C.make_shape(N, K, 1, fmt, 0, xdt, C.DT_F32)
+                v = [ctypes.c_int() for _ in range(5)]
+                assert T_lib.fb_phase_plan(ctypes.byref(s), *[ctypes.byref(a) for a in v]) == 0
+                grid, waves, slices, tq, tr = (a.value for a in v)
+                T = (N + 15) // 16
+                assert grid == min(T, 256) and waves in (8, 16) and slices >= 1, (fmt, K, N)
+                assert grid * tq + tr == T and 0 <= tr < grid
+                if N < 65536 or K * N < 2 ** 30:  # x and the slots fit one slice, 8 waves
+                    assert waves == 8 and slices == 1, (fmt, K, N)
+                if slices == 1 and tq + (tr > 0) > waves * 64:
+                    over.append((fmt, K, N, tq + (tr > 0)))
+    assert (C.FMT_GF4, 512, 2_200_000, 538) in over
+    assert (C.FMT_E2M1, 512, 2_200_000, 538) in over
+
+
 @pytest.mark.parametrize("kw,err", [
     (dict(K=100), -2), (dict(K=0), -2), (dict(N=0), -2), (dict(B=0), -2),
     (dict(group=64), -3), (dict(fmt=7), -4), (dict(x_dtype=C.DT_BF16), -5),
@@ -391,6 +423,59 @@ def test_load_state_dict_takes_the_reference_layers_own_state():
         QuantLinear(torch.nn.Linear(128, 24), pack=False).load_state_dict(sd)
 
 
+def test_load_into_fp4_mfma_module_drops_the_fp4_path_for_other_formats():
+    """A module built for the native FP4 path (fp4_mfma=True: unrotated E2M1 only) that
+    loads another format -- the reference layer's own state (packed as GF4), a packed GF4
+    or a rotated E2M1 checkpoint -- runs that format's exact-decode path afterwards instead
+    of refusing its next forward; an unrotated E2M1 checkpoint keeps the FP4 path."""
+    g = torch.Generator().manual_seed(4)
+    lin = torch.nn.Linear(256, 24)
+    with torch.no_grad():
+        lin.weight.copy_(torch.randn(24, 256, generator=g) * 0.02)
+
+    def fresh():
+        q = QuantLinear(lin, fmt="e2m1", fp4_mfma=True)
+        assert q.fp4_mfma
+        return q
+
+    q = fresh()
+    q.load_state_dict(reference_state(24, 256, seed=3))
+    assert q.fmt == "gf4" and not q.fp4_mfma
+    q = fresh()
+    q.load_state_dict(QuantLinear(lin, fmt="gf4").state_dict())
+    assert q.fmt == "gf4" and not q.fp4_mfma
+    q = fresh()
+    q.load_state_dict(QuantLinear(lin, fmt="e2m1", hadamard=True).state_dict())
+    assert q.fmt == "e2m1" and q.fwht_block == 256 and not q.fp4_mfma
+    q = fresh()
+    q.load_state_dict(QuantLinear(lin, fmt="e2m1").state_dict())
+    assert q.fmt == "e2m1" and q.fwht_block == 0 and q.fp4_mfma
+
+
+def test_backward_decodes_in_chunks_of_row_tiles():
+    """The backward pass decodes the weight a chunk of 16-row tiles at a time: the row
+    offsets into the device stream are whole tiles, and the rows from a tile on are the
+    stream of the layer without its first rows (the layout is tile-major)."""
+    from if_i_could_turn_back_time_amd import linear as LN
+    for fmt, bb in ((C.FMT_GF4, 6144), (C.FMT_E2M1, 4352)):
+        N, K = 80, 1152
+        codes = torch.from_numpy(RNG.integers(0, 256, size=(N, K // 2), dtype=np.uint8))
+        meta = (torch.from_numpy(RNG.integers(0, 2**16, size=(N, K // 128, 16),
+                                              dtype=np.uint16).view(np.int16))
+                if fmt == C.FMT_GF4 else
+                torch.from_numpy(RNG.integers(0, 255, size=(N, K // 32), dtype=np.uint8)))
+        full = C.to_device_layout(codes, meta, C.make_shape(N, K, 1, fmt))
+        for r0 in (16, 48):
+            sh = C.make_shape(N - r0, K, 1, fmt)
+            assert C.tile_offset(sh, r0) == (r0 // 16) * 3 * bb
+            tail = C.to_device_layout(codes[r0:], meta[r0:], sh)
+            off = C.tile_offset(sh, r0)
+            assert torch.equal(full[off:off + tail.numel()], tail)
+    with pytest.raises(ValueError):
+        C.tile_offset(C.make_shape(64, 512, 1, C.FMT_GF4), 8)
+    assert LN.BACKWARD_CHUNK_BYTES // (8192 * 4) // 16 * 16 == 2048
+
+
 def test_replace_forward_packs_adaround_levels():
     from types import SimpleNamespace
     from if_i_could_turn_back_time_amd import adaround_levels, pack_quantized_linears
@@ -669,6 +754,68 @@ def test_jenks2_filters_host_errors_and_conv_mask_api():
     assert torch.equal(m.reshape(32, 9).bool(), torch.from_numpy(keep))
     with pytest.raises(ValueError):
         jenks.conv_mask(torch.randn(4, 9))
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float64])
+def test_jenks2_ssd_host_bit_exact_vs_oracle(dtype):
+    """fb_jenks2_ssd_host (the reference's per-split SSD interface, jenks_optimization_cuda /
+    jenks_optimization_biases_cuda) gives the oracle's jenks2_ssd, rounded to the input's
+    dtype, bit for bit: across the 256-value block and 65,536-value superblock edges, with
+    ties and signed zeros, and on unsorted input (taken in the order given)."""
+    rng = np.random.default_rng(21)
+    npdt = np.float32 if dtype == torch.float32 else np.float64
+    for n in (1, 2, 255, 256, 257, 4097, 65536, 65537, 200003):
+        w = (rng.standard_t(3, size=n) * 0.05).astype(npdt)
+        if n > 8:
+            w[rng.integers(0, n, n // 5)] = 0.0
+            w[rng.integers(0, n, n // 9)] = -0.0
+        v = np.sort(w, kind="stable")
+        got = C.jenks2_ssd(torch.from_numpy(v))
+        assert got.dtype == dtype and got.shape == (n,)
+        ref = O.jenks2_ssd(v).astype(npdt)
+        assert np.array_equal(got.numpy().view(np.uint8), ref.view(np.uint8)), n
+        # the fp64 SSDs' first argmin is the mask path's split on the same (float32) values
+        # (the rounded vector's argmin may fall on a split that rounding made equal)
+        if dtype == torch.float32:
+            assert int(np.argmin(O.jenks2_ssd(v))) == C.jenks2_host(torch.from_numpy(v))[1]
+    u = np.array([3.0, -2.0, 0.5, 0.5, 9.0], npdt)
+    assert np.array_equal(C.jenks2_ssd(torch.from_numpy(u)).numpy(), O.jenks2_ssd(u).astype(npdt))
+
+
+def test_jenks2_ssd_filters_host_and_errors():
+    """fb_jenks2_ssd_filters_host: every filter's row is the oracle's jenks2_ssd of that
+    filter, bit for bit (fp32 and fp64), at the per-filter size edges; argument errors are
+    codes, and the reference-shaped drop-ins refuse CPU tensors as CHECK_INPUT does."""
+    rng = np.random.default_rng(22)
+    for npdt, tdt in ((np.float32, torch.float32), (np.float64, torch.float64)):
+        for n in (1, 9, 25, 256, 257, C.JENKS2_FILTER_MAX):
+            w = np.sort((rng.standard_normal((7, n)) * 0.05).astype(npdt), axis=1, kind="stable")
+            got = C.jenks2_ssd_filters(torch.from_numpy(w), nthreads=3)
+            assert got.dtype == tdt and got.shape == (7, n)
+            ref = np.stack([O.jenks2_ssd(r) for r in w]).astype(npdt)
+            assert np.array_equal(got.numpy().view(np.uint8), ref.view(np.uint8)), n
+    L = C.lib()
+    arena = np.zeros(1 << 12, np.uint8)
+    p = arena.ctypes.data + (-arena.ctypes.data) % 256  # aligned host address: never read
+    assert L.fb_jenks2_ssd_host(p, 0, C.DT_F32, p) == -2
+    assert L.fb_jenks2_ssd_host(p, 4, C.DT_F16, p) == -5
+    assert L.fb_jenks2_ssd_host(None, 4, C.DT_F32, p) == -1
+    assert L.fb_jenks2_ssd_filters_host(p, 2, C.JENKS2_FILTER_MAX + 1, C.DT_F32, p, 1) == -2
+    assert L.fb_jenks2_ssd_filters_host(p, 2, 4, C.DT_BF16, p, 1) == -5
+    assert L.fb_jenks2_ssd_filters_host(p, 2, 4, C.DT_F64, p, 0) == -12
+    assert L.fb_jenks2_ssd_gpu(p, 4, C.DT_F32, p, None, 0, None) == -1   # no device call
+    assert L.fb_jenks2_ssd_gpu(p + 8, 4, C.DT_F32, p, p, 1 << 20, None) == -7
+    assert L.fb_jenks2_ssd_filters_gpu(p, 2, 2000, C.DT_F32, p, None) == -2
+    need = ctypes.c_size_t(0)
+    assert L.fb_jenks2_ssd_workspace(1 << 20, ctypes.byref(need)) == 0 and need.value > 0
+    assert L.fb_jenks2_ssd_gpu(p, 1 << 20, C.DT_F32, p, p, need.value - 1, None) == -8
+    from if_i_could_turn_back_time_amd import module_bias, module_conv, module_weights
+    with pytest.raises(RuntimeError, match="CUDA"):
+        module_weights.jenks_optimization_cuda(torch.zeros(4, 4))
+    with pytest.raises(RuntimeError, match="CUDA"):
+        module_bias.jenks_optimization_biases_cuda(torch.zeros(4))
+    with pytest.raises(RuntimeError, match="CUDA"):
+        module_conv.jenks_optimization_cuda_conv(torch.zeros(2, 2, 3, 3))
 
 
 def test_gemv_noalloc_validation_needs_no_gpu():
