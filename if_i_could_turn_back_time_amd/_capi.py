@@ -20,9 +20,11 @@ import torch
 LIB_PATH = Path(__file__).resolve().with_name("libfourbit.so")
 
 FMT_GF4, FMT_E2M1 = 0, 1
-DT_F16, DT_BF16, DT_F32 = 0, 1, 2
+DT_F16, DT_BF16, DT_F32, DT_F64 = 0, 1, 2, 3
 FMT_BY_NAME = {"gf4": FMT_GF4, "e2m1": FMT_E2M1}
 GROUP_BY_FMT = {FMT_GF4: 128, FMT_E2M1: 32}
+# bytes of one device-stream block (16 rows x 512 K-elements): fourbit_layout.h
+BLOCK_BYTES = {FMT_GF4: 6144, FMT_E2M1: 4352}
 DTYPE_CODE = {torch.float16: DT_F16, torch.bfloat16: DT_BF16, torch.float32: DT_F32}
 ABI_VERSION = 1
 ERR_VALUE = -10  # FB_ERR_VALUE: non-finite / non-integer / out-of-range packer input
@@ -37,6 +39,8 @@ EXPORTED = (
     "fb_jenks2_filters_host", "fb_jenks2_filters_gpu", "fb_gemv_noalloc",
     "fb_mx_split_bytes", "fb_mx_split", "fb_mx_workspace_bytes", "fb_gemv_mx",
     "fb_gemv_mx_presplit", "fb_mx_presplit_workspace_bytes",
+    "fb_jenks2_ssd_host", "fb_jenks2_ssd_workspace", "fb_jenks2_ssd_gpu",
+    "fb_jenks2_ssd_filters_host", "fb_jenks2_ssd_filters_gpu",
 )
 
 
@@ -92,6 +96,11 @@ def lib() -> ctypes.CDLL:
         "fb_gemv_mx": (ctypes.c_int, [vp, vp, vp, sp, vp, sz, vp]),
         "fb_gemv_mx_presplit": (ctypes.c_int, [vp, vp, vp, sp, vp, sz, vp]),
         "fb_mx_presplit_workspace_bytes": (sz, [sp]),
+        "fb_jenks2_ssd_host": (ctypes.c_int, [vp, ctypes.c_int64, i32, vp]),
+        "fb_jenks2_ssd_workspace": (ctypes.c_int, [ctypes.c_int64, ctypes.POINTER(sz)]),
+        "fb_jenks2_ssd_gpu": (ctypes.c_int, [vp, ctypes.c_int64, i32, vp, vp, sz, vp]),
+        "fb_jenks2_ssd_filters_host": (ctypes.c_int, [vp, ctypes.c_int64, i32, i32, vp, i32]),
+        "fb_jenks2_ssd_filters_gpu": (ctypes.c_int, [vp, ctypes.c_int64, i32, i32, vp, vp]),
     }
     for name, (res, args) in sigs.items():
         fn = getattr(L, name)
@@ -230,9 +239,10 @@ def workspace_bytes(shape: FbShape) -> int:
 
 
 def new_workspace(shape: FbShape, device) -> torch.Tensor | None:
-    """Zero-filled device workspace for fb_gemv, or None when the shape needs none."""
+    """Device workspace for fb_gemv, or None when the shape needs none.  Its contents need
+    no initialisation (fb_gemv writes before it reads), so it is left uninitialised."""
     need = workspace_bytes(shape)
-    return torch.zeros(need, dtype=torch.uint8, device=device) if need else None
+    return torch.empty(need, dtype=torch.uint8, device=device) if need else None
 
 
 def gemv(wdev: torch.Tensor, x: torch.Tensor, y: torch.Tensor, shape: FbShape,
@@ -364,12 +374,28 @@ def mx_split(x: torch.Tensor, shape: FbShape):
     return terms.contiguous(), sc.reshape(2, B, K // 32).contiguous()
 
 
-def dequant_device(wdev: torch.Tensor, shape: FbShape, out_dtype=torch.float32) -> torch.Tensor:
+def tile_offset(shape: FbShape, row: int) -> int:
+    """Byte offset of row ``row`` (a multiple of 16) in the device stream: the stream is
+    16-row tiles, each ``ceil(K/512)`` blocks, one after the other, so the rows from
+    ``row`` on are the stream of the same layer without its first ``row`` rows."""
+    if row % 16:
+        raise ValueError("row offsets of the device stream are multiples of 16")
+    return (row // 16) * ((shape.K // 128 + 3) // 4) * BLOCK_BYTES[shape.fmt]
+
+
+def dequant_device(wdev: torch.Tensor, shape: FbShape, out_dtype=torch.float32,
+                   out: torch.Tensor | None = None) -> torch.Tensor:
+    """Exact device decode of the stream ``wdev`` (fb_dequant) to ``[N, K]`` of
+    ``out_dtype``, into ``out`` when given (contiguous, on wdev's device)."""
     if not wdev.is_cuda:
         raise RuntimeError("fb_dequant needs a device tensor (ROCm GPU)")
     if wdev.numel() < device_bytes(shape):
         raise ValueError("weight stream is smaller than fb_device_bytes(shape)")
-    out = torch.empty(shape.N, shape.K, dtype=out_dtype, device=wdev.device)
+    if out is None:
+        out = torch.empty(shape.N, shape.K, dtype=out_dtype, device=wdev.device)
+    elif (tuple(out.shape) != (shape.N, shape.K) or out.dtype != out_dtype
+          or out.device != wdev.device or not out.is_contiguous()):
+        raise ValueError("out does not match the shape, dtype or device")
     with torch.cuda.device(wdev.device):
         check(lib().fb_dequant(_ptr(wdev), _ptr(out), DTYPE_CODE[out_dtype],
                                ctypes.byref(shape), _stream(wdev.device)))
@@ -494,3 +520,68 @@ def jenks2_filters_gpu(w: torch.Tensor):
         check(lib().fb_jenks2_filters_gpu(_ptr(w), nf, n, _ptr(keep), _ptr(split), _ptr(gvf),
                                           _stream(w.device)))
     return keep.bool(), split, gvf
+
+
+# ------------------------------------------------------------------ per-split SSD
+SSD_DTYPE = {torch.float32: DT_F32, torch.float64: DT_F64}
+
+
+def _ssd_operand(t: torch.Tensor, align: int) -> torch.Tensor:
+    """t as a contiguous tensor of an fp32 / fp64 dtype whose data is ``align``-byte
+    aligned (a copy only when it is not)."""
+    if t.dtype not in SSD_DTYPE:
+        raise RuntimeError(f"the per-split SSD takes float32 or float64 values, got {t.dtype}")
+    t = t.detach().contiguous()
+    if t.data_ptr() % align:
+        t = t.clone()
+    return t
+
+
+def jenks2_ssd(srt: torch.Tensor) -> torch.Tensor:
+    """The within-class SSD of every split of the flattened values in the order given
+    (fb_jenks2_ssd_gpu on a device tensor, fb_jenks2_ssd_host on a CPU one; the same bits):
+    a 1-D tensor of srt's dtype and device."""
+    flat = srt.reshape(-1)
+    n = flat.numel()
+    if n < 1:
+        raise RuntimeError("the per-split SSD needs at least one value")
+    if not flat.is_cuda:
+        flat = _ssd_operand(flat, 8)
+        out = torch.empty(n, dtype=flat.dtype)
+        check(lib().fb_jenks2_ssd_host(_ptr(flat), n, SSD_DTYPE[flat.dtype], _ptr(out)))
+        return out
+    flat = _ssd_operand(flat, 16)
+    with torch.cuda.device(flat.device):
+        need = ctypes.c_size_t(0)
+        check(lib().fb_jenks2_ssd_workspace(n, ctypes.byref(need)))
+        ws = torch.empty(need.value + 256, dtype=torch.uint8, device=flat.device)
+        off = (-ws.data_ptr()) % 256
+        out = torch.empty(n, dtype=flat.dtype, device=flat.device)
+        check(lib().fb_jenks2_ssd_gpu(_ptr(flat), n, SSD_DTYPE[flat.dtype], _ptr(out),
+                                      ws.data_ptr() + off, need.value, _stream(flat.device)))
+    return out
+
+
+def jenks2_ssd_filters(srt: torch.Tensor, nthreads: int | None = None) -> torch.Tensor:
+    """Per-split SSD of every row of srt [nf, n] (each row one filter, in the order given;
+    n <= JENKS2_FILTER_MAX): [nf, n] of srt's dtype and device (fb_jenks2_ssd_filters_gpu /
+    fb_jenks2_ssd_filters_host, the same bits)."""
+    if srt.dim() != 2:
+        raise ValueError("srt must be [filters, values per filter]")
+    nf, n = srt.shape
+    if nf < 1 or n < 1:
+        raise RuntimeError("the per-split SSD needs at least one filter of one value")
+    if n > JENKS2_FILTER_MAX:
+        raise RuntimeError(f"filters of more than {JENKS2_FILTER_MAX} values are not supported")
+    if not srt.is_cuda:
+        srt = _ssd_operand(srt, 8)
+        out = torch.empty(nf, n, dtype=srt.dtype)
+        check(lib().fb_jenks2_ssd_filters_host(_ptr(srt), nf, n, SSD_DTYPE[srt.dtype], _ptr(out),
+                                               nthreads or nthreads_default()))
+        return out
+    srt = _ssd_operand(srt, 8)
+    with torch.cuda.device(srt.device):
+        out = torch.empty(nf, n, dtype=srt.dtype, device=srt.device)
+        check(lib().fb_jenks2_ssd_filters_gpu(_ptr(srt), nf, n, SSD_DTYPE[srt.dtype], _ptr(out),
+                                              _stream(srt.device)))
+    return out

@@ -79,29 +79,71 @@ def _fwht_last_dim(t: torch.Tensor, block: int) -> torch.Tensor:
     return (v.reshape(*lead, K) / float(block) ** 0.5)
 
 
-def _gemv_chunks(wdev, N, kp, fmt, fwht_block, xk, y, fp4_mfma=False):
+def _workspace(cache: dict | None, nbytes: int, device: torch.device):
+    """An uninitialised device workspace of at least ``nbytes`` (None for 0), kept in
+    ``cache`` per (device, stream) and grown when a call needs more: fb_gemv and
+    fb_gemv_mx need no initialised contents, and calls on one stream run in order, so one
+    buffer serves every call of a module on that stream (including graph replays)."""
+    if not nbytes:
+        return None
+    key = (device.index, torch.cuda.current_stream(device).cuda_stream)
+    ws = cache.get(key) if cache is not None else None
+    if ws is None or ws.numel() < nbytes:
+        ws = torch.empty(nbytes, dtype=torch.uint8, device=device)
+        if cache is not None:
+            cache[key] = ws
+    return ws
+
+
+def _gemv_chunks(wdev, N, kp, fmt, fwht_block, xk, y, fp4_mfma=False, ws_cache=None):
     f = C.FMT_BY_NAME[fmt]
     for b0 in range(0, xk.shape[0], MAX_GEMV_BATCH):
         b1 = min(b0 + MAX_GEMV_BATCH, xk.shape[0])
         shape = C.make_shape(N, kp, b1 - b0, f, fwht_block, C.DTYPE_CODE[xk.dtype],
                              C.DTYPE_CODE[y.dtype])
         if fp4_mfma:
-            C.gemv_mx(wdev, xk[b0:b1], y[b0:b1], shape)
+            ws = _workspace(ws_cache, C.mx_workspace_bytes(shape), xk.device)
+            C.gemv_mx(wdev, xk[b0:b1], y[b0:b1], shape, ws)
         else:
-            C.gemv(wdev, xk[b0:b1], y[b0:b1], shape, C.new_workspace(shape, xk.device))
+            ws = _workspace(ws_cache, C.workspace_bytes(shape), xk.device)
+            C.gemv(wdev, xk[b0:b1], y[b0:b1], shape, ws)
+
+
+# Most bytes of fp32 weight the backward pass decodes at once (a chunk of 16-row tiles).
+BACKWARD_CHUNK_BYTES = 64 * 2**20
+
+
+def _grad_x(wdev, N, kp, fmt, fwht_block, gy: torch.Tensor) -> torch.Tensor:
+    """``grad_y [M, N] @ W [N, kp]`` in fp32 with W decoded on the device (fb_dequant,
+    exact) a chunk of row tiles at a time: at most ``BACKWARD_CHUNK_BYTES`` of decoded
+    weight exist at once, whatever the layer's size.  Chunks are added in row order."""
+    f = C.FMT_BY_NAME[fmt]
+    rows = max(16, BACKWARD_CHUNK_BYTES // (kp * 4) // 16 * 16)
+    gyf = gy.float()
+    gx = torch.zeros(gy.shape[0], kp, dtype=torch.float32, device=gy.device)
+    buf = None
+    for r0 in range(0, N, rows):
+        r1 = min(N, r0 + rows)
+        shape = C.make_shape(r1 - r0, kp, 1, f, fwht_block)
+        if buf is None or buf.shape[0] != r1 - r0:
+            buf = torch.empty(r1 - r0, kp, dtype=torch.float32, device=gy.device)
+        W = C.dequant_device(wdev[C.tile_offset(shape, r0):], shape, torch.float32, out=buf)
+        gx.addmm_(gyf[:, r0:r1], W)
+    return gx
 
 
 def _kernel_input(x2: torch.Tensor, K: int, fmt: str, fwht_block: int, range_check: bool,
                   f16_exact: bool, fp4_mfma: bool = False) -> torch.Tensor:
     """x [M, K] -> the kernel's activation: fp16 for GF4 and every rotation (E2M1 keeps
     fp16 / bf16, fp32 becomes bf16; on the native FP4 path every dtype becomes bf16),
-    zero-padded to ``packed_k(K)``.  ``range_check``
-    raises where the fp16 staging would overflow: values beyond +-65504 in a wider x, and
-    for a rotation any block of L2 norm >= 65504 (a rotated value is at most its block's
-    norm).  It costs one reduction and a host sync per call."""
+    zero-padded to ``packed_k(K)``.  ``range_check`` raises where the fp16 staging would
+    overflow: values beyond +-65504 in a wider x, and for a rotation any block of L2 norm
+    >= 65504 (a rotated value is at most its block's norm).  It costs one reduction and a
+    host sync per call, so it is off by default and skipped while a graph is captured;
+    without it such an overflow shows as non-finite outputs (the staged value is inf)."""
     if fmt == "gf4" or fwht_block:
         xk = x2.to(torch.float16)
-        if range_check and xk.numel():
+        if range_check and xk.numel() and not torch.cuda.is_current_stream_capturing():
             if x2.dtype != torch.float16 and bool((torch.isfinite(x2) & ~torch.isfinite(xk)).any()):
                 raise ValueError("packed linear: activations beyond the fp16 range (+-65504); "
                                  "the GF4 and rotated kernels take fp16 x")
@@ -128,15 +170,17 @@ def _kernel_input(x2: torch.Tensor, K: int, fmt: str, fwht_block: int, range_che
 class _PackedLinearFn(torch.autograd.Function):
     """``x -> x W^T`` through the fused kernel, differentiable in x (as ``F.linear`` with
     the reference's frozen committed weight is, ``layers.py:34-35``).  Backward:
-    ``grad_x = grad_y W``, with W decoded on the device (fb_dequant, fp32) and, for a
-    rotated weight W' = W H, rotated back: ``grad_x = (grad_y W') H``."""
+    ``grad_x = grad_y W``, with W decoded on the device (fb_dequant, fp32) in chunks of row
+    tiles (``_grad_x``) and, for a rotated weight W' = W H, rotated back:
+    ``grad_x = (grad_y W') H``."""
 
     @staticmethod
-    def forward(ctx, x2, wdev, N, K, fmt, fwht_block, range_check, f16_exact, fp4_mfma=False):
+    def forward(ctx, x2, wdev, N, K, fmt, fwht_block, range_check, f16_exact, fp4_mfma=False,
+                ws_cache=None):
         xk = _kernel_input(x2, K, fmt, fwht_block, range_check, f16_exact, fp4_mfma)
         ydt = x2.dtype if x2.dtype in C.DTYPE_CODE else torch.float32
         y = torch.empty(x2.shape[0], N, dtype=ydt, device=x2.device)
-        _gemv_chunks(wdev, N, packed_k(K), fmt, fwht_block, xk, y, fp4_mfma)
+        _gemv_chunks(wdev, N, packed_k(K), fmt, fwht_block, xk, y, fp4_mfma, ws_cache)
         ctx.save_for_backward(wdev)
         ctx.cfg = (N, K, fmt, fwht_block, x2.dtype)
         return y
@@ -145,18 +189,16 @@ class _PackedLinearFn(torch.autograd.Function):
     def backward(ctx, gy):
         (wdev,) = ctx.saved_tensors
         N, K, fmt, fwht_block, xdt = ctx.cfg
-        shape = C.make_shape(N, packed_k(K), 1, C.FMT_BY_NAME[fmt], fwht_block)
-        W = C.dequant_device(wdev, shape, torch.float32)
-        gx = gy.float() @ W
+        gx = _grad_x(wdev, N, packed_k(K), fmt, fwht_block, gy)
         if fwht_block:
             gx = _fwht_last_dim(gx, fwht_block)
-        return gx[:, :K].to(xdt), None, None, None, None, None, None, None, None
+        return gx[:, :K].to(xdt), None, None, None, None, None, None, None, None, None
 
 
 def packed_linear(wdev: torch.Tensor, N: int, K: int, fmt: str, fwht_block: int,
                   x: torch.Tensor, bias: torch.Tensor | None = None, *,
-                  range_check: bool = True, f16_exact: bool = True,
-                  fp4_mfma: bool = False) -> torch.Tensor:
+                  range_check: bool = False, f16_exact: bool = True,
+                  fp4_mfma: bool = False, ws_cache: dict | None = None) -> torch.Tensor:
     """``F.linear(x, W, bias)`` for a packed 4-bit ``W [N, K]`` (device stream ``wdev``
     of a ``packed_k(K)``-wide weight), through fb_gemv in chunks of 16 rows of x.
 
@@ -164,7 +206,9 @@ def packed_linear(wdev: torch.Tensor, N: int, K: int, fmt: str, fwht_block: int,
     kept in fp16/bf16 (E2M1; fp32 becomes bf16) and zero-padded to ``packed_k(K)``; y
     has x's dtype (fp32 for other dtypes).  Differentiable in x (and bias): the weight is
     frozen, as the reference's committed weight is.  ``range_check`` (see
-    ``_kernel_input``) raises instead of letting fp16 staging overflow; ``f16_exact``
+    ``_kernel_input``) raises instead of letting fp16 staging overflow, at the cost of a
+    host sync; ``ws_cache`` keeps the call's fb_gemv workspace for the next calls (a dict
+    the caller owns, e.g. one per module); ``f16_exact``
     (E2M1 only) says whether the weight's scales decode exactly to fp16.  ``fp4_mfma``
     (unrotated E2M1 only) runs the matrix cores' native FP4 path (fb_gemv_mx): x as bf16,
     split into two MX-E4M3 terms, which hold a bf16 value exactly unless its 32-value block
@@ -182,13 +226,13 @@ def packed_linear(wdev: torch.Tensor, N: int, K: int, fmt: str, fwht_block: int,
     x2 = x.reshape(-1, K)
     if torch.is_grad_enabled() and x.requires_grad:
         y = _PackedLinearFn.apply(x2, wdev, N, K, fmt, fwht_block, range_check, f16_exact,
-                                  fp4_mfma)
+                                  fp4_mfma, ws_cache)
         if bias is not None:
             y = y + bias.to(y.dtype)
         return y.reshape(*lead, N)
     with torch.no_grad():
         y = _PackedLinearFn.forward(_NoCtx(), x2, wdev, N, K, fmt, fwht_block, range_check,
-                                    f16_exact, fp4_mfma)
+                                    f16_exact, fp4_mfma, ws_cache)
     if bias is not None:
         if torch.is_grad_enabled() and bias.requires_grad:
             y = y + bias.to(y.dtype)
@@ -266,8 +310,8 @@ class PackedWeight:
                             C.DTYPE_CODE[x_dtype], C.DTYPE_CODE[y_dtype])
 
     def workspace(self, shape: C.FbShape, device):
-        """Cached zero-initialised fb_gemv workspace for this device and shape (None when
-        the shape needs none)."""
+        """Cached fb_gemv workspace (uninitialised: none is needed) for this device and
+        size (None when the shape needs none)."""
         need = C.workspace_bytes(shape)
         if not need:
             return None
@@ -358,9 +402,13 @@ class QuantLinear(nn.Linear):
         if fp4_mfma and (fmt != "e2m1" or self.fwht_block):
             raise ValueError("fp4_mfma needs fmt='e2m1' without a rotation")
         self.fp4_mfma = fp4_mfma
-        # raise instead of letting fp16 activation staging overflow (one host sync per
-        # call for bf16 / fp32 inputs and for rotated layers); set False to skip
-        self.range_check = True
+        # True: raise instead of letting fp16 activation staging overflow, at one host sync
+        # per call for bf16 / fp32 inputs and for rotated layers (not while a graph is
+        # captured).  Off by default, so the forward never syncs and can be captured in a
+        # HIP graph; an overflow then shows as non-finite outputs.
+        self.range_check = False
+        # fb_gemv / fb_gemv_mx workspaces of this module, per (device, stream)
+        self._ws_cache = {}
         self._f16_exact = True
         self.register_load_state_dict_post_hook(QuantLinear._rebuild_after_load)
         if pack:
@@ -461,6 +509,7 @@ class QuantLinear(nn.Linear):
             self.codes = q.codes.to(dev)
             self.meta = q.meta.to(dev)
             self.hard_quant = False
+            self.fp4_mfma = False  # the reference's weight loads as GF4
             return
         # packed buffers take the checkpoint's shape/dtype (format may differ from ctor),
         # and the mask is present exactly when the checkpoint has one
@@ -484,6 +533,8 @@ class QuantLinear(nn.Linear):
         inv = {v: k for k, v in C.FMT_BY_NAME.items()}
         self.fmt = inv[hdr[1]]
         self.fwht_block = hdr[3]
+        if self.fp4_mfma and (self.fmt != "e2m1" or self.fwht_block):
+            self.fp4_mfma = False  # the native FP4 path takes unrotated E2M1 weights only
         shape = self._shape()
         self.wdev = C.to_device_layout(self.codes.cpu(), self.meta.cpu(), shape).to(
             self.codes.device)
@@ -511,7 +562,7 @@ class QuantLinear(nn.Linear):
         return packed_linear(self.wdev, self.out_features, self.in_features, self.fmt,
                              self.fwht_block, x, self.bias, range_check=self.range_check,
                              f16_exact=self._f16_exact,
-                             fp4_mfma=self.fp4_mfma)
+                             fp4_mfma=self.fp4_mfma, ws_cache=self._ws_cache)
 
     def extra_repr(self) -> str:
         return (f"in_features={self.in_features}, out_features={self.out_features}, "
@@ -544,7 +595,7 @@ def fp4_mfma_shared(layers, x: torch.Tensor):
             q.bias is not None and q.bias.requires_grad for q in layers)):
         return tuple(packed_linear(q.wdev, q.out_features, K, "e2m1", 0, x, q.bias,
                                    range_check=q.range_check, f16_exact=q._f16_exact,
-                                   fp4_mfma=True) for q in layers)
+                                   fp4_mfma=True, ws_cache=q._ws_cache) for q in layers)
     lead = x.shape[:-1]
     x2 = x.reshape(-1, K)
     kp = packed_k(K)
