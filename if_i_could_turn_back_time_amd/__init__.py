@@ -7,10 +7,12 @@ C ABI of ``libfourbit.so`` (``include/fourbit.h``).
 from .linear import (PackedWeight, QuantLinear, fp4_mfma_shared, fwht_block_for,  # noqa: F401
                      packed_k, packed_linear, quantize_module)
 from .brecq import adaround_levels, pack_quantized_linears, replace_forward  # noqa: F401
-from .jenks import bias_mask, jenks2, linear_mask  # noqa: F401
+from .jenks import (bias_mask, jenks2, linear_mask, module_bias, module_conv,  # noqa: F401
+                    module_weights)
 from . import _capi  # noqa: F401
 
 __all__ = ["PackedWeight", "QuantLinear", "fp4_mfma_shared", "fwht_block_for", "packed_k",
            "packed_linear",
            "quantize_module", "adaround_levels", "pack_quantized_linears", "replace_forward",
-           "jenks2", "linear_mask", "bias_mask"]
+           "jenks2", "linear_mask", "bias_mask", "module_weights", "module_bias",
+           "module_conv"]

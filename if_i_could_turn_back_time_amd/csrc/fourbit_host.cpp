@@ -499,17 +499,19 @@ int fb_dequant_host(const uint8_t* codes, const void* meta, float* w_out, const 
   return FB_OK;
 }
 
-// Two-class natural breaks over one array of n finite values (1 <= n < 2^31): the same
-// arithmetic, in the same association order, as fb_jenks2_gpu and the filter kernel of
-// fourbit_jenks2.hip, so that they give the same split, GVF and mask bits.
-static void jenks2_one(const float* w, int64_t n, uint8_t* keep, int64_t* split, double* gvf) {
+}  // extern "C"
+
+namespace {
+
+// The within-class SSD of every split of n values taken in the order given (1 <= n < 2^31):
+// visit(i, ssd(i)) for i = 0, 1, ..., n - 1 in turn.  fp64 sums in a fixed association order
+// -- centre c = srt[n / 2]; d = srt - c and d * d; prefix sums sequential within blocks of
+// 256, block totals sequential within superblocks of 256 blocks, superblock totals sequential
+// -- the same arithmetic, in the same order, as fourbit_jenks2.hip, so that host and GPU
+// give the same bits.  T: float or double values.
+template <typename T, typename Visit>
+void jenks2_ssd_sorted(const T* srt, int64_t n, Visit&& visit) {
   constexpr int64_t kBlk = 256, kSup = 256;
-  std::vector<int> order((size_t)n);
-  std::iota(order.begin(), order.end(), 0);
-  // ascending, stable by index; -0.0 == +0.0 under <
-  std::stable_sort(order.begin(), order.end(), [&](int a, int b) { return w[a] < w[b]; });
-  std::vector<float> srt((size_t)n);
-  for (int64_t t = 0; t < n; ++t) srt[t] = w[order[t]];
   const double c = (double)srt[n / 2];
   const int64_t nblk = (n + kBlk - 1) / kBlk, nsup = (nblk + kSup - 1) / kSup;
   std::vector<double> t1(nblk), t2(nblk), bx1(nblk), bx2(nblk), sx1(nsup + 1), sx2(nsup + 1);
@@ -548,8 +550,6 @@ static void jenks2_one(const float* w, int64_t n, uint8_t* keep, int64_t* split,
     sx2[nsup] = a2;
   }
   const double pt = sx1[nsup], qt = sx2[nsup];
-  double best = 0.0, ssd0 = 0.0;
-  int64_t arg = -1;
   for (int64_t b = 0; b < nblk; ++b) {
     const double base1 = sx1[b / kSup] + bx1[b], base2 = sx2[b / kSup] + bx2[b];
     double l1 = 0.0, l2 = 0.0;
@@ -558,22 +558,48 @@ static void jenks2_one(const float* w, int64_t n, uint8_t* keep, int64_t* split,
       const double left = i == 0 ? 0.0 : q - (p * p) / (double)i;
       const double rp = pt - p;
       const double right = (qt - q) - (rp * rp) / (double)(n - i);
-      const double v = left + right;
-      if (arg < 0 || v < best) {
-        best = v;
-        arg = i;
-      }
-      if (i == 0) ssd0 = v;
+      visit(i, left + right);
       const double d = (double)srt[i] - c;
       const double dq = d * d;
       l1 = l1 + d;
       l2 = l2 + dq;
     }
   }
+}
+
+// Two-class natural breaks over one array of n finite values (1 <= n < 2^31): the stable
+// ascending order, the SSD of every split of it (jenks2_ssd_sorted), the first minimum.  The
+// same bits as fb_jenks2_gpu and the filter kernels of fourbit_jenks2.hip.
+void jenks2_one(const float* w, int64_t n, uint8_t* keep, int64_t* split, double* gvf) {
+  std::vector<int> order((size_t)n);
+  std::iota(order.begin(), order.end(), 0);
+  // ascending, stable by index; -0.0 == +0.0 under <
+  std::stable_sort(order.begin(), order.end(), [&](int a, int b) { return w[a] < w[b]; });
+  std::vector<float> srt((size_t)n);
+  for (int64_t t = 0; t < n; ++t) srt[t] = w[order[t]];
+  double best = 0.0, ssd0 = 0.0;
+  int64_t arg = -1;
+  jenks2_ssd_sorted(srt.data(), n, [&](int64_t i, double v) {
+    if (arg < 0 || v < best) {
+      best = v;
+      arg = i;
+    }
+    if (i == 0) ssd0 = v;
+  });
   for (int64_t t = 0; t < n; ++t) keep[order[t]] = t >= arg ? 1 : 0;
   *split = arg;
   *gvf = (ssd0 - best) / (ssd0 + 1e-8);
 }
+
+// ssd[i] (in T) of every split of srt[0 .. n) in the order given.
+template <typename T>
+void jenks2_ssd_out(const T* srt, int64_t n, T* ssd) {
+  jenks2_ssd_sorted(srt, n, [&](int64_t i, double v) { ssd[i] = (T)v; });
+}
+
+}  // namespace
+
+extern "C" {
 
 // The whole array (the reference's Linear_Mask / Bias_Mask, cuda_helpers.py:378-411).
 int fb_jenks2_host(const float* w, int64_t n, uint8_t* keep, int64_t* split, double* gvf) {
@@ -582,6 +608,40 @@ int fb_jenks2_host(const float* w, int64_t n, uint8_t* keep, int64_t* split, dou
   for (int64_t t = 0; t < n; ++t)
     if (!std::isfinite(w[t])) return FB_ERR_VALUE;
   jenks2_one(w, n, keep, split, gvf);
+  return FB_OK;
+}
+
+// The per-split SSD of a pre-sorted array (the reference's jenks_optimization_cuda and
+// jenks_optimization_biases_cuda, cuda_helpers.py:187-211, :122-146), in its dtype.
+int fb_jenks2_ssd_host(const void* sorted, int64_t n, int32_t dtype, void* ssd) {
+  if (!sorted || !ssd) return FB_ERR_NULL;
+  if (n < 1 || n > INT32_MAX) return FB_ERR_SHAPE;
+  if (dtype == FB_DT_F32)
+    jenks2_ssd_out(static_cast<const float*>(sorted), n, static_cast<float*>(ssd));
+  else if (dtype == FB_DT_F64)
+    jenks2_ssd_out(static_cast<const double*>(sorted), n, static_cast<double*>(ssd));
+  else
+    return FB_ERR_DTYPE;
+  return FB_OK;
+}
+
+// The same for every filter on its own (jenks_optimization_cuda_conv, :258-289).
+int fb_jenks2_ssd_filters_host(const void* sorted, int64_t nf, int32_t n, int32_t dtype,
+                               void* ssd, int32_t nthreads) {
+  if (!sorted || !ssd) return FB_ERR_NULL;
+  if (nf < 1 || n < 1 || n > FB_JENKS2_FILTER_MAX || nf > INT32_MAX) return FB_ERR_SHAPE;
+  if (dtype != FB_DT_F32 && dtype != FB_DT_F64) return FB_ERR_DTYPE;
+  if (nthreads < 1) return FB_ERR_THREADS;
+  parallel_for(nf, nthreads, [&](int64_t b, int64_t e) {
+    for (int64_t f = b; f < e; ++f) {
+      if (dtype == FB_DT_F32)
+        jenks2_ssd_out(static_cast<const float*>(sorted) + f * n, n,
+                       static_cast<float*>(ssd) + f * n);
+      else
+        jenks2_ssd_out(static_cast<const double*>(sorted) + f * n, n,
+                       static_cast<double*>(ssd) + f * n);
+    }
+  });
   return FB_OK;
 }
 

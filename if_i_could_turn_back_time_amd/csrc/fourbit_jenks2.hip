@@ -91,7 +91,8 @@ __global__ void j2_prep(const float* __restrict__ w, float* __restrict__ keys,
   }
 }
 
-__device__ __forceinline__ double centre(const float* __restrict__ s, int n) {
+template <typename T>
+__device__ __forceinline__ double centre(const T* __restrict__ s, int n) {
   return (double)s[n / 2];
 }
 
@@ -101,8 +102,25 @@ __device__ __forceinline__ double centre(const float* __restrict__ s, int n) {
 // single-value reads would touch 64 lines per instruction for 4 bytes each).
 constexpr int kPiece = 16;
 
-// Block totals of d and q: one thread per block of kBlk sorted values.
-__global__ void j2_block_totals(const float* __restrict__ s, int n, int nblk,
+// kPiece values of T (float or double) from 16-byte aligned p, in 16-byte reads.
+template <typename T>
+__device__ __forceinline__ void load_piece(const T* __restrict__ p, T (&f)[kPiece]) {
+  constexpr int kVec = 16 / sizeof(T);
+#pragma unroll
+  for (int r = 0; r < kPiece / kVec; ++r)
+    *reinterpret_cast<uint4*>(f + kVec * r) = reinterpret_cast<const uint4*>(p)[r];
+}
+template <typename T>
+__device__ __forceinline__ void store_piece(T* __restrict__ p, const T (&f)[kPiece]) {
+  constexpr int kVec = 16 / sizeof(T);
+#pragma unroll
+  for (int r = 0; r < kPiece / kVec; ++r)
+    reinterpret_cast<uint4*>(p)[r] = *reinterpret_cast<const uint4*>(f + kVec * r);
+}
+
+// Block totals of d and q: one thread per block of kBlk sorted values (T: float or double).
+template <typename T>
+__global__ void j2_block_totals(const T* __restrict__ s, int n, int nblk,
                                 double* __restrict__ t1, double* __restrict__ t2) {
   const int b = blockIdx.x * blockDim.x + threadIdx.x;
   if (b >= nblk) return;
@@ -111,10 +129,8 @@ __global__ void j2_block_totals(const float* __restrict__ s, int n, int nblk,
   double a1 = 0.0, a2 = 0.0;
   int i = i0;
   for (; i + kPiece <= i1; i += kPiece) {
-    float f[kPiece];
-#pragma unroll
-    for (int r = 0; r < kPiece / 4; ++r)
-      *reinterpret_cast<float4*>(f + 4 * r) = reinterpret_cast<const float4*>(s + i)[r];
+    T f[kPiece];
+    load_piece(s + i, f);
 #pragma unroll
     for (int e = 0; e < kPiece; ++e) {
       const double d = (double)f[e] - c;
@@ -204,12 +220,14 @@ __global__ __launch_bounds__(kTopThreads) void j2_top(const double* __restrict__
   }
 }
 
-// The SSD of every split of one block, and the block's first minimum.
-__global__ void j2_ssd(const float* __restrict__ s, int n, int nblk, int nsup,
+// The SSD of every split of one block, and the block's first minimum; with `out`, every
+// split's SSD is also written there, rounded to T.
+template <typename T>
+__global__ void j2_ssd(const T* __restrict__ s, int n, int nblk, int nsup,
                        const double* __restrict__ bx1, const double* __restrict__ bx2,
                        const double* __restrict__ sx1, const double* __restrict__ sx2,
                        double* __restrict__ bmin, int* __restrict__ bidx,
-                       double* __restrict__ ssd0) {
+                       double* __restrict__ ssd0, T* __restrict__ out) {
   const int b = blockIdx.x * blockDim.x + threadIdx.x;
   if (b >= nblk) return;
   const double c = centre(s, n);
@@ -220,7 +238,7 @@ __global__ void j2_ssd(const float* __restrict__ s, int n, int nblk, int nsup,
   double l1 = 0.0, l2 = 0.0;
   double best = 0.0;
   int arg = -1;
-  auto step = [&](int i, float v) {
+  auto step = [&](int i, T v) -> double {
     const double p = base1 + l1, q = base2 + l2;
     const double left = i == 0 ? 0.0 : q - (p * p) / (double)i;
     const double rp = pt - p;
@@ -235,17 +253,20 @@ __global__ void j2_ssd(const float* __restrict__ s, int n, int nblk, int nsup,
     const double dq = d * d;
     l1 = l1 + d;
     l2 = l2 + dq;
+    return sv;
   };
   int i = i0;
   for (; i + kPiece <= i1; i += kPiece) {
-    float f[kPiece];
+    T f[kPiece], o[kPiece];
+    load_piece(s + i, f);
 #pragma unroll
-    for (int r = 0; r < kPiece / 4; ++r)
-      *reinterpret_cast<float4*>(f + 4 * r) = reinterpret_cast<const float4*>(s + i)[r];
-#pragma unroll
-    for (int e = 0; e < kPiece; ++e) step(i + e, f[e]);
+    for (int e = 0; e < kPiece; ++e) o[e] = (T)step(i + e, f[e]);
+    if (out) store_piece(out + i, o);
   }
-  for (; i < i1; ++i) step(i, s[i]);
+  for (; i < i1; ++i) {
+    const double sv = step(i, s[i]);
+    if (out) out[i] = (T)sv;
+  }
   bmin[b] = best;
   bidx[b] = arg;
 }
@@ -596,9 +617,167 @@ __global__ __launch_bounds__(64) void j2_filters_wave(const float* __restrict__ 
   for (int r = lane; r < n; r += 64) keep[f * n + ord[r]] = r >= arg ? 1 : 0;
 }
 
+// ---------------------------------------------------------------------------------
+// The per-split SSD of arrays that arrive sorted: the reference's jenks_optimization_cuda /
+// jenks_optimization_biases_cuda (cuda_helpers.py:151-211, :85-146) and, per filter,
+// jenks_optimization_cuda_conv (:219-289), which return var[idx] for every split and leave
+// the argmin to the caller (JenksSGD and the other optimizers, custom_optimizer.py:135-136,
+// :164-165).  The same sums as the mask path (no sort: the values are taken in the order
+// given), the SSD of each split rounded to the input's type.
+// ---------------------------------------------------------------------------------
+// Workspace of the whole-array version: the block / superblock sums of j2_block_totals,
+// j2_super, j2_top and j2_ssd (no sort buffers).
+struct J2SsdLayout {
+  int64_t nblk, nsup;
+  size_t off_t1, off_t2, off_bx1, off_bx2, off_u1, off_u2, off_sx1, off_sx2;
+  size_t off_bmin, off_bidx, off_ssd0, total;
+};
+
+J2SsdLayout j2_ssd_layout(int64_t n) {
+  J2SsdLayout L;
+  L.nblk = (n + kBlk - 1) / kBlk;
+  L.nsup = (L.nblk + kSup - 1) / kSup;
+  size_t o = 0;
+  auto take = [&](size_t bytes) {
+    const size_t at = o;
+    o = align256(o + bytes);
+    return at;
+  };
+  L.off_t1 = take(8 * (size_t)L.nblk);
+  L.off_t2 = take(8 * (size_t)L.nblk);
+  L.off_bx1 = take(8 * (size_t)L.nblk);
+  L.off_bx2 = take(8 * (size_t)L.nblk);
+  L.off_u1 = take(8 * (size_t)L.nsup);
+  L.off_u2 = take(8 * (size_t)L.nsup);
+  L.off_sx1 = take(8 * (size_t)(L.nsup + 1));
+  L.off_sx2 = take(8 * (size_t)(L.nsup + 1));
+  L.off_bmin = take(8 * (size_t)L.nblk);
+  L.off_bidx = take(4 * (size_t)L.nblk);
+  L.off_ssd0 = take(8);
+  L.total = o;
+  return L;
+}
+
+template <typename T>
+int ssd_gpu(const T* srt, int64_t n, T* out, void* ws, hipStream_t hs) {
+  const J2SsdLayout L = j2_ssd_layout(n);
+  uint8_t* base = static_cast<uint8_t*>(ws);
+  auto at = [&](size_t off) { return reinterpret_cast<double*>(base + off); };
+  const int ni = (int)n, nblk = (int)L.nblk, nsup = (int)L.nsup;
+  hipLaunchKernelGGL(j2_block_totals<T>, dim3(grid_of(nblk, 64)), dim3(64), 0, hs, srt, ni, nblk,
+                     at(L.off_t1), at(L.off_t2));
+  hipLaunchKernelGGL(j2_super, dim3(grid_of(nsup, 64)), dim3(64), 0, hs, at(L.off_t1),
+                     at(L.off_t2), nblk, nsup, at(L.off_bx1), at(L.off_bx2), at(L.off_u1),
+                     at(L.off_u2));
+  hipLaunchKernelGGL(j2_top, dim3(1), dim3(kTopThreads), 0, hs, at(L.off_u1), at(L.off_u2), nsup,
+                     at(L.off_sx1), at(L.off_sx2));
+  hipLaunchKernelGGL(j2_ssd<T>, dim3(grid_of(nblk, 64)), dim3(64), 0, hs, srt, ni, nblk, nsup,
+                     at(L.off_bx1), at(L.off_bx2), at(L.off_sx1), at(L.off_sx2), at(L.off_bmin),
+                     reinterpret_cast<int*>(base + L.off_bidx), at(L.off_ssd0), out);
+  return hipGetLastError() == hipSuccess ? FB_OK : FB_ERR_HIP;
+}
+
+// Every split's SSD of one sorted filter (n <= kFilterMax values: one superblock of at most
+// four blocks), in the host's association order (every addition it makes, zeros included).
+template <typename T>
+__device__ void filter_ssd(const T* __restrict__ srt, int n, T* __restrict__ out) {
+  const int nblk = (n + kBlk - 1) / kBlk;
+  const double c = (double)srt[n / 2];
+  double t1[4], t2[4], bx1[4], bx2[4];
+  for (int b = 0; b < nblk; ++b) {
+    double a1 = 0.0, a2 = 0.0;
+    for (int i = b * kBlk; i < min(n, b * kBlk + kBlk); ++i) {
+      const double d = (double)srt[i] - c;
+      const double q = d * d;
+      a1 = a1 + d;
+      a2 = a2 + q;
+    }
+    t1[b] = a1;
+    t2[b] = a2;
+  }
+  double u1, u2;
+  {
+    double a1 = 0.0, a2 = 0.0;
+    for (int b = 0; b < nblk; ++b) {
+      bx1[b] = a1;
+      bx2[b] = a2;
+      a1 = a1 + t1[b];
+      a2 = a2 + t2[b];
+    }
+    u1 = a1;
+    u2 = a2;
+  }
+  const double sx1 = 0.0, sx2 = 0.0;
+  const double pt = 0.0 + u1, qt = 0.0 + u2;
+  for (int b = 0; b < nblk; ++b) {
+    const double base1 = sx1 + bx1[b], base2 = sx2 + bx2[b];
+    double l1 = 0.0, l2 = 0.0;
+    for (int i = b * kBlk; i < min(n, b * kBlk + kBlk); ++i) {
+      const double p = base1 + l1, q = base2 + l2;
+      const double left = i == 0 ? 0.0 : q - (p * p) / (double)i;
+      const double rp = pt - p;
+      const double right = (qt - q) - (rp * rp) / (double)(n - i);
+      out[i] = (T)(left + right);
+      const double d = (double)srt[i] - c;
+      const double dq = d * d;
+      l1 = l1 + d;
+      l2 = l2 + dq;
+    }
+  }
+}
+
+// One thread per filter (as the reference's conv kernel runs one per (in, out) pair).
+template <typename T>
+__global__ __launch_bounds__(256) void j2_ssd_filters(const T* __restrict__ srt, int64_t nf,
+                                                      int n, T* __restrict__ out) {
+  const int64_t f = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (f < nf) filter_ssd(srt + f * n, n, out + f * n);
+}
+
 }  // namespace
 
 extern "C" {
+
+int fb_jenks2_ssd_workspace(int64_t n, size_t* bytes) {
+  if (!bytes) return FB_ERR_NULL;
+  if (n < 1 || n > INT32_MAX) return FB_ERR_SHAPE;
+  *bytes = j2_ssd_layout(n).total;
+  return FB_OK;
+}
+
+int fb_jenks2_ssd_gpu(const void* sorted, int64_t n, int32_t dtype, void* ssd, void* ws,
+                      size_t ws_bytes, void* stream) {
+  if (!sorted || !ssd || !ws) return FB_ERR_NULL;
+  if (n < 1 || n > INT32_MAX) return FB_ERR_SHAPE;
+  if (dtype != FB_DT_F32 && dtype != FB_DT_F64) return FB_ERR_DTYPE;
+  if ((reinterpret_cast<uintptr_t>(sorted) & 15u) || (reinterpret_cast<uintptr_t>(ssd) & 15u) ||
+      (reinterpret_cast<uintptr_t>(ws) & 255u))
+    return FB_ERR_ALIGN;
+  if (ws_bytes < j2_ssd_layout(n).total) return FB_ERR_WORKSPACE;
+  hipStream_t hs = static_cast<hipStream_t>(stream);
+  if (dtype == FB_DT_F32)
+    return ssd_gpu(static_cast<const float*>(sorted), n, static_cast<float*>(ssd), ws, hs);
+  return ssd_gpu(static_cast<const double*>(sorted), n, static_cast<double*>(ssd), ws, hs);
+}
+
+int fb_jenks2_ssd_filters_gpu(const void* sorted, int64_t nf, int32_t n, int32_t dtype, void* ssd,
+                              void* stream) {
+  if (!sorted || !ssd) return FB_ERR_NULL;
+  if (nf < 1 || n < 1 || n > FB_JENKS2_FILTER_MAX || nf > INT32_MAX) return FB_ERR_SHAPE;
+  if (dtype != FB_DT_F32 && dtype != FB_DT_F64) return FB_ERR_DTYPE;
+  const uintptr_t a = dtype == FB_DT_F32 ? 3u : 7u;
+  if ((reinterpret_cast<uintptr_t>(sorted) & a) || (reinterpret_cast<uintptr_t>(ssd) & a))
+    return FB_ERR_ALIGN;
+  hipStream_t hs = static_cast<hipStream_t>(stream);
+  const dim3 grid((unsigned)((nf + 255) / 256));
+  if (dtype == FB_DT_F32)
+    hipLaunchKernelGGL(j2_ssd_filters<float>, grid, dim3(256), 0, hs,
+                       static_cast<const float*>(sorted), nf, (int)n, static_cast<float*>(ssd));
+  else
+    hipLaunchKernelGGL(j2_ssd_filters<double>, grid, dim3(256), 0, hs,
+                       static_cast<const double*>(sorted), nf, (int)n, static_cast<double*>(ssd));
+  return hipGetLastError() == hipSuccess ? FB_OK : FB_ERR_HIP;
+}
 
 int fb_jenks2_workspace(int64_t n, size_t* bytes) {
   if (!bytes) return FB_ERR_NULL;
@@ -643,13 +822,13 @@ int fb_jenks2_gpu(const float* w, int64_t n, uint8_t* keep, int64_t* split, doub
   if (hipcub::DeviceRadixSort::SortPairs(at(L.off_sort), sb, keys_in, keys_out, vals_in, vals_out,
                                          ni, 0, 32, hs) != hipSuccess)
     return FB_ERR_HIP;
-  hipLaunchKernelGGL(j2_block_totals, dim3(grid_of(nblk, 64)), dim3(64), 0, hs, keys_out, ni, nblk,
-                     t1, t2);
+  hipLaunchKernelGGL(j2_block_totals<float>, dim3(grid_of(nblk, 64)), dim3(64), 0, hs, keys_out, ni,
+                     nblk, t1, t2);
   hipLaunchKernelGGL(j2_super, dim3(grid_of(nsup, 64)), dim3(64), 0, hs, t1, t2, nblk, nsup, bx1,
                      bx2, u1, u2);
   hipLaunchKernelGGL(j2_top, dim3(1), dim3(kTopThreads), 0, hs, u1, u2, nsup, sx1, sx2);
-  hipLaunchKernelGGL(j2_ssd, dim3(grid_of(nblk, 64)), dim3(64), 0, hs, keys_out, ni, nblk, nsup,
-                     bx1, bx2, sx1, sx2, bmin, bidx, ssd0);
+  hipLaunchKernelGGL(j2_ssd<float>, dim3(grid_of(nblk, 64)), dim3(64), 0, hs, keys_out, ni, nblk,
+                     nsup, bx1, bx2, sx1, sx2, bmin, bidx, ssd0, (float*)nullptr);
   hipLaunchKernelGGL(j2_min_super, dim3(nsup), dim3(64), 0, hs, bmin, bidx, nblk, nsup, smin,
                      sidx);
   hipLaunchKernelGGL(j2_final, dim3(1), dim3(kFinalThreads), 0, hs, smin, sidx, nsup, ssd0, split,

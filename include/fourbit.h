@@ -49,7 +49,8 @@ typedef enum {
 } fb_status;
 
 typedef enum { FB_FMT_GF4 = 0, FB_FMT_E2M1 = 1 } fb_fmt;
-typedef enum { FB_DT_F16 = 0, FB_DT_BF16 = 1, FB_DT_F32 = 2 } fb_dtype;
+/* FB_DT_F64 is taken by the per-split SSD entry points (fb_jenks2_ssd_*) only. */
+typedef enum { FB_DT_F16 = 0, FB_DT_BF16 = 1, FB_DT_F32 = 2, FB_DT_F64 = 3 } fb_dtype;
 
 /* One quantized linear layer: y[B,N] = x[B,K] . W[N,K]^T. */
 typedef struct {
@@ -312,6 +313,49 @@ int fb_jenks2_filters_host(const float* w, int64_t nf, int32_t n, uint8_t* keep,
  * host version rejects them with FB_ERR_VALUE). */
 int fb_jenks2_filters_gpu(const float* w, int64_t nf, int32_t n, uint8_t* keep, int32_t* split,
                           double* gvf, void* stream);
+
+/* ---------------------------------------------------------------------------------
+ * The per-split SSD of arrays that arrive sorted, the interface the reference's optimizers
+ * bind directly: var = module_weights.jenks_optimization_cuda(sorted) and
+ * module_bias.jenks_optimization_biases_cuda(sorted), then var.argmin()
+ * (Python_Jenks_Test/Jenks_Tests/custom_optimizer.py:135-136, :164-165 and 20 more sites),
+ * over the kernels at cuda_helpers.py:151-211 and :85-146 (one thread per split, each
+ * summing both classes serially: O(n^2)).  Here the prefix-sum rule of fb_jenks2_host, in
+ * O(n), without its sort (the values are taken in the order given, as the reference's
+ * kernels take them):
+ *   sorted  fp32 or fp64 [n] (dtype FB_DT_F32 / FB_DT_F64), ascending as the caller sorted it
+ *   ssd     [n] of the same dtype: ssd[i] = the within-class SSD of [0, i) plus that of
+ *           [i, n) (i = 0: one class), fp64 sums in fb_jenks2_host's order, rounded to dtype
+ * The reference's own serial fp32 (or fp64) two-pass sums round differently: values agree
+ * to within that rounding (about 1e-5 of ssd[0] in fp32), and argmin agrees wherever the
+ * minimum is not a near-tie.  Non-finite values give non-finite SSDs, as the reference's
+ * do.  1 <= n <= 2^31 - 1.
+ * ------------------------------------------------------------------------------- */
+int fb_jenks2_ssd_host(const void* sorted, int64_t n, int32_t dtype, void* ssd);
+
+/* Device workspace bytes fb_jenks2_ssd_gpu needs for n values (host-side arithmetic). */
+int fb_jenks2_ssd_workspace(int64_t n, size_t* bytes);
+
+/* GPU version of fb_jenks2_ssd_host, bit-identical.  sorted, ssd (16-byte aligned) and ws
+ * (256-byte aligned, at least fb_jenks2_ssd_workspace(n) bytes) are device pointers;
+ * asynchronous on the stream (the reference synchronises the device after its launch). */
+int fb_jenks2_ssd_gpu(const void* sorted, int64_t n, int32_t dtype, void* ssd, void* ws,
+                      size_t ws_bytes, void* stream);
+
+/* The same per filter: module_conv.jenks_optimization_cuda_conv(sorted) (cuda_helpers.py:
+ * 258-289 over the kernel at :219-255, called from Conv_Mask :356), whose input is an
+ * [C0, C1, kh, kw] weight with each (c0, c1) filter's kh*kw values sorted, and whose output
+ * is the SSD of every split of every filter, flat [C0*C1*kh*kw] in the same order.
+ *   sorted  [nf, n] (nf = C0*C1 filters of n = kh*kw values), ssd [nf, n], same dtype;
+ *   each filter's row is bit for bit fb_jenks2_ssd_host of that filter alone.
+ * 1 <= n <= FB_JENKS2_FILTER_MAX, 1 <= nf < 2^31. */
+int fb_jenks2_ssd_filters_host(const void* sorted, int64_t nf, int32_t n, int32_t dtype,
+                               void* ssd, int32_t nthreads);
+
+/* GPU version, bit-identical to fb_jenks2_ssd_filters_host: one thread per filter, no
+ * workspace.  Device pointers aligned to the dtype's size; asynchronous on the stream. */
+int fb_jenks2_ssd_filters_gpu(const void* sorted, int64_t nf, int32_t n, int32_t dtype,
+                              void* ssd, void* stream);
 
 #ifdef __cplusplus
 }

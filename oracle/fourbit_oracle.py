@@ -120,7 +120,30 @@ def jenks2(values: np.ndarray):
     if n < 1 or not np.isfinite(w).all():
         raise ValueError("need a non-empty finite array")
     order = np.argsort(w, kind="stable")          # -0.0 == +0.0 under <
-    srt = w[order]
+    ssd = jenks2_ssd(w[order])
+    split = int(np.argmin(ssd))                               # first minimum
+    keep = np.zeros(n, bool)
+    keep[order[split:]] = True
+    gvf = (ssd[0] - ssd[split]) / (ssd[0] + 1e-8)
+    return keep, split, float(gvf), ssd
+
+
+def jenks2_ssd(srt: np.ndarray) -> np.ndarray:
+    """The within-class SSD of every split ``idx`` in ``[0, n)`` of an array taken in the
+    order given (the caller sorts it), float64 ``[n]``: what the reference's
+    ``jenks_optimization_cuda`` / ``jenks_optimization_biases_cuda`` return per split
+    (``cuda_helpers.py:151-211``, ``:85-146``): class ``[0, idx)`` about its mean plus class
+    ``[idx, n)`` about its own, ``idx = 0`` being one class.  float32 or float64 values
+    (float64 ones are used as they are); the sums in the build's fixed fp64 order (centre
+    c = srt[n // 2]; prefix sums sequential in blocks of 256, block totals sequential in
+    superblocks of 256 blocks, superblock totals sequential):
+    ``ssd(i) = [i ? Q(i) - P(i)^2 / i : 0] + [(Qt - Q(i)) - (Pt - P(i))^2 / (n - i)]``."""
+    srt = np.asarray(srt).reshape(-1)
+    if srt.dtype not in (np.float32, np.float64):
+        srt = srt.astype(np.float32)
+    n = srt.size
+    if n < 1:
+        raise ValueError("need a non-empty array")
     c = np.float64(srt[n // 2])
     d = srt.astype(np.float64) - c
     q = d * d
@@ -151,12 +174,7 @@ def jenks2(values: np.ndarray):
         left = np.where(i == 0, 0.0, Q - (P * P) / i)
     rp = Pt - P
     right = (Qt - Q) - (rp * rp) / (n - i)
-    ssd = left + right
-    split = int(np.argmin(ssd))                               # first minimum
-    keep = np.zeros(n, bool)
-    keep[order[split:]] = True
-    gvf = (ssd[0] - ssd[split]) / (ssd[0] + 1e-8)
-    return keep, split, float(gvf), ssd
+    return left + right
 
 
 def jenks2_filters(w: np.ndarray):

@@ -164,6 +164,28 @@ int main(void) {
     free(split);
     free(gvf);
   }
+  /* the per-split SSD of sorted arrays, fp32 and fp64, whole and per filter */
+  for (size_t i = 0; i < sizeof(sizes) / sizeof(sizes[0]); ++i) {
+    const int64_t n = sizes[i];
+    float* w = malloc(sizeof(float) * n);
+    float* ssd = malloc(sizeof(float) * n);
+    double* wd = malloc(sizeof(double) * n);
+    double* ssdd = malloc(sizeof(double) * n);
+    fill(w, n, (int)(i % 4));
+    for (int64_t j = 0; j < n; ++j) wd[j] = w[j];
+    CHECK(fb_jenks2_ssd_host(w, n, FB_DT_F32, ssd) == FB_OK);
+    CHECK(fb_jenks2_ssd_host(wd, n, FB_DT_F64, ssdd) == FB_OK);
+    for (int64_t j = 0; j < n; ++j) CHECK(ssd[j] == (float)ssdd[j]);
+    if (n <= FB_JENKS2_FILTER_MAX) {
+      CHECK(fb_jenks2_ssd_filters_host(wd, 1, (int32_t)n, FB_DT_F64, ssdd, 2) == FB_OK);
+      CHECK(fb_jenks2_ssd_filters_host(w, 1, (int32_t)n, FB_DT_F32, ssd, 1) == FB_OK);
+      for (int64_t j = 0; j < n; ++j) CHECK(ssd[j] == (float)ssdd[j]);
+    }
+    free(w);
+    free(ssd);
+    free(wd);
+    free(ssdd);
+  }
   /* errors are reported, not crashed on */
   float bad[2] = {1.0f, NAN};
   uint8_t k2[2];

@@ -449,6 +449,51 @@ def test_jenks2_matches_reference_kernel_arithmetic():
         assert np.isclose(gvf, (var64[0] - var64.min()) / (var64[0] + 1e-8), rtol=1e-9)
 
 
+def _reference_var_f64(v):
+    """The SSD of every split as the reference's kernels compute it (cuda_helpers.py:85-118
+    biases, :151-184 weights, :232-253 per conv filter: the class means from serial sums,
+    then the serial sum of squared deviations), in float64."""
+    v = np.asarray(v, np.float64)
+    n = v.size
+    var = np.zeros(n)
+    for idx in range(n):
+        m1 = v[:idx].sum() / idx if idx else 0.0
+        m2 = v[idx:].sum() / (n - idx)
+        var[idx] = ((v[:idx] - m1) ** 2).sum() + ((v[idx:] - m2) ** 2).sum()
+    return var
+
+
+def test_jenks2_ssd_per_split_matches_reference_kernels():
+    """jenks2_ssd, the per-split SSD vector of a pre-sorted array (what
+    jenks_optimization_cuda / jenks_optimization_biases_cuda return), against the
+    reference kernels' two-pass arithmetic: in float64 on float32 and float64 inputs (to
+    1e-9 of the total SSD), and against the kernels' own float32 arithmetic (to 1e-5 of
+    it); the first argmin is the reference's split wherever the minimum is not a near-tie.
+    Across the 256-value block edge too (n up to 600)."""
+    for dt in (np.float32, np.float64):
+        for n in (1, 2, 3, 17, 255, 256, 257, 600):
+            w = (RNG.standard_t(3, size=n) * 0.05).astype(dt)
+            v = np.sort(w, kind="stable")
+            ssd = O.jenks2_ssd(v)
+            assert ssd.dtype == np.float64 and ssd.shape == (n,)
+            ref = _reference_var_f64(v)
+            assert np.allclose(ssd, ref, rtol=0, atol=1e-9 * ref[0] + 1e-18), (dt, n)
+            if dt == np.float32 and n <= 257:
+                _, var32 = _reference_k2_split_fp32(v)
+                assert np.allclose(ssd, var32, rtol=0, atol=1e-5 * ref[0] + 1e-12), n
+            srt = np.sort(ref)
+            if n == 1 or srt[1] - srt[0] > 1e-6 * srt[0]:
+                assert int(np.argmin(ssd)) == int(np.argmin(ref))
+    # split 0 is the whole array's SSD; the last split leaves one value on the right
+    v = np.array([-1.0, 0.0, 2.0, 7.0])
+    ssd = O.jenks2_ssd(v)
+    assert ssd[0] == ((v - v.mean()) ** 2).sum()
+    assert np.isclose(ssd[3], ((v[:3] - v[:3].mean()) ** 2).sum(), rtol=1e-15)
+    # the array is taken in the order given (no re-sort), as the reference kernels take it
+    u = np.array([3.0, -2.0, 0.5, 0.5, 9.0])
+    assert np.allclose(O.jenks2_ssd(u), _reference_var_f64(u), rtol=0, atol=1e-12)
+
+
 def test_jenks2_brute_force_over_all_two_way_partitions():
     """For n <= 10, every partition of the values into two sets (one may be empty): the
     minimum within-class SSD is the one at the chosen split, so the optimum is contiguous
