@@ -446,6 +446,12 @@ def test_gpu_packer_bit_exact_vs_host(density):
     torch.cuda.synchronize()
     assert torch.equal(dc.cpu(), hc)
     assert torch.equal(db.cpu(), hb)
+    # and the oracle's bytes on the same weights
+    wn = w.numpy()
+    oc, ob = (O.gf4_quantize(wn) if keep is None
+              else O.gf4_quantize_masked(wn, keep.numpy()))
+    assert np.array_equal(O.unpack_nibbles(dc.cpu().numpy()), oc)
+    assert np.array_equal(db.cpu().numpy().view(np.uint16), ob)
 
 
 def test_gpu_packer_rejects_nonfinite():
@@ -555,3 +561,6 @@ def test_gpu_e2m1_packer_bit_exact_vs_host():
     torch.cuda.synchronize()
     assert torch.equal(dc.cpu(), hc)
     assert torch.equal(ds.cpu(), hs)
+    oc, osc = O.e2m1_quantize(w.numpy())
+    assert np.array_equal(O.unpack_nibbles(dc.cpu().numpy()), oc)
+    assert np.array_equal(ds.cpu().numpy(), osc)
