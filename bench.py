@@ -79,13 +79,13 @@ def time_gpu(pw: PackedWeight, x: torch.Tensor, y: torch.Tensor, steps: int, war
     wps = [c.data_ptr() for c in copies]
     xp, yp = x.data_ptr(), y.data_ptr()
     if mx == "split":
-        ws = torch.empty(C.mx_workspace_bytes(shape), dtype=torch.uint8, device=x.device)
+        ws = torch.zeros(C.mx_workspace_bytes(shape), dtype=torch.uint8, device=x.device)
         gemv = L.fb_gemv_mx
     elif mx == "presplit":
         xsplit = C.mx_split_raw(x, shape)
         xp = xsplit.data_ptr()
         nws = L.fb_mx_presplit_workspace_bytes(sref)
-        ws = torch.empty(nws, dtype=torch.uint8, device=x.device) if nws else None
+        ws = torch.zeros(nws, dtype=torch.uint8, device=x.device) if nws else None
         gemv = L.fb_gemv_mx_presplit
     else:
         ws = C.new_workspace(shape, x.device)
@@ -363,21 +363,26 @@ PHASES = {  # lane index in the diagnostic build's per-wave record -> phase
 }
 
 
-def phase_trace(name: str, calls: int, packer: str) -> dict:
+def phase_trace(name: str, calls: int, packer: str, parts: int = 0) -> dict:
     """Per-wave phase timestamps of the GEMV on workload ``name``, from the diagnostic copy
     of the library (``libfourbit_trace.so``, built with FB_PHASE_TRACE: each wave records a
     100 MHz chip-wide clock at fixed points of the kernel).  ``calls`` traced calls run back
     to back after the usual warm-up, on cold weight copies; times are relative to the
     call's first wave start.  Also: each workgroup's end (its last wave's), grouped by the
     XCD it ran on, and the gap between one call's last end and the next call's first
-    start."""
+    start.  ``parts`` (2, 4, 8; -1 = none) forces the split-K part count of batch >= 2
+    calls in the diagnostic library (0: its own choice); a split-K call's second kernel
+    (the part sum) is not traced."""
     tl = ctypes.CDLL(str(ROOT / "if_i_could_turn_back_time_amd" / "libfourbit_trace.so"))
     vp = ctypes.c_void_p
     tl.fb_gemv.restype = ctypes.c_int
     tl.fb_gemv.argtypes = [vp, vp, vp, ctypes.POINTER(C.FbShape), vp, ctypes.c_size_t, vp]
     tl.fb_phase_trace_set.argtypes = [vp, ctypes.c_size_t]
     ip = ctypes.POINTER(ctypes.c_int)
-    tl.fb_phase_plan.argtypes = [ctypes.POINTER(C.FbShape), ip, ip, ip, ip, ip]
+    tl.fb_phase_plan.argtypes = [ctypes.POINTER(C.FbShape), ip, ip, ip, ip, ip, ip]
+    tl.fb_workspace_bytes.restype = ctypes.c_size_t
+    tl.fb_workspace_bytes.argtypes = [ctypes.POINTER(C.FbShape)]
+    C.check(tl.fb_phase_force_parts(parts))
     fmt, K, N, B, kind, fwht = WORKLOADS[name]
     xdt = torch.float16 if fmt in ("gf4", "int4ref") else torch.bfloat16
     w, x = workloads.synth(kind, N, K, B, xdt)
@@ -390,19 +395,22 @@ def phase_trace(name: str, calls: int, packer: str) -> dict:
     xd = x.to("cuda:0")
     y = torch.empty(B, N, dtype=xdt, device="cuda:0")
     shape = pw.shape(B, xd.dtype, y.dtype)
-    ws = C.new_workspace(shape, xd.device)
+    need = tl.fb_workspace_bytes(ctypes.byref(shape))  # the diagnostic library's plan
+    ws = torch.zeros(need, dtype=torch.uint8, device=xd.device) if need else None
     wsp, nws = (ws.data_ptr(), ws.numel()) if ws is not None else (None, 0)
-    # with a workspace the GEMV runs unrotated on the rotated x: that is the plan traced
-    launched = C.make_shape(N, K, B, pw.fmt, 0 if ws is not None else fb,
+    # with a workspace a rotated GEMV runs unrotated on the rotated x: that is the plan traced
+    rot_once = ws is not None and fb and B * K >= 16384
+    launched = C.make_shape(N, K, B, pw.fmt, 0 if rot_once else fb,
                             C.DTYPE_CODE[xd.dtype], C.DTYPE_CODE[y.dtype])
-    plan = [ctypes.c_int() for _ in range(5)]
+    plan = [ctypes.c_int() for _ in range(6)]
     C.check(tl.fb_phase_plan(ctypes.byref(launched), *[ctypes.byref(v) for v in plan]))
-    grid, nw, S, tq, tr = (v.value for v in plan)
+    grid, nw, S, tq, tr, P = (v.value for v in plan)
+    wgs = grid * max(1, P)  # workgroups per call
     ncp = n_copies(pw.wdev.numel(), True)
     copies = [pw.wdev] + [pw.wdev.clone() for _ in range(ncp - 1)]
     sref = ctypes.byref(shape)
     sp = torch.cuda.current_stream().cuda_stream
-    per_call = grid * nw * 64
+    per_call = wgs * nw * 64
     bufs = torch.zeros(calls, per_call, dtype=torch.int64, device="cuda:0")
 
     def run(f, n, traced=False):
@@ -431,7 +439,8 @@ def phase_trace(name: str, calls: int, packer: str) -> dict:
     torch.cuda.synchronize()
     us_traced_lib = timed(tl.fb_gemv)
     us_product = timed(C.lib().fb_gemv)
-    t = bufs.cpu().numpy().astype(np.int64).reshape(calls, grid, nw, 64)
+    C.check(tl.fb_phase_force_parts(0))
+    t = bufs.cpu().numpy().astype(np.int64).reshape(calls, wgs, nw, 64)
     del bufs, copies
     start = t[..., 0]
     g0 = start.reshape(calls, -1).min(axis=1)[:, None, None]
@@ -458,8 +467,9 @@ def phase_trace(name: str, calls: int, packer: str) -> dict:
     period = [us(start[c + 1].min() - start[c].min()) for c in range(calls - 1)]
     return {
         "phase_trace": name, "calls": calls, "plan": {"grid": grid, "waves": nw, "slices": S,
-                                                      "tiles_per_wg": tq, "wgs_with_one_more": tr},
-        "rotate_once": ws is not None,
+                                                      "tiles_per_wg": tq, "wgs_with_one_more": tr,
+                                                      "splitk_parts": P},
+        "rotate_once": bool(rot_once),
         "us_per_call_untraced": round(us_product, 3), "us_per_call_trace_build": round(us_traced_lib, 3),
         "phases_us_from_call_start": phases,
         "workgroup_end_us": dict(stats(wg_end), p10=round(float(np.percentile(wg_end, 10)), 3),
@@ -579,6 +589,107 @@ def jenks2_filters_bench(shape, steps: int) -> dict:
             "identical_to_host": bool(same)}
 
 
+FLOOR_WORKLOADS = ("gf4_k4096_n4096_b1", "e2m1_k4096_n4096_b1", "e2m1_k4096_n11008_b1",
+                   "e2m1_k11008_n4096_b1", "gf4fwht_k4096_n4096_b1", "gf4fwht_k4096_n11008_b1",
+                   "gf4fwht_k11008_n4096_b1", "gf4_k8192_n28672_b1")
+
+
+def floor_bench(names, steps: int, regions: int = 10) -> list:
+    """The launch floor of each batch-1 workload's plan: an empty kernel with the GEMV's
+    grid, waves, LDS, register count and argument block (fb_phase_floor of the diagnostic
+    library), launched back to back, against the product GEMV launched the same way (cold:
+    weight copies cycled).  Each is timed twice: launched from Python one call at a time
+    (host launch work included, as in the default bench), and replayed from a HIP graph of
+    ``steps`` launches (the device's own cost per launch).  Median µs per call over
+    ``regions`` regions, HIP events on the launch stream."""
+    tl = ctypes.CDLL(str(ROOT / "if_i_could_turn_back_time_amd" / "libfourbit_trace.so"))
+    vp = ctypes.c_void_p
+    tl.fb_phase_floor.argtypes = [ctypes.POINTER(C.FbShape), vp]
+    tl.fb_phase_floor.restype = ctypes.c_int
+    out = []
+    for name in names:
+        fmt, K, N, B, kind, fwht = WORKLOADS[name]
+        xdt = torch.float16 if fmt == "gf4" else torch.bfloat16
+        w, x = workloads.synth(kind, N, K, B, xdt)
+        fb = fwht_block_for(K) if fwht else 0
+        pw = PackedWeight.quantize(w, fmt, fwht_block=fb, device="cuda:0", packer="gpu")
+        xd = x.to("cuda:0")
+        y = torch.empty(B, N, dtype=xdt, device="cuda:0")
+        shape = pw.shape(B, xd.dtype, y.dtype)
+        sref = ctypes.byref(shape)
+        stream = torch.cuda.current_stream()
+        sp = stream.cuda_stream
+        for _ in range(2000):  # warm-up past the clock ramp
+            C.check(tl.fb_phase_floor(sref, sp))
+        torch.cuda.synchronize()
+        floor = []
+        for _ in range(regions):
+            e0 = torch.cuda.Event(enable_timing=True)
+            e1 = torch.cuda.Event(enable_timing=True)
+            for _ in range(PRE_CALLS):
+                tl.fb_phase_floor(sref, sp)
+            e0.record(stream)
+            for _ in range(steps):
+                tl.fb_phase_floor(sref, sp)
+            e1.record(stream)
+            torch.cuda.synchronize()
+            floor.append(e0.elapsed_time(e1) / steps * 1e3)
+        first, _, extra = time_gpu(pw, xd, y, steps, 50, cold=True, windows=regions - 1)
+        gemv = [v * 1e3 for v in [first] + extra]
+        # the same launches replayed from a HIP graph: no host work per launch
+        ncp = n_copies(pw.wdev.numel(), True)
+        copies = [pw.wdev] + [pw.wdev.clone() for _ in range(ncp - 1)]
+        L = C.lib()
+        g_floor, g_gemv = torch.cuda.CUDAGraph(), torch.cuda.CUDAGraph()
+        side = torch.cuda.Stream()
+        side.wait_stream(stream)
+        with torch.cuda.stream(side):
+            C.check(L.fb_gemv(copies[0].data_ptr(), xd.data_ptr(), y.data_ptr(), sref, None, 0,
+                              side.cuda_stream))
+            torch.cuda.synchronize()
+            with torch.cuda.graph(g_floor, stream=side):
+                for _ in range(steps):
+                    C.check(tl.fb_phase_floor(sref, side.cuda_stream))
+            with torch.cuda.graph(g_gemv, stream=side):
+                for i in range(steps):
+                    C.check(L.fb_gemv(copies[i % ncp].data_ptr(), xd.data_ptr(), y.data_ptr(),
+                                      sref, None, 0, side.cuda_stream))
+        torch.cuda.synchronize()
+
+        def replay(gr):
+            vals = []
+            for _ in range(3):
+                gr.replay()
+            torch.cuda.synchronize()
+            for _ in range(regions):
+                e0 = torch.cuda.Event(enable_timing=True)
+                e1 = torch.cuda.Event(enable_timing=True)
+                e0.record(stream)
+                gr.replay()
+                e1.record(stream)
+                torch.cuda.synchronize()
+                vals.append(e0.elapsed_time(e1) / steps * 1e3)
+            return vals
+
+        floor_g, gemv_g = replay(g_floor), replay(g_gemv)
+        del g_floor, g_gemv, copies
+        nbytes = pw.algorithmic_bytes(B)
+        f_med, g_med = float(np.median(floor)), float(np.median(gemv))
+        fg_med, gg_med = float(np.median(floor_g)), float(np.median(gemv_g))
+        out.append({"workload": name, "bytes_per_call": nbytes,
+                    "floor_us_per_call_median": f_med, "floor_us_per_call_regions": floor,
+                    "gemv_us_per_call_median": g_med, "gemv_us_per_call_regions": gemv,
+                    "graph_floor_us_per_call_median": fg_med,
+                    "graph_gemv_us_per_call_median": gg_med,
+                    "graph_floor_us_per_call_regions": floor_g,
+                    "graph_gemv_us_per_call_regions": gemv_g,
+                    "GBps_eager": nbytes / (g_med * 1e-6) / 1e9,
+                    "GBps_graph": nbytes / (gg_med * 1e-6) / 1e9})
+        del pw, xd, y
+        torch.cuda.empty_cache()
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -600,12 +711,18 @@ def main():
     ap.add_argument("--phase-trace", action="store_true",
                     help="only trace the GEMV's phases on --workload (diagnostic library) and "
                          "print a JSON summary")
+    ap.add_argument("--parts", type=int, default=0,
+                    help="with --phase-trace: force the split-K part count (2, 4, 8; -1 none)")
     ap.add_argument("--jenks2", type=int, default=0, metavar="N",
                     help="only time the two-class Jenks mask (fb_jenks2_gpu) over N values")
     ap.add_argument("--mx", action="store_true",
                     help="only compare the native FP4 path (fb_gemv_mx) with the exact-decode "
                          "path on every unrotated E2M1 workload (or --workload, if it is one), "
                          "one JSON line per path")
+    ap.add_argument("--floor", action="store_true",
+                    help="only time the launch floor (an empty kernel with each batch-1 "
+                         "workload's plan) against the GEMV, one JSON line per workload "
+                         "(--workload narrows it to one)")
     ap.add_argument("--jenks2-filters", default="", metavar="OUT,IN,KH,KW",
                     help="only time the per-filter Jenks mask (fb_jenks2_filters_gpu) on a "
                          "convolution weight of that shape")
@@ -629,10 +746,16 @@ def main():
         print("bench.py: no ROCm GPU visible", file=sys.stderr)
         sys.exit(1)
     if args.phase_trace:
-        print(json.dumps(phase_trace(args.workload, 20, args.packer)))
+        print(json.dumps(phase_trace(args.workload, 20, args.packer, args.parts)))
         return
     if args.jenks2:
         print(json.dumps(jenks2_bench(args.jenks2, min(args.steps, 50))))
+        return
+    if args.floor:
+        names = [args.workload] if args.workload in FLOOR_WORKLOADS and "--workload" in sys.argv \
+            else list(FLOOR_WORKLOADS)
+        for rec in floor_bench(names, min(args.steps, 400)):
+            print(json.dumps(rec), flush=True)
         return
     if args.mx:
         names = [n for n in sorted(WORKLOADS) if WORKLOADS[n][0] == "e2m1" and not WORKLOADS[n][5]]

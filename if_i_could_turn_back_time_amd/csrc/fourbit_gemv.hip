@@ -290,8 +290,8 @@ __device__ void stage_plain(uint8_t* lds, const XPre<XP>& xp, rsrc_t xrs, int K,
 // libfourbit_trace.so): lane i of each wave keeps the s_memrealtime value (a 100 MHz
 // clock common to the chip) at which the wave passed phase i; at the end of the kernel each
 // wave writes its 64 values to the buffer given to fb_phase_trace_set, at
-// ((blockIdx.x * NW + wave) * 64 + lane).  Lane 16 holds the XCC (XCD) id and lane 17 the
-// slice count.  Each mark waits for the wave's outstanding LDS and scalar operations (the
+// (((blockIdx.y * gridDim.x + blockIdx.x) * NW + wave) * 64 + lane).  Lane 16 holds the XCC
+// (XCD) id and lane 17 the slice count.  Each mark waits for the wave's outstanding LDS and scalar operations (the
 // counter read goes through the scalar memory path), so traced timings run a little long.
 // ---------------------------------------------------------------------------------
 enum {
@@ -311,7 +311,8 @@ struct Phases {
   __device__ __forceinline__ void mark(int i) { put(i, __builtin_amdgcn_s_memrealtime()); }
   __device__ __forceinline__ void flush(int nw, unsigned long long* buf) {
     put(kPhXcc, __builtin_amdgcn_s_getreg(20 | (15 << 11)));  // HW_REG_XCC_ID
-    const size_t i = ((size_t)blockIdx.x * nw + (threadIdx.x >> 6)) * 64 + (threadIdx.x & 63);
+    const size_t wg = (size_t)blockIdx.y * gridDim.x + blockIdx.x;  // split-K: part-major
+    const size_t i = (wg * nw + (threadIdx.x >> 6)) * 64 + (threadIdx.x & 63);
     if (buf) buf[i] = ((unsigned long long)hi << 32) | lo;
   }
 };
@@ -1334,15 +1335,30 @@ bool make_plan(const fb_shape_t* s, int cus, Plan& pl) {
 // per workgroup (8192 -> 8192, 8192 -> 28672 at batch 8/16) up to 8 us slower.  P: the
 // sliced plan's slice count rounded up to a power of two (at most 8), if its LDS fits.
 // 0 where it does not apply.
+#if defined(FB_PHASE_TRACE) && !defined(FB_GEMV_ILP_TU)
+// Diagnostic library only: a part count that overrides the choice below (fb_phase_force_parts;
+// 0 = the library's own choice, -1 = never, 2 / 4 / 8 = that many parts for every unrotated
+// batch >= 2 whose plan fits).
+std::atomic<int> g_force_parts{0};
+int forced_parts() { return g_force_parts.load(std::memory_order_relaxed); }
+#else
+constexpr int forced_parts() { return 0; }
+#endif
+
 int splitk_parts(const fb_shape_t* s, int cus, Plan* out) {
-  if (s->fwht_block || s->B < 2 || s->K < 10240) return 0;
-  Plan std_pl;
-  if (!make_plan(s, cus, std_pl) || std_pl.S < 3) return 0;
+  const int forced = forced_parts();
+  if (forced < 0 || s->fwht_block || s->B < 2) return 0;
   const int GS = (s->K / 128 + 3) / 4;
   const int T = (s->N + 15) / 16;
-  if ((T + std_pl.grid - 1) / std_pl.grid > 2) return 0;
-  int P = 2;
-  while (P < std_pl.S) P *= 2;
+  int P = forced;
+  if (!P) {
+    if (s->K < 10240) return 0;
+    Plan std_pl;
+    if (!make_plan(s, cus, std_pl) || std_pl.S < 3) return 0;
+    if ((T + std_pl.grid - 1) / std_pl.grid > 2) return 0;
+    P = 2;
+    while (P < std_pl.S) P *= 2;
+  }
   if (P > 8 || P > GS) return 0;
   const int SPL = (GS + P - 1) / P;
   if ((P - 1) * SPL >= GS) return 0;  // the last part would have no span
@@ -1393,7 +1409,7 @@ int launch_gemv(const void* wdev, const void* x, void* y, const fb_shape_t* s, c
                      static_cast<const uint8_t*>(wdev), x, s->K, s->B, pl.SPL, pl.GS, pl.tq,
                      pl.tr, div_magic(pl.SPL), pl.S, s->fwht_block, x_row_stride(pl.SPL * 4),
                      fwht_scale(s->fwht_block), y, s->N, s->y_dtype
-                     PH_KARG((size_t)pl.grid * NW * 64));
+                     PH_KARG((size_t)pl.grid * (pl.P ? pl.P : 1) * NW * 64));
   return hipGetLastError() == hipSuccess ? FB_OK : FB_ERR_HIP;
 }
 
@@ -1501,11 +1517,13 @@ int gemv_planned(const void* wdev, const void* x, void* y, const fb_shape_t* s, 
     const dim3 grid((unsigned)((n + 1023) / 1024));
     const float* part = static_cast<const float*>(ws);
     // P is 4 or 8: splitk_parts takes the sliced plan's slice count (3 or more) rounded up
-    // to a power of two, at most 8
+    // to a power of two, at most 8 (2 only when the diagnostic library forces it)
     if (pl.P == 4)
       hipLaunchKernelGGL(splitk_sum<4>, grid, dim3(256), 0, hs, part, n, y, s->y_dtype);
-    else
+    else if (pl.P == 8)
       hipLaunchKernelGGL(splitk_sum<8>, grid, dim3(256), 0, hs, part, n, y, s->y_dtype);
+    else
+      hipLaunchKernelGGL(splitk_sum<2>, grid, dim3(256), 0, hs, part, n, y, s->y_dtype);
     return hipGetLastError() == hipSuccess ? FB_OK : FB_ERR_HIP;
   }
   if (make_plan(s, cus, pl)) return launch_plan(wdev, x, y, s, pl, hs);
@@ -1626,6 +1644,45 @@ int gemv_mx_impl(const void* wdev, const void* x, void* y, const fb_shape_t* s, 
   uint8_t* w8 = static_cast<uint8_t*>(ws);
   return gemv_mx_split_run(wdev, w8, y, s, cus, w8 + need, ws_bytes - need, hs);
 }
+
+#ifdef FB_PHASE_TRACE
+// The launch floor of a GEMV plan (diagnostic library only): a kernel that does nothing, with
+// the GEMV's argument block, grid, waves per workgroup and dynamic LDS, holding VG VGPRs (the
+// count of the GEMV kernel it stands in for: 183 for the 8-wave GF4 batch-1 kernels, 92 for
+// the E2M1 ones), so the same number of its workgroups fit a CU.  Its traced duration and its
+// back-to-back rate are what a call of that plan costs before any work.
+template <int NW, int VG>
+__global__ __launch_bounds__(NW * 64) void floor_kernel(
+    const uint8_t* __restrict__ w, const void* __restrict__ x, int K, int Bin, int SPL, int GS,
+    int tq, int tr, unsigned spl_m, int S, int fwht_block, int RS, float fwht_scale,
+    void* __restrict__ y, int N, int ydt) {
+  extern __shared__ __align__(16) uint8_t lds[];
+  if constexpr (VG == 183)
+    asm volatile("v_mov_b32 v182, 0" ::: "v182");
+  else
+    asm volatile("v_mov_b32 v91, 0" ::: "v91");
+  // never true for a real launch (N >= 1): keeps the arguments and the LDS live
+  if (N < 0 && threadIdx.x == 0)
+    static_cast<uint8_t*>(y)[blockIdx.x] = lds[threadIdx.x] + w[K] + static_cast<const uint8_t*>(x)[Bin];
+}
+
+template <int NW, int VG>
+int launch_floor(const fb_shape_t* s, const Plan& pl, hipStream_t stream) {
+  auto kern = floor_kernel<NW, VG>;
+  static std::atomic<bool> attr_set{false};  // diagnostic library: the first device only
+  if (!attr_set.load(std::memory_order_acquire)) {
+    if (hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, kLdsLimit) != hipSuccess)
+      return FB_ERR_HIP;
+    attr_set.store(true, std::memory_order_release);
+  }
+  hipLaunchKernelGGL(kern, dim3(pl.grid), dim3(NW * 64), pl.lds, stream, nullptr, nullptr, s->K,
+                     s->B, pl.SPL, pl.GS, pl.tq, pl.tr, div_magic(pl.SPL), pl.S, s->fwht_block,
+                     x_row_stride(pl.SPL * 4), fwht_scale(s->fwht_block), nullptr, s->N,
+                     s->y_dtype);
+  return hipGetLastError() == hipSuccess ? FB_OK : FB_ERR_HIP;
+}
+#endif
 
 // Scratch of the allocation-free entry point: a file-scope device array (one per GPU the
 // library runs on, alive until the process ends).  Host code never uses the array's name as
@@ -1796,20 +1853,47 @@ int fb_phase_trace_set(void* buf, size_t entries) {
   return FB_OK;
 }
 
-// The launch plan fb_gemv uses for a shape on the current device: workgroups, waves per
-// workgroup, K-slices, row tiles per workgroup (the first tr take one more).
-int fb_phase_plan(const fb_shape_t* s, int* grid, int* waves, int* slices, int* tq, int* tr) {
-  if (!s || !grid || !waves || !slices || !tq || !tr) return FB_ERR_NULL;
+// The launch plan fb_gemv uses for a shape on the current device, given a workspace of
+// fb_workspace_bytes(s): workgroups (per K-part), waves per workgroup, K-slices (split-K:
+// parts), row tiles per workgroup (the first tr take one more), and the split-K part count
+// (0: the slices in turn).
+int fb_phase_plan(const fb_shape_t* s, int* grid, int* waves, int* slices, int* tq, int* tr,
+                  int* parts) {
+  if (!s || !grid || !waves || !slices || !tq || !tr || !parts) return FB_ERR_NULL;
   const int st = fb_validate(s);
   if (st != FB_OK) return st;
   Plan pl;
-  if (!make_plan(s, device_cus(), pl)) return FB_ERR_LDS;
+  if (!splitk_parts(s, device_cus(), &pl) && !make_plan(s, device_cus(), pl)) return FB_ERR_LDS;
   *grid = pl.grid;
   *waves = pl.nw;
   *slices = pl.S;
   *tq = pl.tq;
   *tr = pl.tr;
+  *parts = pl.P;
   return FB_OK;
+}
+
+// The split-K part count of the following calls (see g_force_parts); not for concurrent use.
+int fb_phase_force_parts(int parts) {
+  if (parts != 0 && parts != -1 && parts != 2 && parts != 4 && parts != 8) return FB_ERR_SHAPE;
+  g_force_parts.store(parts, std::memory_order_relaxed);
+  return FB_OK;
+}
+
+// Launches floor_kernel with the plan fb_gemv would launch for a batch-1 shape that runs one
+// kernel (no workspace): its grid, waves and LDS, and the register count of the GF4 (183) or
+// E2M1 (92) 8-wave kernel.
+int fb_phase_floor(const fb_shape_t* s, void* stream) {
+  if (!s) return FB_ERR_NULL;
+  const int st = fb_validate(s);
+  if (st != FB_OK) return st;
+  Plan pl;
+  if (!make_plan(s, device_cus(), pl)) return FB_ERR_LDS;
+  hipStream_t hs = static_cast<hipStream_t>(stream);
+  const bool gf4 = s->fmt == FB_FMT_GF4;
+  if (pl.nw == kWaves / 2)
+    return gf4 ? launch_floor<kWaves / 2, 183>(s, pl, hs) : launch_floor<kWaves / 2, 92>(s, pl, hs);
+  return launch_floor<kWaves, 92>(s, pl, hs);
 }
 #endif
 

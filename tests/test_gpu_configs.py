@@ -487,3 +487,50 @@ def test_splitk_against_slices_and_oracle(fmt, N, ydt, K):
     host = pw.dequant_host()[rows]
     ok, emax = within_tol(y_sk[:, rows], torch.nn.functional.linear(x.cpu().float(), host), extra)
     assert ok, f"split-K vs oracle decode: {emax}"
+
+
+def test_one_workspace_shared_across_shapes_and_paths():
+    """One uninitialised workspace (sized for the largest call) serves split-K calls of
+    different shapes and part counts, a rotated call whose x' lands where the other shapes'
+    part sums were, and the native FP4 path, interleaved and repeated: every call gives the
+    bits of the same call on a fresh workspace, whatever the previous calls left in it."""
+    import ctypes
+    g = torch.Generator().manual_seed(77)
+    cases = []
+    for fmt, N, K, B, block in (("gf4", 1000, 11008, 16, 0), ("e2m1", 520, 28672, 16, 0),
+                                ("gf4", 640, 11008, 16, 256), ("gf4", 96, 11008, 12, 0)):
+        w = torch.randn(N, K, generator=g) * 0.02
+        pw = PackedWeight.quantize(w, fmt, fwht_block=block, device=DEV,
+                                   packer="gpu" if fmt == "gf4" else "host")
+        xdt = torch.float16 if fmt == "gf4" else torch.bfloat16
+        x = torch.randn(B, K, generator=g).to(xdt).to(DEV)
+        cases.append((pw, x, pw.shape(B, xdt, torch.float32)))
+    L = C.lib()
+    sp = torch.cuda.current_stream().cuda_stream
+    need = max(C.workspace_bytes(sh) for _, _, sh in cases)
+    mx_sh = cases[1][2]
+    need = max(need, C.mx_workspace_bytes(mx_sh))
+    shared = torch.full((need,), 0x7F, dtype=torch.uint8, device=DEV)
+
+    def call(i, ws, mx=False):
+        pw, x, sh = cases[i]
+        y = torch.full((sh.B, sh.N), float("nan"), device=DEV)
+        f = L.fb_gemv_mx if mx else L.fb_gemv
+        assert f(pw.wdev.data_ptr(), x.data_ptr(), y.data_ptr(), ctypes.byref(sh),
+                 ws.data_ptr(), ws.numel(), sp) == 0
+        return y
+
+    fresh = {}
+    for i in range(len(cases)):
+        fresh[i] = call(i, torch.empty(need, dtype=torch.uint8, device=DEV))
+    fresh["mx"] = call(1, torch.empty(need, dtype=torch.uint8, device=DEV), mx=True)
+    order = [0, 1, 2, 3, "mx", 2, 0, 3, 1, "mx", 0]
+    for k in order:
+        y = call(1, shared, mx=True) if k == "mx" else call(k, shared)
+        torch.cuda.synchronize()
+        assert torch.equal(y, fresh[k]), f"case {k}"
+    for i, (pw, x, sh) in enumerate(cases):
+        W = pw.dequant_device(torch.float32)
+        xr = O.rotate_x(x.cpu(), pw.fwht_block).to(DEV) if pw.fwht_block else x.float()
+        ok, emax = within_tol(fresh[i], xr @ W.t())
+        assert ok, f"case {i}: max abs err {emax}"

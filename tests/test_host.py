@@ -34,16 +34,21 @@ def test_abi_exports_every_declared_symbol():
 
 def test_diagnostic_trace_library_exports():
     """libfourbit_trace.so (the GEMV with per-wave phase timestamps, read by
-    `bench.py --phase-trace`) exports the same C ABI plus its two diagnostic entry points;
-    the product library exports neither of those."""
+    `bench.py --phase-trace`) exports the same C ABI plus its diagnostic entry points (the
+    phase buffer, the launch plan, the launch-floor kernel, the forced split-K part count);
+    the product library exports none of those."""
     path = Path(C.__file__).resolve().parent / "libfourbit_trace.so"
     T = ctypes.CDLL(str(path))
     for name in C.EXPORTED:
         assert getattr(T, name) is not None
     assert T.fb_phase_trace_set is not None and T.fb_phase_plan is not None
+    assert T.fb_phase_floor is not None
     T.fb_phase_trace_set.argtypes = [ctypes.c_void_p, ctypes.c_size_t]
     assert T.fb_phase_trace_set(None, 0) == 0  # host-side only: needs no GPU
-    for name in ("fb_phase_trace_set", "fb_phase_plan"):
+    T.fb_phase_floor.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
+    assert T.fb_phase_floor(None, None) == -1  # validated before any device call
+    assert T.fb_phase_force_parts(3) == -2 and T.fb_phase_force_parts(0) == 0
+    for name in ("fb_phase_trace_set", "fb_phase_plan", "fb_phase_floor", "fb_phase_force_parts"):
         with pytest.raises(AttributeError):
             getattr(C.lib(), name)
 
@@ -59,16 +64,17 @@ def test_batch1_plans_over_a_shape_sweep():
     K = 512: 538 tiles per 512-thread workgroup)."""
     T_lib = ctypes.CDLL(str(Path(C.__file__).resolve().parent / "libfourbit_trace.so"))
     ip = ctypes.POINTER(ctypes.c_int)
-    T_lib.fb_phase_plan.argtypes = [ctypes.POINTER(C.FbShape), ip, ip, ip, ip, ip]
+    T_lib.fb_phase_plan.argtypes = [ctypes.POINTER(C.FbShape), ip, ip, ip, ip, ip, ip]
     over = []
     for fmt in (C.FMT_GF4, C.FMT_E2M1):
         xdt = C.DT_F16 if fmt == C.FMT_GF4 else C.DT_BF16
         for K in (128, 512, 2048, 4096, 8192):
             for N in (1, 16, 4095, 65536, 2_200_000, 4_200_000):
                 s = C.make_shape(N, K, 1, fmt, 0, xdt, C.DT_F32)
-                v = [ctypes.c_int() for _ in range(5)]
+                v = [ctypes.c_int() for _ in range(6)]
                 assert T_lib.fb_phase_plan(ctypes.byref(s), *[ctypes.byref(a) for a in v]) == 0
-                grid, waves, slices, tq, tr = (a.value for a in v)
+                grid, waves, slices, tq, tr, parts = (a.value for a in v)
+                assert parts == 0
                 T = (N + 15) // 16
                 assert grid == min(T, 256) and waves in (8, 16) and slices >= 1, (fmt, K, N)
                 assert grid * tq + tr == T and 0 <= tr < grid
