@@ -70,7 +70,8 @@ def time_gpu(pw: PackedWeight, x: torch.Tensor, y: torch.Tensor, steps: int, war
     region, number of weight copies, [ms per call of each extra region]).  mx: "split" times
     fb_gemv_mx (the native FP4 path, its x split included) instead of fb_gemv; "presplit"
     times fb_gemv_mx_presplit on one split made beforehand (what each further layer with the
-    same input costs)."""
+    same input costs); "splitfloor" the same after an empty kernel with the split's launch
+    shape (fb_phase_mx_floor of the diagnostic library): the floor of a separate split."""
     L = C.lib()
     shape = pw.shape(x.shape[0], x.dtype, y.dtype)
     sref = ctypes.byref(shape)
@@ -81,12 +82,18 @@ def time_gpu(pw: PackedWeight, x: torch.Tensor, y: torch.Tensor, steps: int, war
     if mx == "split":
         ws = torch.zeros(C.mx_workspace_bytes(shape), dtype=torch.uint8, device=x.device)
         gemv = L.fb_gemv_mx
-    elif mx == "presplit":
+    elif mx in ("presplit", "splitfloor"):
         xsplit = C.mx_split_raw(x, shape)
         xp = xsplit.data_ptr()
         nws = L.fb_mx_presplit_workspace_bytes(sref)
         ws = torch.zeros(nws, dtype=torch.uint8, device=x.device) if nws else None
         gemv = L.fb_gemv_mx_presplit
+        if mx == "splitfloor":
+            tl = ctypes.CDLL(str(ROOT / "if_i_could_turn_back_time_amd" / "libfourbit_trace.so"))
+            vp = ctypes.c_void_p
+            gemv = tl.fb_phase_mx_floor
+            gemv.restype = ctypes.c_int
+            gemv.argtypes = [vp, vp, vp, ctypes.POINTER(C.FbShape), vp, ctypes.c_size_t, vp]
     else:
         ws = C.new_workspace(shape, x.device)
         gemv = L.fb_gemv
@@ -307,7 +314,8 @@ def run_workload(name: str, steps: int, warmup: int, want_cpu: bool, check: bool
     gbs = nbytes / (ms * 1e-3) / 1e9
     rec = {
         "workload": name, "fmt": fmt, "K": K, "N": N, "B": B, "fwht_block": fb,
-        "path": {"split": "fp4_mfma", "presplit": "fp4_mfma_presplit"}.get(mx, "exact_decode"),
+        "path": {"split": "fp4_mfma", "presplit": "fp4_mfma_presplit",
+                 "splitfloor": "fp4_mfma_presplit_after_empty_split"}.get(mx, "exact_decode"),
         "bytes_per_call": nbytes, "weight_stream_bytes": N * K // 2,
         "us_per_call": ms * 1e3, "GBps": gbs, "frac_of_8TBps": gbs / PEAK_GBS,
         "weight_copies_cycled": ncp, "warmup_calls_run": warm_calls,
@@ -324,7 +332,7 @@ def run_workload(name: str, steps: int, warmup: int, want_cpu: bool, check: bool
         yk = torch.empty(B, N, dtype=torch.float32, device="cuda:0")
         if mx == "split":
             pw.gemv_mx(xd, out=yk)
-        elif mx == "presplit":
+        elif mx in ("presplit", "splitfloor"):
             sh = pw.shape(B, xd.dtype, torch.float32)
             C.gemv_mx_presplit(pw.wdev, C.mx_split_raw(xd, sh), yk, sh)
         else:
@@ -718,7 +726,8 @@ def main():
     ap.add_argument("--mx", action="store_true",
                     help="only compare the native FP4 path (fb_gemv_mx) with the exact-decode "
                          "path on every unrotated E2M1 workload (or --workload, if it is one), "
-                         "one JSON line per path")
+                         "one JSON line per path, with the FP4 GEMV on a pre-made split, alone "
+                         "and after an empty kernel of the split's launch shape")
     ap.add_argument("--floor", action="store_true",
                     help="only time the launch floor (an empty kernel with each batch-1 "
                          "workload's plan) against the GEMV, one JSON line per workload "
@@ -763,7 +772,7 @@ def main():
             names = [args.workload]
         cache = {}
         for name in names:
-            for mx in ("", "split", "presplit"):
+            for mx in ("", "split", "presplit", "splitfloor"):
                 rec, pw = run_workload(name, args.steps, args.warmup, False, cache=cache,
                                        windows=MEDIAN_WINDOWS, mx=mx)
                 del pw

@@ -673,81 +673,111 @@ __host__ __device__ inline size_t mx_split_bytes(int B, int K) {
   return mx_scale_offset(B, K) + (((size_t)B * (K / 128) * 8 + 255) & ~size_t(255));
 }
 
-// E8M0 exponent of a block: the smallest e with amax <= 448 2^e, within [-127, 127] (a block
-// of zeros: -127).
-__device__ __forceinline__ int mx_exponent(float amax) {
-  if (!(amax > 0.0f)) return -127;
-  const int ex = __builtin_amdgcn_frexp_expf(amax);  // amax = m 2^ex, m in [0.5, 1)
-  const float m = __builtin_amdgcn_frexp_mantf(amax);
-  const int e = ex - 9 + (m > 0.875f ? 1 : 0);        // 448 = 0.875 2^9
-  return e < -127 ? -127 : e > 127 ? 127 : e;
+// E8M0 byte (e + 127) of a 32-value block whose largest magnitude has the bf16 bit pattern a
+// (sign cleared): e is the smallest exponent with that magnitude at most 448 2^e (448 = 1.75 2^8,
+// E4M3's largest finite value), and at least -127.  With a = (biased exponent E, fraction F, 7
+// bits), e + 127 = E - 8 + (F > 0x60); adding 31 carries into E exactly when F > 0x60.  A zero
+// or bf16-subnormal block gets 0 (2^-127).  x must be finite.
+__device__ __forceinline__ unsigned mx_scale_byte(unsigned a) {
+  const int s = (int)((a + 31u) >> 7) - 8;
+  return s < 0 ? 0u : (unsigned)s;
 }
 
-// E4M3 (OCP e4m3fn: bias 7, 3 fraction bits, subnormal step 2^-9) code of v, |v| <= 448,
-// rounded to nearest, ties to even; *q = the code's value.
-__device__ __forceinline__ unsigned e4m3_rne(float v, float* q) {
-  const unsigned u = __builtin_bit_cast(unsigned, v);
-  const unsigned sign = (u >> 24) & 0x80u;
-  const float a = __builtin_fabsf(v);
-  unsigned code;
-  float qa;
-  if (a < 0.015625f) {  // below 2^-6, the smallest normal: multiples of 2^-9
-    const float r = __builtin_rintf(a * 512.0f);  // 0..8 (8 is the smallest normal)
-    code = (unsigned)r;
-    qa = r * 0.001953125f;
-  } else {
-    unsigned au = u & 0x7FFFFFFFu;
-    au = (au + 0x7FFFFu + ((au >> 20) & 1u)) & ~0xFFFFFu;  // 3 fraction bits, ties to even
-    code = (((au >> 23) - 120u) << 3) | ((au >> 20) & 7u);
-    qa = __builtin_bit_cast(float, au);
-  }
-  *q = sign ? -qa : qa;
-  return sign | code;
+// Largest of v over the lane's quad (the 4 threads of one 32-value block), by two DPP quad
+// permutes.
+__device__ __forceinline__ unsigned quad_max(unsigned v) {
+  v = max(v, (unsigned)__builtin_amdgcn_update_dpp(0, (int)v, 0xB1, 0xF, 0xF, false));  // [1,0,3,2]
+  v = max(v, (unsigned)__builtin_amdgcn_update_dpp(0, (int)v, 0x4E, 0xF, 0xF, false));  // [2,3,0,1]
+  return v;
 }
 
-// The split: one thread per 8 consecutive values, so 4 threads per 32-value block and 16 per
-// 128-value group (n8 = B K / 8 is a multiple of 16, and a group's threads are 16 aligned
-// lanes of one wave).
-__global__ __launch_bounds__(256) void mx_split_kernel(const uint16_t* __restrict__ x,
-                                                       uint8_t* __restrict__ out, int n8,
-                                                       size_t sc_off) {
-  const int i = blockIdx.x * 256 + threadIdx.x;
-  const int lane = threadIdx.x & 63;
+typedef short s16x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+// A word as two bf16 values.  Taken by value: clang's __builtin_bit_cast of a vector element
+// (raw.y) reads the vector's first element instead.
+__device__ __forceinline__ bf16x2_t bf16_pair(unsigned w) { return __builtin_bit_cast(bf16x2_t, w); }
+
+// The split: one thread per 8 consecutive values (n8 = B K / 8 threads, a multiple of 16), so
+// the 4 threads of a 32-value block are one aligned lane quad and a 128-value group's 16
+// threads are aligned lanes of one wave.  The rounding is gfx950's scaled conversions:
+// v_cvt_scalef32_pk_fp8_{bf16,f32} divide two values by the power of two whose exponent field
+// is their f32 scale operand's (all 8 bits: field 0 is 2^-127, as in E8M0) and round to the
+// nearest E4M3 value, ties to even, subnormals included, with no saturation needed (every
+// quotient is at most 448 by the choice of e); v_cvt_scalef32_pk_f32_fp8 multiplies the codes
+// back, exactly wherever the product is within fp32's range (below).  The GPU tests
+// hold the result to the oracle's split byte for byte, over every finite bf16 value.
+//  - Term 0 rounds x.  Its block maximum is taken on the bf16 bit patterns (magnitudes order
+//    as unsigned integers), two at a time.
+//  - Term 1 rounds t = x - term 0, computed in fp32 and exact (x and term 0 lie on x's bf16
+//    grid, within a factor 2 of each other, or term 0 is zero), and itself a bf16 value, so
+//    its maximum's top 16 bits are its bf16 pattern.
+__global__ __launch_bounds__(64) void mx_split_kernel(const uint16_t* __restrict__ x,
+                                                      uint8_t* __restrict__ out, int n8,
+                                                      size_t sc_off) {
+  const int i = blockIdx.x * 64 + threadIdx.x;
   const bool in = i < n8;
   const u32x4 raw = in ? *reinterpret_cast<const u32x4*>(x + (size_t)i * 8) : u32x4{0u, 0u, 0u, 0u};
-  float v[8];
+  const size_t rec = (size_t)(i >> 4);  // (b K/128 + g): values 8i.. are b K + k
+  uint8_t* codes = out + rec * 256 + (i & 15) * 8;
+  uint8_t* sbyte = out + sc_off + rec * 8 + ((i >> 2) & 3);  // the block's scale byte, term 0
+  const bool first = in && (i & 3) == 0;                     // the block's first thread writes it
+
+  // term 0
+  const u16x2 m01 = __builtin_elementwise_max(__builtin_bit_cast(u16x2, raw.x & 0x7FFF7FFFu),
+                                              __builtin_bit_cast(u16x2, raw.y & 0x7FFF7FFFu));
+  const u16x2 m23 = __builtin_elementwise_max(__builtin_bit_cast(u16x2, raw.z & 0x7FFF7FFFu),
+                                              __builtin_bit_cast(u16x2, raw.w & 0x7FFF7FFFu));
+  const u16x2 m = __builtin_elementwise_max(m01, m23);
+  const unsigned sb0 = mx_scale_byte(quad_max(max((unsigned)m.x, (unsigned)m.y)));
+  const float sc0 = __builtin_bit_cast(float, sb0 << 23);
+  s16x2 c01 = {0, 0}, c23 = {0, 0};
+  c01 = __builtin_amdgcn_cvt_scalef32_pk_fp8_bf16(c01, bf16_pair(raw.x), sc0, false);
+  c01 = __builtin_amdgcn_cvt_scalef32_pk_fp8_bf16(c01, bf16_pair(raw.y), sc0, true);
+  c23 = __builtin_amdgcn_cvt_scalef32_pk_fp8_bf16(c23, bf16_pair(raw.z), sc0, false);
+  c23 = __builtin_amdgcn_cvt_scalef32_pk_fp8_bf16(c23, bf16_pair(raw.w), sc0, true);
+  const unsigned w0 = __builtin_bit_cast(unsigned, c01), w1 = __builtin_bit_cast(unsigned, c23);
+  if (in) *reinterpret_cast<uint2*>(codes) = uint2{w0, w1};
+  if (first) sbyte[0] = (uint8_t)sb0;
+
+  // term 1: t = x - term 0
+  // A block of scale 2^120 (the largest a finite bf16 block gets) can round to 256 2^120 =
+  // 2^128, past fp32's range: there term 0 is taken back at half its value h and t = (x - h) - h,
+  // both steps exact (x and h have one sign and lie on x's bf16 grid).
+  const bool top = sb0 >= 247;
+  const float scq = __builtin_bit_cast(float, (sb0 - (top ? 1u : 0u)) << 23);
+  const f32x2 q[4] = {__builtin_amdgcn_cvt_scalef32_pk_f32_fp8(w0, scq, false),
+                      __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(w0, scq, true),
+                      __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(w1, scq, false),
+                      __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(w1, scq, true)};
+  float t[8];
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
-    v[2 * j] = __builtin_bit_cast(float, raw[j] << 16);
-    v[2 * j + 1] = __builtin_bit_cast(float, raw[j] & 0xFFFF0000u);
+    t[2 * j] = __builtin_bit_cast(float, raw[j] << 16) - q[j].x;
+    t[2 * j + 1] = __builtin_bit_cast(float, raw[j] & 0xFFFF0000u) - q[j].y;
   }
-  const size_t rec = (size_t)(i >> 4);  // (b K/128 + g): values 8i.. are b K + k
+  if (top) {
 #pragma unroll
-  for (int t = 0; t < 2; ++t) {
-    float amax = 0.0f;
-#pragma unroll
-    for (int j = 0; j < 8; ++j) amax = fmaxf(amax, __builtin_fabsf(v[j]));
-    amax = fmaxf(amax, __shfl_xor(amax, 1));
-    amax = fmaxf(amax, __shfl_xor(amax, 2));
-    const int e = mx_exponent(amax);
-    unsigned w0 = 0, w1 = 0;
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      float q;
-      const unsigned c = e4m3_rne(__builtin_ldexpf(v[j], -e), &q);
-      if (j < 4)
-        w0 |= c << (8 * j);
-      else
-        w1 |= c << (8 * (j - 4));
-      v[j] -= __builtin_ldexpf(q, e);  // exact: what the next term rounds
+    for (int j = 0; j < 4; ++j) {
+      t[2 * j] -= q[j].x;
+      t[2 * j + 1] -= q[j].y;
     }
-    if (in) *reinterpret_cast<uint2*>(out + rec * 256 + t * 128 + (i & 15) * 8) = uint2{w0, w1};
-    // the group's four block scales, gathered in its first thread
-    const unsigned sb = (unsigned)(e + 127);
-    const unsigned s1 = __shfl(sb, lane + 4), s2 = __shfl(sb, lane + 8), s3 = __shfl(sb, lane + 12);
-    if (in && (i & 15) == 0)
-      *reinterpret_cast<unsigned*>(out + sc_off + rec * 8 + t * 4) = sb | s1 << 8 | s2 << 16 | s3 << 24;
   }
+  float a = __builtin_fmaxf(__builtin_fabsf(t[0]), __builtin_fabsf(t[1]));
+#pragma unroll
+  for (int j = 2; j < 8; ++j) a = __builtin_fmaxf(a, __builtin_fabsf(t[j]));
+  const unsigned sb1 = mx_scale_byte(quad_max(__builtin_bit_cast(unsigned, a) >> 16));
+  const float sc1 = __builtin_bit_cast(float, sb1 << 23);
+  s16x2 d01 = {0, 0}, d23 = {0, 0};
+  d01 = __builtin_amdgcn_cvt_scalef32_pk_fp8_f32(d01, t[0], t[1], sc1, false);
+  d01 = __builtin_amdgcn_cvt_scalef32_pk_fp8_f32(d01, t[2], t[3], sc1, true);
+  d23 = __builtin_amdgcn_cvt_scalef32_pk_fp8_f32(d23, t[4], t[5], sc1, false);
+  d23 = __builtin_amdgcn_cvt_scalef32_pk_fp8_f32(d23, t[6], t[7], sc1, true);
+  if (in)
+    *reinterpret_cast<uint2*>(codes + 128) =
+        uint2{__builtin_bit_cast(unsigned, d01), __builtin_bit_cast(unsigned, d23)};
+  if (first) sbyte[4] = (uint8_t)sb1;
 }
 
 typedef int i32x8 __attribute__((ext_vector_type(8)));
@@ -1600,7 +1630,7 @@ int mx_check(const fb_shape_t* s) {
 
 int launch_mx_split(const void* x, void* out, const fb_shape_t* s, hipStream_t hs) {
   const int n8 = s->B * (s->K / 8);  // B K < 2^31 (fb_validate)
-  hipLaunchKernelGGL(mx_split_kernel, dim3((n8 + 255) / 256), dim3(256), 0, hs,
+  hipLaunchKernelGGL(mx_split_kernel, dim3((n8 + 63) / 64), dim3(64), 0, hs,
                      static_cast<const uint16_t*>(x), static_cast<uint8_t*>(out), n8,
                      mx_scale_offset(s->B, s->K));
   return hipGetLastError() == hipSuccess ? FB_OK : FB_ERR_HIP;
@@ -1681,6 +1711,17 @@ int launch_floor(const fb_shape_t* s, const Plan& pl, hipStream_t stream) {
                      x_row_stride(pl.SPL * 4), fwht_scale(s->fwht_block), nullptr, s->N,
                      s->y_dtype);
   return hipGetLastError() == hipSuccess ? FB_OK : FB_ERR_HIP;
+}
+
+// The launch floor of the native FP4 path's split (diagnostic library only): a kernel with
+// mx_split_kernel's grid, block and arguments that does nothing.  fb_phase_mx_floor launches
+// it and then the GEMV on a split made beforehand, so its time per call against
+// fb_gemv_mx_presplit's is what a separate split launch costs before any work.
+__global__ __launch_bounds__(64) void split_floor_kernel(const uint16_t* __restrict__ x,
+                                                         uint8_t* __restrict__ out, int n8,
+                                                         size_t sc_off) {
+  // never true for a real launch (n8 >= 16): keeps the arguments live
+  if (n8 < 0 && threadIdx.x == 0) out[blockIdx.x] = (uint8_t)x[sc_off];
 }
 #endif
 
@@ -1835,6 +1876,23 @@ int fb_gemv_mx_presplit(const void* wdev, const void* xs, void* y, const fb_shap
   if (!ws) ws_bytes = 0;
   return gemv_mx_split_run(wdev, xs, y, s, cus, ws, ws_bytes, static_cast<hipStream_t>(stream));
 }
+
+#ifdef FB_PHASE_TRACE
+// fb_gemv_mx_presplit after an empty kernel with the split's launch shape (diagnostic
+// library; see split_floor_kernel).  xs: a split made beforehand, as for the presplit call.
+int fb_phase_mx_floor(const void* wdev, const void* xs, void* y, const fb_shape_t* s, void* ws,
+                      size_t ws_bytes, void* stream) {
+  if (!s || !wdev || !xs || !y) return FB_ERR_NULL;
+  const int st = mx_gemv_check(s, device_cus());
+  if (st != FB_OK) return st;
+  const int n8 = s->B * (s->K / 8);
+  hipLaunchKernelGGL(split_floor_kernel, dim3((n8 + 63) / 64), dim3(64), 0,
+                     static_cast<hipStream_t>(stream), static_cast<const uint16_t*>(xs),
+                     static_cast<uint8_t*>(ws ? ws : y), n8, mx_scale_offset(s->B, s->K));
+  if (hipGetLastError() != hipSuccess) return FB_ERR_HIP;
+  return fb_gemv_mx_presplit(wdev, xs, y, s, ws, ws_bytes, stream);
+}
+#endif
 
 size_t fb_mx_presplit_workspace_bytes(const fb_shape_t* s) {
   if (!s || mx_check(s) != FB_OK) return 0;

@@ -62,6 +62,31 @@ def test_mx_split_bit_exact_vs_oracle(B, K, kind):
     assert np.array_equal(codes.cpu().numpy(), oc)
 
 
+@pytest.mark.parametrize("order", ["sorted", "shuffled"])
+def test_mx_split_every_bf16_value(order):
+    """Every finite bf16 value (65,280 bit patterns, as x of 15 rows of 4,352) through the
+    split, against the oracle's split byte for byte.  In pattern order each 32-value block
+    holds neighbouring values of one sign, so every value meets term 0's rounding at its own
+    block's scale; shuffled (seeded), the blocks span up to the whole exponent range, so
+    small values round to E4M3 subnormals or zero at a large block's scale and term 1 picks
+    them up."""
+    p = np.arange(65536, dtype=np.uint32)
+    p = p[((p >> 7) & 0xFF) != 0xFF]
+    assert p.size == 15 * 4352
+    if order == "shuffled":
+        p = np.random.default_rng(5).permutation(p)
+    x = torch.from_numpy(p.astype(np.uint16).view(np.int16).reshape(15, 4352)).view(torch.bfloat16)
+    say("mx split, every bf16 value,", order)
+    shape = C.make_shape(64, 4352, 15, C.FMT_E2M1, 0, C.DT_BF16, C.DT_F32)
+    codes, scales = C.mx_split(x.to(DEV), shape)
+    torch.cuda.synchronize()
+    oc, osc = O.mx_split_x(x.float().numpy())
+    bad = np.argwhere(scales.cpu().numpy() != osc)
+    assert bad.size == 0, f"scale bytes differ at (term, row, block) {bad[:8].tolist()}"
+    bad = np.argwhere(codes.cpu().numpy() != oc)
+    assert bad.size == 0, f"codes differ at (term, row, k) {bad[:8].tolist()}"
+
+
 _PW = {}
 
 

@@ -35,8 +35,8 @@ def test_abi_exports_every_declared_symbol():
 def test_diagnostic_trace_library_exports():
     """libfourbit_trace.so (the GEMV with per-wave phase timestamps, read by
     `bench.py --phase-trace`) exports the same C ABI plus its diagnostic entry points (the
-    phase buffer, the launch plan, the launch-floor kernel, the forced split-K part count);
-    the product library exports none of those."""
+    phase buffer, the launch plan, the launch-floor kernels of the GEMV and of the FP4 path's
+    split, the forced split-K part count); the product library exports none of those."""
     path = Path(C.__file__).resolve().parent / "libfourbit_trace.so"
     T = ctypes.CDLL(str(path))
     for name in C.EXPORTED:
@@ -48,7 +48,10 @@ def test_diagnostic_trace_library_exports():
     T.fb_phase_floor.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
     assert T.fb_phase_floor(None, None) == -1  # validated before any device call
     assert T.fb_phase_force_parts(3) == -2 and T.fb_phase_force_parts(0) == 0
-    for name in ("fb_phase_trace_set", "fb_phase_plan", "fb_phase_floor", "fb_phase_force_parts"):
+    T.fb_phase_mx_floor.argtypes = [ctypes.c_void_p] * 5 + [ctypes.c_size_t, ctypes.c_void_p]
+    assert T.fb_phase_mx_floor(None, None, None, None, None, 0, None) == -1
+    for name in ("fb_phase_trace_set", "fb_phase_plan", "fb_phase_floor", "fb_phase_force_parts",
+                 "fb_phase_mx_floor"):
         with pytest.raises(AttributeError):
             getattr(C.lib(), name)
 
