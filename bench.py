@@ -367,7 +367,8 @@ PHASES = {  # lane index in the diagnostic build's per-wave record -> phase
     1: "x loads issued", 2: "x arrived", 3: "first unit issued", 4: "first 256 points done",
     5: "phase barrier", 6: "rotation done", 7: "x staged (barrier)", 12: "slice 1 staged",
     13: "slice 2 staged", 8: "first unit done", 14: "slice 0 loop end",
-    15: "slice 1 loop end", 9: "last loop end", 10: "final barrier", 11: "end",
+    15: "slice 1 loop end", 18: "first 4096-point group loaded", 19: "unit decoded ahead",
+    9: "last loop end", 10: "final barrier", 11: "end",
 }
 
 

@@ -298,7 +298,7 @@ enum {
   kPhStart = 0, kPhXIssued = 1, kPhXArrived = 2, kPhU0Issued = 3, kPhStages07 = 4,
   kPhPhaseBar = 5, kPhStages811 = 6, kPhStaged = 7, kPhUnit0 = 8, kPhLoopEnd = 9,
   kPhFinalBar = 10, kPhEnd = 11, kPhStaged1 = 12, kPhStaged2 = 13, kPhSliceEnd0 = 14,
-  kPhSliceEnd1 = 15, kPhXcc = 16, kPhSlices = 17
+  kPhSliceEnd1 = 15, kPhXcc = 16, kPhSlices = 17, kPhGroupLoaded = 18, kPhDecodedAhead = 19
 };
 #ifdef FB_PHASE_TRACE
 struct Phases {
@@ -358,10 +358,10 @@ namespace {
 //    4l..4l+3: stages 0-1 are in-lane, stages 2-7 pair lanes l and l ^ 2^(s-2) (lane_xor).
 //    The x of a wave's first kXPre sub-blocks is loaded by rot_preload before the slice's
 //    weight loads are issued.
-//  - Blocks larger than 256 go through LDS (F: B*kw floats) once: each 4096-value piece is
-//    read back in 16 column groups, taken by the waves in turn; group c holds value
-//    e = (16c + l % 16) + 256 (r + 4 (l / 16)) in lane l, register r, so stages 8-9 are
-//    in-lane and stages 10-11 pair lanes l and l ^ 16, 32.
+//  - Blocks larger than 256 go through LDS (F: B*kw floats) once: each block is read back
+//    in 4 groups of 64 positions, taken by the waves in turn; lane l of group c holds value
+//    64c + l of each of the block's nb = fb / 256 sub-blocks, so stages 8 .. lg_fb-1 are
+//    in-lane butterflies across sub-blocks.
 //  - A lane-pair butterfly is one fma: v' = s v + o with o the partner's value and
 //    s = +1 in the lower lane (v + o), -1 in the upper one (o - v), the same roundings as
 //    the add and the subtract.
@@ -573,54 +573,38 @@ __device__ void stage_fwht(uint8_t* lds, float* F, const XRot& xr, rsrc_t xrs, i
     else
       __syncthreads();
     PH_MARK(kPhPhaseBar);
-    const int total = B * kw;
-    const float inv_kw = 1.0f / (float)kw;
-    const int npieces = ((total + 4095) >> 12) << 4;  // (4096-value piece, column group)
-    // With kw a multiple of 4096 a piece lies in one batch row, found once per piece.
-    const bool whole = (kw & 4095) == 0;
-    for (int piece = wave; piece < npieces; piece += NW) {
-      const int base = (piece >> 4) * 4096 + (piece & 15) * 16;
-      float v[4];
-      int e[4];
+    // Stages 8 .. lg_fb-1 run across the nb = fb / 256 sub-blocks of a block, in registers:
+    // a wave takes 64 positions p of one block at a time (lane = p % 64) and holds value p of
+    // each of its sub-blocks, so the stages are in-lane butterflies on sub-block index bits
+    // 0, 1, 2, 3 in turn.  kw is a whole number of blocks (fb divides K, and a K-slice holds
+    // whole blocks).
+    const int nb = fb >> 8;
+    const int bpr = kw >> lg_fb;  // blocks per batch row
+    const int ngroups = B * bpr * 4;
+    for (int g = wave; g < ngroups; g += NW) {
+      const int blk = g >> 2;  // uniform
+      const int p = (g & 3) * 64 + lane;
+      const int e0 = blk * fb + p;  // value index of sub-block 0, over the batch
+      float v[16];
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        e[r] = base + (lane & 15) + 256 * (r + 4 * (lane >> 4));
-        v[r] = e[r] < total ? F[fpad(e[r])] : 0.0f;
-      }
-      if (lg_fb > 8) {
-        bfly(v[0], v[1]);
-        bfly(v[2], v[3]);
-      }
-      if (lg_fb > 9) {
-        bfly(v[0], v[2]);
-        bfly(v[1], v[3]);
-      }
+      for (int j = 0; j < 16; ++j) v[j] = j < nb ? F[fpad(e0 + j * 256)] : 0.0f;
 #pragma unroll
-      for (int st = 0; st < 2; ++st) {
-        if (st + 10 < lg_fb) {  // uniform
+      for (int t = 0; t < 4; ++t) {
+        if ((2 << t) <= nb) {  // uniform
 #pragma unroll
-          for (int r = 0; r < 4; ++r) v[r] = __builtin_fmaf(sgn[4 + st], v[r], lane_xor(v[r], 16 << st, lane));
+          for (int j = 0; j < 16; ++j)
+            if (!(j & (1 << t))) bfly(v[j], v[j | (1 << t)]);
         }
       }
-      auto store_x = [&](int bb, int k, float val) {
-        *(reinterpret_cast<_Float16*>(lds + bb * RS + (k >> 7) * kSliceBytes) + (k & 127)) =
-            (_Float16)(val * sc);
-      };
-      if (whole) {
-        const int bb = ((piece >> 4) * 4096) / kw;  // uniform
-        const int kofs = bb * kw;
+      if (g == wave) PH_MARK(kPhGroupLoaded);
+      const int bb = B == 1 ? 0 : small_div(blk, bpr);  // batch row (uniform)
+      const int k0b = (blk - bb * bpr) * fb + p;         // k of sub-block 0 within the row
 #pragma unroll
-        for (int r = 0; r < 4; ++r) store_x(bb, e[r] - kofs, v[r]);  // total: whole pieces
-      } else {
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          if (e[r] < total) {
-            // e < 16 * kw < 2^24: the float quotient is within one of e / kw
-            int bb = (int)((float)e[r] * inv_kw);
-            bb -= bb * kw > e[r] ? 1 : 0;
-            bb += (bb + 1) * kw <= e[r] ? 1 : 0;
-            store_x(bb, e[r] - bb * kw, v[r]);
-          }
+      for (int j = 0; j < 16; ++j) {
+        if (j < nb) {
+          const int k = k0b + j * 256;
+          *(reinterpret_cast<_Float16*>(lds + bb * RS + (k >> 7) * kSliceBytes) + (k & 127)) =
+              (_Float16)(v[j] * sc);
         }
       }
     }
@@ -1154,6 +1138,7 @@ __global__ __launch_bounds__(NW * 64) void gemv_kernel(
         issue(s, u0, ring[0]);
         if (s == 0) PH_MARK(kPhU0Issued);
         unit_decode<FMT, XDT>(ring[0], dec);  // waits for its weights, not for x
+        if (s == 0) PH_MARK(kPhDecodedAhead);
         u1 = __builtin_amdgcn_readfirstlane(grab());
         issue(s, u1, ring[1]);
       }
