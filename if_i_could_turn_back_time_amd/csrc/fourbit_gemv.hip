@@ -24,6 +24,7 @@
 #include <algorithm>
 #include <cmath>
 #include <atomic>
+#include <type_traits>
 
 #include "fourbit.h"
 #include "fourbit_layout.h"
@@ -490,8 +491,12 @@ __device__ __forceinline__ void lds_barrier(int* cnt, int n) {
 
 // NW: the waves that take part (the first NW of the workgroup).  LBAR: they meet at the
 // LDS barrier on *rbar instead of the workgroup barrier, so the workgroup's other waves are
-// free meanwhile.
-template <int NW, bool LBAR = false>
+// free meanwhile.  PRE: every sub-block a wave rotates is among its kXPre preloaded ones (the
+// caller's plan guarantees it), so the rotation issues no load of its own: a load there,
+// issued after the first weight unit's, could only be waited for together with those weights,
+// and the compiler's waits for it (or for its registers' reuse) held the later stages until
+// the weights had arrived.
+template <int NW, bool LBAR = false, bool PRE = false>
 __device__ void stage_fwht(uint8_t* lds, float* F, const XRot& xr, rsrc_t xrs, int K, int B,
                            int k0, int kw, int nsl, int RS, int fb, float sc,
                            int tid, int* rbar PH_PARAM) {
@@ -516,7 +521,7 @@ __device__ void stage_fwht(uint8_t* lds, float* F, const XRot& xr, rsrc_t xrs, i
     const int k = (sb - b * nsb) * 256 + lpos;
     const bool live = k < kw;  // kw is a multiple of 128: whole lanes are in or out
     uint2 raw = {0u, 0u};
-    if (i < kXPre) {
+    if (PRE || i < kXPre) {
 #pragma unroll
       for (int j = 0; j < kXPre; ++j)
         if (j == i) raw = xr.v[j];
@@ -578,36 +583,45 @@ __device__ void stage_fwht(uint8_t* lds, float* F, const XRot& xr, rsrc_t xrs, i
     // each of its sub-blocks, so the stages are in-lane butterflies on sub-block index bits
     // 0, 1, 2, 3 in turn.  kw is a whole number of blocks (fb divides K, and a K-slice holds
     // whole blocks).
-    const int nb = fb >> 8;
     const int bpr = kw >> lg_fb;  // blocks per batch row
     const int ngroups = B * bpr * 4;
-    for (int g = wave; g < ngroups; g += NW) {
-      const int blk = g >> 2;  // uniform
-      const int p = (g & 3) * 64 + lane;
-      const int e0 = blk * fb + p;  // value index of sub-block 0, over the batch
-      float v[16];
+    // NB = fb / 256 sub-blocks per block, fixed at compile time so that the group's loads,
+    // butterflies and stores are straight-line code (with a runtime count the compiler
+    // branched around each and waited for the LDS after every store)
+    auto groups = [&](auto nbc) {
+      constexpr int NB = decltype(nbc)::value;
+      for (int g = wave; g < ngroups; g += NW) {
+        const int blk = g >> 2;  // uniform
+        const int p = (g & 3) * 64 + lane;
+        const int e0 = blk * fb + p;  // value index of sub-block 0, over the batch
+        float v[NB];
 #pragma unroll
-      for (int j = 0; j < 16; ++j) v[j] = j < nb ? F[fpad(e0 + j * 256)] : 0.0f;
+        for (int j = 0; j < NB; ++j) v[j] = F[fpad(e0 + j * 256)];
 #pragma unroll
-      for (int t = 0; t < 4; ++t) {
-        if ((2 << t) <= nb) {  // uniform
+        for (int t = 0; (1 << t) < NB; ++t) {
 #pragma unroll
-          for (int j = 0; j < 16; ++j)
+          for (int j = 0; j < NB; ++j)
             if (!(j & (1 << t))) bfly(v[j], v[j | (1 << t)]);
         }
-      }
-      if (g == wave) PH_MARK(kPhGroupLoaded);
-      const int bb = B == 1 ? 0 : small_div(blk, bpr);  // batch row (uniform)
-      const int k0b = (blk - bb * bpr) * fb + p;         // k of sub-block 0 within the row
+        if (g == wave) PH_MARK(kPhGroupLoaded);
+        const int bb = B == 1 ? 0 : small_div(blk, bpr);  // batch row (uniform)
+        const int k0b = (blk - bb * bpr) * fb + p;         // k of sub-block 0 within the row
 #pragma unroll
-      for (int j = 0; j < 16; ++j) {
-        if (j < nb) {
+        for (int j = 0; j < NB; ++j) {
           const int k = k0b + j * 256;
           *(reinterpret_cast<_Float16*>(lds + bb * RS + (k >> 7) * kSliceBytes) + (k & 127)) =
               (_Float16)(v[j] * sc);
         }
       }
-    }
+    };
+    if (lg_fb == 12)
+      groups(std::integral_constant<int, 16>());
+    else if (lg_fb == 11)
+      groups(std::integral_constant<int, 8>());
+    else if (lg_fb == 10)
+      groups(std::integral_constant<int, 4>());
+    else
+      groups(std::integral_constant<int, 2>());
   }
   PH_MARK(kPhStages811);
   // zeros past the rotated width (the weight stream is zero there too)
@@ -1131,13 +1145,18 @@ __global__ __launch_bounds__(NW * 64) void gemv_kernel(
         if (s == 0) PH_MARK(kPhXArrived);
         issue(s, u0, ring[0]);
         if (s == 0) PH_MARK(kPhU0Issued);
-        stage_fwht<NWR, true>(xst, reinterpret_cast<float*>(xst + B * RS), xr, xrs, K, B, k0, kw,
-                              nsl, RS, fwht_block, fwht_scale, tid, counter + 1 PH_ARG);
+        stage_fwht<NWR, true, true>(xst, reinterpret_cast<float*>(xst + B * RS), xr, xrs, K, B,
+                                    k0, kw, nsl, RS, fwht_block, fwht_scale, tid, counter + 1 PH_ARG);
       } else {
         u0 = wave - NWR;
         issue(s, u0, ring[0]);
         if (s == 0) PH_MARK(kPhU0Issued);
         unit_decode<FMT, XDT>(ring[0], dec);  // waits for its weights, not for x
+#ifdef FB_PHASE_TRACE
+        // the mark after the decode's last result, not wherever the scheduler would put it
+#pragma unroll
+        for (int j = 0; j < 16; ++j) asm volatile("" ::"v"(dec.a[j]));
+#endif
         if (s == 0) PH_MARK(kPhDecodedAhead);
         u1 = __builtin_amdgcn_readfirstlane(grab());
         issue(s, u1, ring[1]);
