@@ -919,7 +919,11 @@ constexpr int zero_bytes(int fmt) { return fmt == kFmtMx ? 1088 : 256; }
 // registers, so that this decode runs during the rotation's waits instead of after it.  Each is
 // compiled with only the staging it needs, which keeps the kernel short and its registers
 // few.
-enum { kFlat = 0, kSliced = 1, kRotated = 2, kRot1 = 3, kFlat1 = 4, kSplitK = 5, kRotDA = 6 };
+// kRotDAall = kRotDA where a workgroup owns no more units than waves: the rotating waves also
+// decode their one unit before the staging barrier (with more units that would hold the
+// barrier back).
+enum { kFlat = 0, kSliced = 1, kRotated = 2, kRot1 = 3, kFlat1 = 4, kSplitK = 5, kRotDA = 6,
+       kRotDAall = 7 };
 // NW: waves per workgroup.  16 (one workgroup per CU) in general; 8 (two per CU) for
 // layers with few row tiles per CU, where twice the workgroups, each with half the waves,
 // finish sooner.
@@ -934,7 +938,8 @@ __global__ __launch_bounds__(NW * 64) void gemv_kernel(
   // kRot1 / kFlat1: batch 1 in one K-slice, with both fixed at compile time so that the
   // batch-row and slice bookkeeping folds away (16 waves per CU share one scalar unit, and
   // the prologue is on the critical path of small layers)
-  constexpr bool da = MODE == kRotDA;
+  constexpr bool da_all = MODE == kRotDAall;
+  constexpr bool da = MODE == kRotDA || da_all;
   constexpr bool rot1 = MODE == kRot1 || da;
   constexpr bool flat1 = MODE == kFlat1;
   constexpr int NWR = da ? NW / 2 : NW;  // waves that rotate x
@@ -1147,6 +1152,10 @@ __global__ __launch_bounds__(NW * 64) void gemv_kernel(
         if (s == 0) PH_MARK(kPhU0Issued);
         stage_fwht<NWR, true, true>(xst, reinterpret_cast<float*>(xst + B * RS), xr, xrs, K, B,
                                     k0, kw, nsl, RS, fwht_block, fwht_scale, tid, counter + 1 PH_ARG);
+        if constexpr (da_all) {
+          issue(s, u1, ring[1]);
+          unit_decode<FMT, XDT>(ring[0], dec);
+        }
       } else {
         u0 = wave - NWR;
         issue(s, u0, ring[0]);
@@ -1163,7 +1172,7 @@ __global__ __launch_bounds__(NW * 64) void gemv_kernel(
       }
       __syncthreads();  // x staged
       PH_MARK(kPhStaged);
-      if (rw) {
+      if (rw && !da_all) {
         issue(s, u1, ring[1]);
         __builtin_amdgcn_sched_barrier(0);  // keep the prefetch ahead of the compute
         if (u0 < nu) process(ring[0], s, u0);
@@ -1414,7 +1423,8 @@ struct Plan {
   int xp = 4;    // x chunks each thread preloads per slice: 4, or 8 for larger slices
   size_t lds = 0;
   int P = 0;     // kSplitK: K-parts run side by side (grid grid x P); 0: slices in turn
-  bool da = false;  // kRotDA: batch-1 rotation with decode-ahead waves (16 per workgroup)
+  bool da = false;      // kRotDA: batch-1 rotation with decode-ahead waves
+  bool da_all = false;  // kRotDAall: the same, every wave decoding ahead (one unit per wave)
 };
 
 
@@ -1484,6 +1494,10 @@ bool make_plan(const fb_shape_t* s, int cus, Plan& pl) {
       // decoding ahead, 128 registers): 6.67, 10.36.
       pl.da = s->fwht_block > 256 && s->B == 1 && S == 1 && pass == 0 &&
               (s->K + 255) / 256 <= kWaves / 4 * kXPre;
+      // every wave decoding ahead where a workgroup owns at most one unit per wave; measured
+      // on 4096^2 (one tile of 8 units per workgroup) 5.66 -> 5.46 us, and slower where the
+      // workgroups own more (4096 -> 11008: 9.37 -> 9.93)
+      pl.da_all = pl.da && (pl.tq + (pl.tr ? 1 : 0)) * SPL <= nw;
       return true;
     }
   }
@@ -1593,8 +1607,10 @@ int launch_mode(int mode, const void* wdev, const void* x, void* y, const fb_sha
   // per CU: the GF4 copy's registers leave room for no second one)
   if constexpr (ilp) {
     if ((mode == kRot1 || mode == kFlat1) && pl.nw == kWaves / 2)
-      return fb_ilp::launch(FMT, XDT, mode == kRot1 && pl.da ? kRotDA : mode, wdev, x, y, s,
-                            pl.grid, pl.SPL, pl.GS, pl.tq, pl.tr, pl.S, pl.lds, deep, stream);
+      return fb_ilp::launch(FMT, XDT,
+                            mode != kRot1 ? mode : pl.da_all ? kRotDAall : pl.da ? kRotDA : mode,
+                            wdev, x, y, s, pl.grid, pl.SPL, pl.GS, pl.tq, pl.tr, pl.S, pl.lds,
+                            deep, stream);
   }
   if (mode == kSplitK)
     return deep ? launch_gemv<FMT, XDT, kSplitK, kWaves, 8>(wdev, x, y, s, pl, stream)
@@ -1908,6 +1924,12 @@ int launch(int fmt, int xdt, int mode, const void* wdev, const void* x, void* y,
     return fmt == FB_FMT_GF4
                ? launch_gemv<FB_FMT_GF4, FB_DT_F16, kRotDA, kWaves / 2, 4>(wdev, x, y, s, pl, stream)
                : launch_gemv<FB_FMT_E2M1, FB_DT_F16, kRotDA, kWaves / 2, 4>(wdev, x, y, s, pl, stream);
+  }
+  if (mode == kRotDAall) {
+    if (xdt != FB_DT_F16) return FB_ERR_DTYPE;
+    return fmt == FB_FMT_GF4
+               ? launch_gemv<FB_FMT_GF4, FB_DT_F16, kRotDAall, kWaves / 2, 4>(wdev, x, y, s, pl, stream)
+               : launch_gemv<FB_FMT_E2M1, FB_DT_F16, kRotDAall, kWaves / 2, 4>(wdev, x, y, s, pl, stream);
   }
   // kFlat1: GF4 with fp16 x, E2M1 with fp16 or bf16 x
   if (xp8) {
