@@ -598,6 +598,49 @@ def jenks2_filters_bench(shape, steps: int) -> dict:
             "identical_to_host": bool(same)}
 
 
+def xfill_bench(steps: int = 200) -> list:
+    """The fill rate of x staging alone (fb_phase_xfill of the diagnostic library): one
+    workgroup per CU reads the same x bytes into LDS in 16-byte chunks, the way the GEMV's x
+    preload does, with no weight stream beside it.  Per size (16 KiB ... 256 KiB: batch 1 to 16
+    at K = 8192), threads (1024 = the 16-wave plan, 512 = the 8-wave one) and passes (a second
+    pass reads what the first left in the caches): the median over waves of the time from the
+    wave's own start until its loads are issued, until they have arrived and until the
+    barrier, in µs of the 100 MHz chip clock, and µs per launch back to back (HIP events)."""
+    tl = ctypes.CDLL(str(ROOT / "if_i_could_turn_back_time_amd" / "libfourbit_trace.so"))
+    vp, ci = ctypes.c_void_p, ctypes.c_int
+    tl.fb_phase_xfill.argtypes = [vp, ci, ci, ci, ci, vp, vp]
+    tl.fb_phase_xfill.restype = ci
+    grid = torch.cuda.get_device_properties(0).multi_processor_count
+    x = torch.randint(0, 255, (256 * 1024,), dtype=torch.uint8, device="cuda:0")
+    ts = torch.zeros(grid * 16 * 4, dtype=torch.int64, device="cuda:0")
+    stream = torch.cuda.current_stream()
+    sp = stream.cuda_stream
+    out = []
+    for threads in (1024, 512):
+        for kib in (16, 32, 64, 128, 256):
+            for passes in (1, 2):
+                args = (x.data_ptr(), kib * 1024, threads, passes, grid, ts.data_ptr(), sp)
+                for _ in range(200):  # past the clock ramp
+                    C.check(tl.fb_phase_xfill(*args))
+                torch.cuda.synchronize()
+                e0 = torch.cuda.Event(enable_timing=True)
+                e1 = torch.cuda.Event(enable_timing=True)
+                e0.record(stream)
+                for _ in range(steps):
+                    tl.fb_phase_xfill(*args)
+                e1.record(stream)
+                C.check(tl.fb_phase_xfill(*args))  # the launch whose timestamps are read
+                torch.cuda.synchronize()
+                nw = threads // 64
+                t = ts[: grid * nw * 4].view(grid * nw, 4).cpu().double() / 100.0
+                own = [float((t[:, i] - t[:, 0]).median()) for i in (1, 2, 3)]
+                out.append({"xfill_KiB": kib, "threads": threads, "passes": passes, "grid": grid,
+                            "us_per_launch": e0.elapsed_time(e1) / steps * 1e3,
+                            "issued_us": own[0], "arrived_us": own[1], "barrier_us": own[2],
+                            "span_us": float(t[:, 3].max() - t[:, 0].min())})
+    return out
+
+
 FLOOR_WORKLOADS = ("gf4_k4096_n4096_b1", "e2m1_k4096_n4096_b1", "e2m1_k4096_n11008_b1",
                    "e2m1_k11008_n4096_b1", "gf4fwht_k4096_n4096_b1", "gf4fwht_k4096_n11008_b1",
                    "gf4fwht_k11008_n4096_b1", "gf4_k8192_n28672_b1")
@@ -733,6 +776,9 @@ def main():
                     help="only time the launch floor (an empty kernel with each batch-1 "
                          "workload's plan) against the GEMV, one JSON line per workload "
                          "(--workload narrows it to one)")
+    ap.add_argument("--xfill", action="store_true",
+                    help="only time x staging alone (every CU reading the same 16-256 KiB into "
+                         "LDS, no weights), one JSON line per size, thread count and pass count")
     ap.add_argument("--jenks2-filters", default="", metavar="OUT,IN,KH,KW",
                     help="only time the per-filter Jenks mask (fb_jenks2_filters_gpu) on a "
                          "convolution weight of that shape")
@@ -760,6 +806,10 @@ def main():
         return
     if args.jenks2:
         print(json.dumps(jenks2_bench(args.jenks2, min(args.steps, 50))))
+        return
+    if args.xfill:
+        for rec in xfill_bench(min(args.steps, 200)):
+            print(json.dumps(rec), flush=True)
         return
     if args.floor:
         names = [args.workload] if args.workload in FLOOR_WORKLOADS and "--workload" in sys.argv \

@@ -1865,6 +1865,59 @@ int launch_floor(const fb_shape_t* s, const Plan& pl, hipStream_t stream) {
   return hipGetLastError() == hipSuccess ? FB_OK : FB_ERR_HIP;
 }
 
+// The fill rate of x staging alone (diagnostic library only): every workgroup reads the same
+// xbytes of x in 16-byte chunks through a buffer resource, XP per thread, the way the GEMV's
+// x preload does, writes them to LDS and meets at a barrier; no weight stream runs beside it.
+// Each wave records s_memrealtime (100 MHz) at its start, after its loads are issued, after they
+// have arrived and after the barrier, at ts[((blockIdx.x * NT / 64) + wave) * 4 + i], for the
+// last of `passes` rounds (a second round reads x that the first left in the caches).
+template <int NT, int XP>
+__global__ __launch_bounds__(NT) void xfill_kernel(const uint8_t* __restrict__ x, int xbytes,
+                                                   int passes, unsigned long long* __restrict__ ts) {
+  extern __shared__ __align__(16) uint8_t lds[];
+  const rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(x), (short)0, xbytes,
+                                                      kRsrcWord3);
+  const int n = xbytes / 16;
+  unsigned long long t[4];
+  t[0] = __builtin_amdgcn_s_memrealtime();
+  for (int p = 0; p < passes; ++p) {
+    u32x4 v[XP];
+#pragma unroll
+    for (int j = 0; j < XP; ++j) {
+      const int c = threadIdx.x + j * NT;
+      if (c < n)
+        v[j] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, c * 16, 0, 0));
+    }
+    t[1] = __builtin_amdgcn_s_memrealtime();
+#pragma unroll
+    for (int j = 0; j < XP; ++j) {
+      const int c = threadIdx.x + j * NT;
+      if (c < n) *reinterpret_cast<u32x4*>(lds + (c & 8191) * 16) = v[j];
+    }
+    __builtin_amdgcn_s_waitcnt(0);
+    t[2] = __builtin_amdgcn_s_memrealtime();
+    __syncthreads();
+    t[3] = __builtin_amdgcn_s_memrealtime();
+  }
+  if ((threadIdx.x & 63) == 0) {
+    unsigned long long* o = ts + ((size_t)blockIdx.x * (NT / 64) + (threadIdx.x >> 6)) * 4;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) o[i] = t[i];
+  }
+}
+
+template <int NT, int XP>
+int launch_xfill(const void* x, int xbytes, int passes, int grid, void* ts, hipStream_t stream) {
+  auto kern = xfill_kernel<NT, XP>;
+  if (hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                          hipFuncAttributeMaxDynamicSharedMemorySize, kLdsLimit) != hipSuccess)
+    return FB_ERR_HIP;
+  hipLaunchKernelGGL(kern, dim3(grid), dim3(NT), 8192 * 16, stream,
+                     static_cast<const uint8_t*>(x), xbytes, passes,
+                     static_cast<unsigned long long*>(ts));
+  return hipGetLastError() == hipSuccess ? FB_OK : FB_ERR_HIP;
+}
+
 // The launch floor of the native FP4 path's split (diagnostic library only): a kernel with
 // mx_split_kernel's grid, block and arguments that does nothing.  fb_phase_mx_floor launches
 // it and then the GEMV on a split made beforehand, so its time per call against
@@ -2100,6 +2153,29 @@ int fb_phase_force_parts(int parts) {
   if (parts != 0 && parts != -1 && parts != 2 && parts != 4 && parts != 8) return FB_ERR_SHAPE;
   g_force_parts.store(parts, std::memory_order_relaxed);
   return FB_OK;
+}
+
+// Launches xfill_kernel: grid workgroups of `threads` (512 or 1024) threads each read the same
+// xbytes (a multiple of 16, at most 256 KiB) of x into LDS, `passes` (1 or 2) times; ts holds
+// grid * threads / 64 * 4 timestamps.
+int fb_phase_xfill(const void* x, int xbytes, int threads, int passes, int grid, void* ts,
+                   void* stream) {
+  if (!x || !ts) return FB_ERR_NULL;
+  if (xbytes < 16 || xbytes % 16 || xbytes > 256 * 1024 || (threads != 512 && threads != 1024) ||
+      passes < 1 || passes > 2 || grid < 1 || grid > 65535)
+    return FB_ERR_SHAPE;
+  hipStream_t hs = static_cast<hipStream_t>(stream);
+  const int per = (xbytes / 16 + threads - 1) / threads;  // chunks per thread
+  if (threads == 1024) {
+    if (per <= 1) return launch_xfill<1024, 1>(x, xbytes, passes, grid, ts, hs);
+    if (per <= 4) return launch_xfill<1024, 4>(x, xbytes, passes, grid, ts, hs);
+    if (per <= 8) return launch_xfill<1024, 8>(x, xbytes, passes, grid, ts, hs);
+    return launch_xfill<1024, 16>(x, xbytes, passes, grid, ts, hs);
+  }
+  if (per <= 2) return launch_xfill<512, 2>(x, xbytes, passes, grid, ts, hs);
+  if (per <= 8) return launch_xfill<512, 8>(x, xbytes, passes, grid, ts, hs);
+  if (per <= 16) return launch_xfill<512, 16>(x, xbytes, passes, grid, ts, hs);
+  return launch_xfill<512, 32>(x, xbytes, passes, grid, ts, hs);
 }
 
 // Launches floor_kernel with the plan fb_gemv would launch for a batch-1 shape that runs one

@@ -36,7 +36,8 @@ def test_diagnostic_trace_library_exports():
     """libfourbit_trace.so (the GEMV with per-wave phase timestamps, read by
     `bench.py --phase-trace`) exports the same C ABI plus its diagnostic entry points (the
     phase buffer, the launch plan, the launch-floor kernels of the GEMV and of the FP4 path's
-    split, the forced split-K part count); the product library exports none of those."""
+    split, the forced split-K part count, the x fill-rate kernel); the product library exports
+    none of those."""
     path = Path(C.__file__).resolve().parent / "libfourbit_trace.so"
     T = ctypes.CDLL(str(path))
     for name in C.EXPORTED:
@@ -50,8 +51,14 @@ def test_diagnostic_trace_library_exports():
     assert T.fb_phase_force_parts(3) == -2 and T.fb_phase_force_parts(0) == 0
     T.fb_phase_mx_floor.argtypes = [ctypes.c_void_p] * 5 + [ctypes.c_size_t, ctypes.c_void_p]
     assert T.fb_phase_mx_floor(None, None, None, None, None, 0, None) == -1
+    T.fb_phase_xfill.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                 ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p]
+    assert T.fb_phase_xfill(None, 16, 1024, 1, 1, None, None) == -1
+    one = ctypes.c_char_p(b"x")  # any non-null pointer: the shape is checked before any launch
+    for xb, nt, passes in ((24, 1024, 1), (512 * 1024, 1024, 1), (16, 256, 1), (16, 512, 3)):
+        assert T.fb_phase_xfill(one, xb, nt, passes, 1, one, None) == -2
     for name in ("fb_phase_trace_set", "fb_phase_plan", "fb_phase_floor", "fb_phase_force_parts",
-                 "fb_phase_mx_floor"):
+                 "fb_phase_mx_floor", "fb_phase_xfill"):
         with pytest.raises(AttributeError):
             getattr(C.lib(), name)
 
