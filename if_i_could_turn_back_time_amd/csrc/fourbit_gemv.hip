@@ -1186,6 +1186,11 @@ __global__ __launch_bounds__(NW * 64) void gemv_kernel(
       // first weight unit arrive later: wait for x first
       if constexpr (rot) __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
       if (rot && s == 0) PH_MARK(kPhXArrived);
+      // E2M1 at batch >= 2: the workgroup's x requests all enter the CU's load queue before
+      // any weight request (a wave that starts late would otherwise queue its x behind the
+      // others' first units, and the staging barrier waits for it)
+      if constexpr (FMT == FB_FMT_E2M1 && !rot && !flat1)
+        if (s == s_begin) __builtin_amdgcn_s_barrier();
       issue(s, u0, ring[0]);
       if (s == 0) PH_MARK(kPhU0Issued);
       // The next slice's x (into registers) and first weight unit are requested before the
