@@ -40,7 +40,7 @@ namespace fb_ilp {
 // the library's ABI.
 __attribute__((visibility("hidden"))) int launch(int fmt, int xdt, int mode, const void* wdev, const void* x, void* y,
            const fb_shape_t* s, int grid, int SPL, int GS, int tq, int tr, int S, size_t lds,
-           bool xp8, hipStream_t stream);
+           int xp, hipStream_t stream);
 }  // namespace fb_ilp
 
 namespace {
@@ -1458,13 +1458,22 @@ size_t plan_lds(const fb_shape_t* s, int tpw, int SPL) {
 //   4096 -> 11008 8.77 -> 8.19; E2M1 8192 -> 28672 20.58 -> 20.28; the rest within 0.1.
 //   Rotated, against 16 waves on the rotated kernel's max-ILP copy: 4096^2 7.27 -> 6.96,
 //   4096 -> 11008 10.58 -> 10.06, 11008 -> 4096 10.35 -> 9.60, 8192^2 14.45 -> 13.95.
+// - Unrotated GF4 at batch 2-8 with at most 2 row tiles per CU, whose x fits one slice: the
+//   same (one 8-wave workgroup per CU on the max-ILP copy, x preloaded 16 chunks per thread
+//   where it needs them).  Measured against 16 waves, same box, median us (bitwise-equal
+//   outputs): 8192^2 B=2 12.71 -> 11.61, B=4 12.92 -> 11.85, B=8 13.63 -> 12.87; 4096^2
+//   B=2 6.06 -> 5.36, B=4 6.23 -> 5.62, B=8 6.35 -> 5.85; 28672 -> 8192 B=2 31.09 -> 30.64.
+//   With more row tiles per CU 16 waves were faster (8192 -> 28672 B=2 30.53 / 30.68, B=4
+//   30.71 / 31.39), and so was E2M1 (8192^2 B=8 8.90 / 9.48).
 // - The native FP4 path's batch-1 layers with few row tiles per CU (at most 2) and LDS that
 //   fits twice in a CU: two 8-wave workgroups per CU.
 // - Otherwise one 16-wave workgroup per CU.
 bool make_plan(const fb_shape_t* s, int cus, Plan& pl) {
   const int GS = (s->K / 128 + 3) / 4;
   const int T = (s->N + 15) / 16;
-  const bool one8 = s->B == 1 && s->fmt != kFmtMx;
+  const bool one8 = (s->B == 1 && s->fmt != kFmtMx) ||
+                    (s->fmt == FB_FMT_GF4 && !s->fwht_block && s->B <= 8 && T <= 2 * cus &&
+                     s->x_dtype == FB_DT_F16);
   const bool half = one8 || (!s->fwht_block && s->B == 1 && T <= 2 * cus);
   for (int pass = half ? 0 : 1; pass < 2; ++pass) {
     const int nw = pass == 0 ? kWaves / 2 : kWaves;
@@ -1488,7 +1497,9 @@ bool make_plan(const fb_shape_t* s, int cus, Plan& pl) {
       pl.tq = T / grid;
       pl.tr = T % grid;
       pl.nw = nw;
-      pl.xp = (s->B * SPL + nw - 1) / nw <= 4 ? 4 : 8;  // 16-byte chunks per thread
+      // 16-byte x chunks per thread: 4 or 8 (16 only in the 8-wave batch 2-8 plan)
+      const int chunks = (s->B * SPL + nw - 1) / nw;
+      pl.xp = chunks <= 4 ? 4 : chunks <= 8 || nw == kWaves || s->B == 1 ? 8 : 16;
       pl.lds = lds;
       // The 8-wave rotated plan with decode-ahead waves (kRotDA) where half the waves can
       // rotate x: blocks larger than one 256-value sub-block (whose rotation has a barrier's
@@ -1599,23 +1610,24 @@ int launch_gemv(const void* wdev, const void* x, void* y, const fb_shape_t* s, c
 }
 
 // The host side from here to the end of the file is compiled in the default unit only, so
-// that the max-ILP unit instantiates no kernel but its own two.
+// that the max-ILP unit instantiates no kernel but its own.
 #ifndef FB_GEMV_ILP_TU
 
 template <int FMT, int XDT>
 int launch_mode(int mode, const void* wdev, const void* x, void* y, const fb_shape_t* s,
                 const Plan& pl, hipStream_t stream) {
-  const bool deep = pl.xp == 8;
-  // fb_ilp::launch starts these two kernels (instantiated in the max-ILP unit, not here)
+  const bool deep = pl.xp >= 8;
+  // fb_ilp::launch starts these kernels (instantiated in the max-ILP unit, not here)
   constexpr bool ilp = FMT != kFmtMx;
-  // the max-ILP copies: the rotated batch-1 kernel and the 8-wave batch-1 one (one workgroup
-  // per CU: the GF4 copy's registers leave room for no second one)
+  // the max-ILP copies: the rotated batch-1 kernel, the 8-wave batch-1 one and the 8-wave GF4
+  // batch 2-8 one (one workgroup per CU: the GF4 copies' registers leave room for no second)
   if constexpr (ilp) {
-    if ((mode == kRot1 || mode == kFlat1) && pl.nw == kWaves / 2)
+    if ((mode == kRot1 || mode == kFlat1 || (mode == kFlat && FMT == FB_FMT_GF4)) &&
+        pl.nw == kWaves / 2)
       return fb_ilp::launch(FMT, XDT,
                             mode != kRot1 ? mode : pl.da_all ? kRotDAall : pl.da ? kRotDA : mode,
                             wdev, x, y, s, pl.grid, pl.SPL, pl.GS, pl.tq, pl.tr, pl.S, pl.lds,
-                            deep, stream);
+                            pl.xp, stream);
   }
   if (mode == kSplitK)
     return deep ? launch_gemv<FMT, XDT, kSplitK, kWaves, 8>(wdev, x, y, s, pl, stream)
@@ -1960,7 +1972,7 @@ void* scratch_ptr(int dev) {
 namespace fb_ilp {
 int launch(int fmt, int xdt, int mode, const void* wdev, const void* x, void* y,
            const fb_shape_t* s, int grid, int SPL, int GS, int tq, int tr, int S, size_t lds,
-           bool xp8, hipStream_t stream) {
+           int xp, hipStream_t stream) {
   Plan pl;
   pl.grid = grid;
   pl.SPL = SPL;
@@ -1969,7 +1981,7 @@ int launch(int fmt, int xdt, int mode, const void* wdev, const void* x, void* y,
   pl.tr = tr;
   pl.S = S;
   pl.lds = lds;
-  pl.xp = xp8 ? 8 : 4;
+  pl.xp = xp;
   pl.nw = kWaves / 2;
   if (mode == kRot1) {  // a rotation takes fp16 x (and preloads its own way)
     if (xdt != FB_DT_F16) return FB_ERR_DTYPE;
@@ -1989,8 +2001,14 @@ int launch(int fmt, int xdt, int mode, const void* wdev, const void* x, void* y,
                ? launch_gemv<FB_FMT_GF4, FB_DT_F16, kRotDAall, kWaves / 2, 4>(wdev, x, y, s, pl, stream)
                : launch_gemv<FB_FMT_E2M1, FB_DT_F16, kRotDAall, kWaves / 2, 4>(wdev, x, y, s, pl, stream);
   }
+  if (mode == kFlat) {  // GF4 at batch 2-8 in one K-slice
+    if (fmt != FB_FMT_GF4 || xdt != FB_DT_F16) return FB_ERR_DTYPE;
+    if (xp == 4) return launch_gemv<FB_FMT_GF4, FB_DT_F16, kFlat, kWaves / 2, 4>(wdev, x, y, s, pl, stream);
+    if (xp == 8) return launch_gemv<FB_FMT_GF4, FB_DT_F16, kFlat, kWaves / 2, 8>(wdev, x, y, s, pl, stream);
+    return launch_gemv<FB_FMT_GF4, FB_DT_F16, kFlat, kWaves / 2, 16>(wdev, x, y, s, pl, stream);
+  }
   // kFlat1: GF4 with fp16 x, E2M1 with fp16 or bf16 x
-  if (xp8) {
+  if (xp >= 8) {
     if (fmt == FB_FMT_GF4)
       return launch_gemv<FB_FMT_GF4, FB_DT_F16, kFlat1, kWaves / 2, 8>(wdev, x, y, s, pl, stream);
     if (xdt == FB_DT_BF16)

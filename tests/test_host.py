@@ -96,6 +96,31 @@ def test_batch1_plans_over_a_shape_sweep():
     assert (C.FMT_E2M1, 512, 2_200_000, 538) in over
 
 
+def test_small_batch_wave_plans():
+    """Batches 2-8 (fb_phase_plan, host-side, 256 CUs): unrotated GF4 layers of at most 2 row
+    tiles per CU whose x fits one K-slice run one 8-wave workgroup per CU; E2M1, layers of
+    more row tiles per CU, rotated layers and x that needs K-slices keep 16-wave
+    workgroups."""
+    T_lib = ctypes.CDLL(str(Path(C.__file__).resolve().parent / "libfourbit_trace.so"))
+    ip = ctypes.POINTER(ctypes.c_int)
+    T_lib.fb_phase_plan.argtypes = [ctypes.POINTER(C.FbShape), ip, ip, ip, ip, ip, ip]
+
+    def plan(fmt, K, N, B, fb=0):
+        xdt = C.DT_F16 if fmt == C.FMT_GF4 else C.DT_BF16
+        s = C.make_shape(N, K, B, fmt, fb, xdt, C.DT_F16)
+        v = [ctypes.c_int() for _ in range(6)]
+        assert T_lib.fb_phase_plan(ctypes.byref(s), *[ctypes.byref(a) for a in v]) == 0
+        return v[1].value, v[2].value  # waves, slices
+
+    for K, N, B in ((8192, 8192, 2), (8192, 8192, 8), (4096, 4096, 4), (28672, 8192, 2)):
+        assert plan(C.FMT_GF4, K, N, B) == (8, 1), (K, N, B)
+        assert plan(C.FMT_E2M1, K, N, B)[0] == 16, (K, N, B)
+    assert plan(C.FMT_GF4, 8192, 28672, 2)[0] == 16  # 7 row tiles per CU
+    assert plan(C.FMT_GF4, 8192, 8192, 16) == (16, 2)  # batch 16: two K-slices
+    assert plan(C.FMT_GF4, 28672, 8192, 4)[0] == 16  # x needs two K-slices
+    assert plan(C.FMT_GF4, 4096, 4096, 2, fb=4096)[0] == 16  # rotated in the kernel
+
+
 @pytest.mark.parametrize("kw,err", [
     (dict(K=100), -2), (dict(K=0), -2), (dict(N=0), -2), (dict(B=0), -2),
     (dict(group=64), -3), (dict(fmt=7), -4), (dict(x_dtype=C.DT_BF16), -5),
