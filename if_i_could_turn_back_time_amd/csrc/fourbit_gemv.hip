@@ -1458,13 +1458,15 @@ size_t plan_lds(const fb_shape_t* s, int tpw, int SPL) {
 //   4096 -> 11008 8.77 -> 8.19; E2M1 8192 -> 28672 20.58 -> 20.28; the rest within 0.1.
 //   Rotated, against 16 waves on the rotated kernel's max-ILP copy: 4096^2 7.27 -> 6.96,
 //   4096 -> 11008 10.58 -> 10.06, 11008 -> 4096 10.35 -> 9.60, 8192^2 14.45 -> 13.95.
-// - Unrotated GF4 at batch 2-8 with at most 2 row tiles per CU, whose x fits one slice: the
-//   same (one 8-wave workgroup per CU on the max-ILP copy, x preloaded 16 chunks per thread
-//   where it needs them).  Measured against 16 waves, same box, median us (bitwise-equal
+// - Unrotated GF4 at batch 2-8 with at most 2 row tiles per CU, whose x fits one or two
+//   K-slices: the same (one 8-wave workgroup per CU on the max-ILP copy, x preloaded 16
+//   chunks per thread where it needs them).  Measured against 16 waves, same box, median us (bitwise-equal
 //   outputs): 8192^2 B=2 12.71 -> 11.61, B=4 12.92 -> 11.85, B=8 13.63 -> 12.87; 4096^2
 //   B=2 6.06 -> 5.36, B=4 6.23 -> 5.62, B=8 6.35 -> 5.85; 28672 -> 8192 B=2 31.09 -> 30.64.
-//   With more row tiles per CU 16 waves were faster (8192 -> 28672 B=2 30.53 / 30.68, B=4
-//   30.71 / 31.39), and so was E2M1 (8192^2 B=8 8.90 / 9.48).
+//   Two K-slices: 11008 -> 4096 B=8 12.31 -> 11.60, 28672 -> 8192 B=4 unchanged (34.27 /
+//   34.30); with four (28672 -> 8192 B=8) 39.10 / 41.31, so no more than two.  With more
+//   row tiles per CU 16 waves were faster (8192 -> 28672 B=2 30.53 / 30.68, B=4 30.71 /
+//   31.39), and so was E2M1 (8192^2 B=8 8.90 / 9.48).
 // - The native FP4 path's batch-1 layers with few row tiles per CU (at most 2) and LDS that
 //   fits twice in a CU: two 8-wave workgroups per CU.
 // - Otherwise one 16-wave workgroup per CU.
@@ -1487,7 +1489,8 @@ bool make_plan(const fb_shape_t* s, int cus, Plan& pl) {
         SPL = (SPL + bs - 1) / bs * bs;
       }
       if ((S - 1) * SPL >= GS) continue;  // the last slice would have no span
-      if (pass == 0 && S > 1) break;  // 8-wave workgroups only with one K-slice
+      // 8-wave workgroups with one K-slice at batch 1, at most two at batch 2-8 (GF4)
+      if (pass == 0 && S > (s->B == 1 ? 1 : 2)) break;
       const size_t lds = plan_lds(s, tpw, SPL);
       if (lds > limit) continue;
       pl.S = S;
@@ -1622,7 +1625,8 @@ int launch_mode(int mode, const void* wdev, const void* x, void* y, const fb_sha
   // the max-ILP copies: the rotated batch-1 kernel, the 8-wave batch-1 one and the 8-wave GF4
   // batch 2-8 one (one workgroup per CU: the GF4 copies' registers leave room for no second)
   if constexpr (ilp) {
-    if ((mode == kRot1 || mode == kFlat1 || (mode == kFlat && FMT == FB_FMT_GF4)) &&
+    if ((mode == kRot1 || mode == kFlat1 ||
+         ((mode == kFlat || mode == kSliced) && FMT == FB_FMT_GF4)) &&
         pl.nw == kWaves / 2)
       return fb_ilp::launch(FMT, XDT,
                             mode != kRot1 ? mode : pl.da_all ? kRotDAall : pl.da ? kRotDA : mode,
@@ -2000,6 +2004,12 @@ int launch(int fmt, int xdt, int mode, const void* wdev, const void* x, void* y,
     return fmt == FB_FMT_GF4
                ? launch_gemv<FB_FMT_GF4, FB_DT_F16, kRotDAall, kWaves / 2, 4>(wdev, x, y, s, pl, stream)
                : launch_gemv<FB_FMT_E2M1, FB_DT_F16, kRotDAall, kWaves / 2, 4>(wdev, x, y, s, pl, stream);
+  }
+  if (mode == kSliced) {
+    if (fmt != FB_FMT_GF4 || xdt != FB_DT_F16) return FB_ERR_DTYPE;
+    if (xp == 4) return launch_gemv<FB_FMT_GF4, FB_DT_F16, kSliced, kWaves / 2, 4>(wdev, x, y, s, pl, stream);
+    if (xp == 8) return launch_gemv<FB_FMT_GF4, FB_DT_F16, kSliced, kWaves / 2, 8>(wdev, x, y, s, pl, stream);
+    return launch_gemv<FB_FMT_GF4, FB_DT_F16, kSliced, kWaves / 2, 16>(wdev, x, y, s, pl, stream);
   }
   if (mode == kFlat) {  // GF4 at batch 2-8 in one K-slice
     if (fmt != FB_FMT_GF4 || xdt != FB_DT_F16) return FB_ERR_DTYPE;
