@@ -1458,13 +1458,14 @@ size_t plan_lds(const fb_shape_t* s, int tpw, int SPL) {
 //   4096 -> 11008 8.77 -> 8.19; E2M1 8192 -> 28672 20.58 -> 20.28; the rest within 0.1.
 //   Rotated, against 16 waves on the rotated kernel's max-ILP copy: 4096^2 7.27 -> 6.96,
 //   4096 -> 11008 10.58 -> 10.06, 11008 -> 4096 10.35 -> 9.60, 8192^2 14.45 -> 13.95.
-// - Unrotated GF4 at batch 2-8 with at most 2 row tiles per CU, whose x fits one or two
+// - Unrotated GF4 at batch 2-16 with at most 2 row tiles per CU, whose x fits one or two
 //   K-slices: the same (one 8-wave workgroup per CU on the max-ILP copy, x preloaded 16
 //   chunks per thread where it needs them).  Measured against 16 waves, same box, median us (bitwise-equal
 //   outputs): 8192^2 B=2 12.71 -> 11.61, B=4 12.92 -> 11.85, B=8 13.63 -> 12.87; 4096^2
 //   B=2 6.06 -> 5.36, B=4 6.23 -> 5.62, B=8 6.35 -> 5.85; 28672 -> 8192 B=2 31.09 -> 30.64.
 //   Two K-slices: 11008 -> 4096 B=8 12.31 -> 11.60, 28672 -> 8192 B=4 unchanged (34.27 /
-//   34.30); with four (28672 -> 8192 B=8) 39.10 / 41.31, so no more than two.  With more
+//   34.30), 8192^2 B=16 15.49 -> 15.18, 4096^2 B=16 7.12 -> 6.73; with four (28672 -> 8192
+//   B=8) 39.10 / 41.31, so no more than two.  With more
 //   row tiles per CU 16 waves were faster (8192 -> 28672 B=2 30.53 / 30.68, B=4 30.71 /
 //   31.39), and so was E2M1 (8192^2 B=8 8.90 / 9.48).
 // - The native FP4 path's batch-1 layers with few row tiles per CU (at most 2) and LDS that
@@ -1474,7 +1475,7 @@ bool make_plan(const fb_shape_t* s, int cus, Plan& pl) {
   const int GS = (s->K / 128 + 3) / 4;
   const int T = (s->N + 15) / 16;
   const bool one8 = (s->B == 1 && s->fmt != kFmtMx) ||
-                    (s->fmt == FB_FMT_GF4 && !s->fwht_block && s->B <= 8 && T <= 2 * cus &&
+                    (s->fmt == FB_FMT_GF4 && !s->fwht_block && s->B <= 16 && T <= 2 * cus &&
                      s->x_dtype == FB_DT_F16);
   const bool half = one8 || (!s->fwht_block && s->B == 1 && T <= 2 * cus);
   for (int pass = half ? 0 : 1; pass < 2; ++pass) {
@@ -1489,7 +1490,7 @@ bool make_plan(const fb_shape_t* s, int cus, Plan& pl) {
         SPL = (SPL + bs - 1) / bs * bs;
       }
       if ((S - 1) * SPL >= GS) continue;  // the last slice would have no span
-      // 8-wave workgroups with one K-slice at batch 1, at most two at batch 2-8 (GF4)
+      // 8-wave workgroups with one K-slice at batch 1, at most two at batch 2-16 (GF4)
       if (pass == 0 && S > (s->B == 1 ? 1 : 2)) break;
       const size_t lds = plan_lds(s, tpw, SPL);
       if (lds > limit) continue;
@@ -1500,7 +1501,7 @@ bool make_plan(const fb_shape_t* s, int cus, Plan& pl) {
       pl.tq = T / grid;
       pl.tr = T % grid;
       pl.nw = nw;
-      // 16-byte x chunks per thread: 4 or 8 (16 only in the 8-wave batch 2-8 plan)
+      // 16-byte x chunks per thread: 4 or 8 (16 only in the 8-wave batch 2-16 plan)
       const int chunks = (s->B * SPL + nw - 1) / nw;
       pl.xp = chunks <= 4 ? 4 : chunks <= 8 || nw == kWaves || s->B == 1 ? 8 : 16;
       pl.lds = lds;
@@ -1623,7 +1624,7 @@ int launch_mode(int mode, const void* wdev, const void* x, void* y, const fb_sha
   // fb_ilp::launch starts these kernels (instantiated in the max-ILP unit, not here)
   constexpr bool ilp = FMT != kFmtMx;
   // the max-ILP copies: the rotated batch-1 kernel, the 8-wave batch-1 one and the 8-wave GF4
-  // batch 2-8 one (one workgroup per CU: the GF4 copies' registers leave room for no second)
+  // batch 2-16 ones (one workgroup per CU: the GF4 copies' registers leave room for no second)
   if constexpr (ilp) {
     if ((mode == kRot1 || mode == kFlat1 ||
          ((mode == kFlat || mode == kSliced) && FMT == FB_FMT_GF4)) &&
@@ -2011,7 +2012,7 @@ int launch(int fmt, int xdt, int mode, const void* wdev, const void* x, void* y,
     if (xp == 8) return launch_gemv<FB_FMT_GF4, FB_DT_F16, kSliced, kWaves / 2, 8>(wdev, x, y, s, pl, stream);
     return launch_gemv<FB_FMT_GF4, FB_DT_F16, kSliced, kWaves / 2, 16>(wdev, x, y, s, pl, stream);
   }
-  if (mode == kFlat) {  // GF4 at batch 2-8 in one K-slice
+  if (mode == kFlat) {  // GF4 at batch 2-16 in one K-slice
     if (fmt != FB_FMT_GF4 || xdt != FB_DT_F16) return FB_ERR_DTYPE;
     if (xp == 4) return launch_gemv<FB_FMT_GF4, FB_DT_F16, kFlat, kWaves / 2, 4>(wdev, x, y, s, pl, stream);
     if (xp == 8) return launch_gemv<FB_FMT_GF4, FB_DT_F16, kFlat, kWaves / 2, 8>(wdev, x, y, s, pl, stream);

@@ -97,7 +97,7 @@ def test_batch1_plans_over_a_shape_sweep():
 
 
 def test_small_batch_wave_plans():
-    """Batches 2-8 (fb_phase_plan, host-side, 256 CUs): unrotated GF4 layers of at most 2 row
+    """Batches 2-16 (fb_phase_plan, host-side, 256 CUs): unrotated GF4 layers of at most 2 row
     tiles per CU whose x fits one or two K-slices run one 8-wave workgroup per CU; E2M1,
     layers of more row tiles per CU, rotated layers and x that needs more K-slices keep
     16-wave workgroups."""
@@ -116,7 +116,7 @@ def test_small_batch_wave_plans():
         assert plan(C.FMT_GF4, K, N, B) == (8, 1), (K, N, B)
         assert plan(C.FMT_E2M1, K, N, B)[0] == 16, (K, N, B)
     assert plan(C.FMT_GF4, 8192, 28672, 2)[0] == 16  # 7 row tiles per CU
-    assert plan(C.FMT_GF4, 8192, 8192, 16) == (16, 2)  # batch 16: two K-slices
+    assert plan(C.FMT_GF4, 8192, 8192, 16) == (8, 2)  # batch 16: two K-slices
     assert plan(C.FMT_GF4, 11008, 4096, 8) == (8, 2)  # two K-slices
     assert plan(C.FMT_GF4, 28672, 8192, 4) == (8, 2)
     assert plan(C.FMT_GF4, 28672, 8192, 8)[0] == 16  # x needs four K-slices
