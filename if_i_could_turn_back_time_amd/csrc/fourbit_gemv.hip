@@ -1458,16 +1458,22 @@ size_t plan_lds(const fb_shape_t* s, int tpw, int SPL) {
 //   4096 -> 11008 8.77 -> 8.19; E2M1 8192 -> 28672 20.58 -> 20.28; the rest within 0.1.
 //   Rotated, against 16 waves on the rotated kernel's max-ILP copy: 4096^2 7.27 -> 6.96,
 //   4096 -> 11008 10.58 -> 10.06, 11008 -> 4096 10.35 -> 9.60, 8192^2 14.45 -> 13.95.
-// - Unrotated GF4 at batch 2-16 with at most 2 row tiles per CU, whose x fits one or two
-//   K-slices: the same (one 8-wave workgroup per CU on the max-ILP copy, x preloaded 16
-//   chunks per thread where it needs them).  Measured against 16 waves, same box, median us (bitwise-equal
-//   outputs): 8192^2 B=2 12.71 -> 11.61, B=4 12.92 -> 11.85, B=8 13.63 -> 12.87; 4096^2
-//   B=2 6.06 -> 5.36, B=4 6.23 -> 5.62, B=8 6.35 -> 5.85; 28672 -> 8192 B=2 31.09 -> 30.64.
-//   Two K-slices: 11008 -> 4096 B=8 12.31 -> 11.60, 28672 -> 8192 B=4 unchanged (34.27 /
-//   34.30), 8192^2 B=16 15.49 -> 15.18, 4096^2 B=16 7.12 -> 6.73; with four (28672 -> 8192
-//   B=8) 39.10 / 41.31, so no more than two.  With more
-//   row tiles per CU 16 waves were faster (8192 -> 28672 B=2 30.53 / 30.68, B=4 30.71 /
-//   31.39), and so was E2M1 (8192^2 B=8 8.90 / 9.48).
+// - Unrotated GF4 (and E2M1 with bf16 x) at batch 2-16 with at most 2 row tiles per CU,
+//   whose x fits one K-slice, or two of at most 4 units per wave each: the same (one 8-wave
+//   workgroup per CU on the max-ILP copy, x preloaded 16 chunks per thread where it needs
+//   them).  Measured against 16 waves, same box, median us (bitwise-equal outputs):
+//   - GF4, one slice: 8192^2 B=2 12.71 -> 11.61, B=4 12.92 -> 11.85, B=8 13.63 -> 12.87;
+//     4096^2 B=2 6.06 -> 5.36, B=4 6.23 -> 5.62, B=8 6.35 -> 5.85; 28672 -> 8192 B=2
+//     31.09 -> 30.64;
+//   - GF4, two slices: 11008 -> 4096 B=8 12.31 -> 11.60, 8192^2 B=16 15.49 -> 15.18,
+//     4096^2 B=16 7.12 -> 6.73; but 28672 -> 8192 B=4 (7 units per wave per slice) 33.24 on
+//     16 waves against 33.60, and with four slices (28672 -> 8192 B=8) 39.10 / 41.31;
+//   - E2M1 (bf16 x), another box: 8192^2 B=8 9.04 -> 8.75, B=16 11.92 -> 11.67, 4096^2 B=4
+//     4.89 -> 4.32, 11008 -> 4096 B=8 9.48 -> 9.14 (an earlier build's 8-wave E2M1, with x
+//     past an 8-chunk preload loaded behind the first unit, had been slower: 8192^2 B=8
+//     8.90 / 9.48);
+//   - with more row tiles per CU 16 waves were faster (GF4 8192 -> 28672 B=2 30.53 / 30.68,
+//     B=4 30.71 / 31.39).
 // - The native FP4 path's batch-1 layers with few row tiles per CU (at most 2) and LDS that
 //   fits twice in a CU: two 8-wave workgroups per CU.
 // - Otherwise one 16-wave workgroup per CU.
@@ -1475,8 +1481,9 @@ bool make_plan(const fb_shape_t* s, int cus, Plan& pl) {
   const int GS = (s->K / 128 + 3) / 4;
   const int T = (s->N + 15) / 16;
   const bool one8 = (s->B == 1 && s->fmt != kFmtMx) ||
-                    (s->fmt == FB_FMT_GF4 && !s->fwht_block && s->B <= 16 && T <= 2 * cus &&
-                     s->x_dtype == FB_DT_F16);
+                    ((s->fmt == FB_FMT_GF4 && s->x_dtype == FB_DT_F16) ||
+                     (s->fmt == FB_FMT_E2M1 && s->x_dtype == FB_DT_BF16)) &&
+                     !s->fwht_block && s->B <= 16 && T <= 2 * cus;
   const bool half = one8 || (!s->fwht_block && s->B == 1 && T <= 2 * cus);
   for (int pass = half ? 0 : 1; pass < 2; ++pass) {
     const int nw = pass == 0 ? kWaves / 2 : kWaves;
@@ -1490,8 +1497,10 @@ bool make_plan(const fb_shape_t* s, int cus, Plan& pl) {
         SPL = (SPL + bs - 1) / bs * bs;
       }
       if ((S - 1) * SPL >= GS) continue;  // the last slice would have no span
-      // 8-wave workgroups with one K-slice at batch 1, at most two at batch 2-16 (GF4)
+      // 8-wave workgroups with one K-slice at batch 1, at most two at batch 2-16
       if (pass == 0 && S > (s->B == 1 ? 1 : 2)) break;
+      // two slices only where each wave has few units per slice
+      if (pass == 0 && S == 2 && tpw * SPL > 4 * nw) break;
       const size_t lds = plan_lds(s, tpw, SPL);
       if (lds > limit) continue;
       pl.S = S;
@@ -1623,11 +1632,12 @@ int launch_mode(int mode, const void* wdev, const void* x, void* y, const fb_sha
   const bool deep = pl.xp >= 8;
   // fb_ilp::launch starts these kernels (instantiated in the max-ILP unit, not here)
   constexpr bool ilp = FMT != kFmtMx;
-  // the max-ILP copies: the rotated batch-1 kernel, the 8-wave batch-1 one and the 8-wave GF4
-  // batch 2-16 ones (one workgroup per CU: the GF4 copies' registers leave room for no second)
+  // the max-ILP copies: the rotated batch-1 kernel, the 8-wave batch-1 one and the 8-wave
+  // batch 2-16 ones of GF4 and of E2M1 with bf16 x (one workgroup per CU: the GF4 copies'
+  // registers leave room for no second)
   if constexpr (ilp) {
     if ((mode == kRot1 || mode == kFlat1 ||
-         ((mode == kFlat || mode == kSliced) && FMT == FB_FMT_GF4)) &&
+         ((mode == kFlat || mode == kSliced) && (FMT == FB_FMT_GF4 || XDT == FB_DT_BF16))) &&
         pl.nw == kWaves / 2)
       return fb_ilp::launch(FMT, XDT,
                             mode != kRot1 ? mode : pl.da_all ? kRotDAall : pl.da ? kRotDA : mode,
@@ -2006,13 +2016,25 @@ int launch(int fmt, int xdt, int mode, const void* wdev, const void* x, void* y,
                ? launch_gemv<FB_FMT_GF4, FB_DT_F16, kRotDAall, kWaves / 2, 4>(wdev, x, y, s, pl, stream)
                : launch_gemv<FB_FMT_E2M1, FB_DT_F16, kRotDAall, kWaves / 2, 4>(wdev, x, y, s, pl, stream);
   }
+  if (mode == kSliced && fmt == FB_FMT_E2M1) {
+    if (xdt != FB_DT_BF16) return FB_ERR_DTYPE;
+    if (xp == 4) return launch_gemv<FB_FMT_E2M1, FB_DT_BF16, kSliced, kWaves / 2, 4>(wdev, x, y, s, pl, stream);
+    if (xp == 8) return launch_gemv<FB_FMT_E2M1, FB_DT_BF16, kSliced, kWaves / 2, 8>(wdev, x, y, s, pl, stream);
+    return launch_gemv<FB_FMT_E2M1, FB_DT_BF16, kSliced, kWaves / 2, 16>(wdev, x, y, s, pl, stream);
+  }
+  if (mode == kFlat && fmt == FB_FMT_E2M1) {
+    if (xdt != FB_DT_BF16) return FB_ERR_DTYPE;
+    if (xp == 4) return launch_gemv<FB_FMT_E2M1, FB_DT_BF16, kFlat, kWaves / 2, 4>(wdev, x, y, s, pl, stream);
+    if (xp == 8) return launch_gemv<FB_FMT_E2M1, FB_DT_BF16, kFlat, kWaves / 2, 8>(wdev, x, y, s, pl, stream);
+    return launch_gemv<FB_FMT_E2M1, FB_DT_BF16, kFlat, kWaves / 2, 16>(wdev, x, y, s, pl, stream);
+  }
   if (mode == kSliced) {
     if (fmt != FB_FMT_GF4 || xdt != FB_DT_F16) return FB_ERR_DTYPE;
     if (xp == 4) return launch_gemv<FB_FMT_GF4, FB_DT_F16, kSliced, kWaves / 2, 4>(wdev, x, y, s, pl, stream);
     if (xp == 8) return launch_gemv<FB_FMT_GF4, FB_DT_F16, kSliced, kWaves / 2, 8>(wdev, x, y, s, pl, stream);
     return launch_gemv<FB_FMT_GF4, FB_DT_F16, kSliced, kWaves / 2, 16>(wdev, x, y, s, pl, stream);
   }
-  if (mode == kFlat) {  // GF4 at batch 2-16 in one K-slice
+  if (mode == kFlat) {  // GF4 at batch 2-16 in one K-slice (E2M1: above)
     if (fmt != FB_FMT_GF4 || xdt != FB_DT_F16) return FB_ERR_DTYPE;
     if (xp == 4) return launch_gemv<FB_FMT_GF4, FB_DT_F16, kFlat, kWaves / 2, 4>(wdev, x, y, s, pl, stream);
     if (xp == 8) return launch_gemv<FB_FMT_GF4, FB_DT_F16, kFlat, kWaves / 2, 8>(wdev, x, y, s, pl, stream);
