@@ -1476,7 +1476,8 @@ size_t plan_lds(const fb_shape_t* s, int tpw, int SPL) {
 //     B=4 30.71 / 31.39).
 // - The native FP4 path's batch-1 layers with few row tiles per CU (at most 2) and LDS that
 //   fits twice in a CU: two 8-wave workgroups per CU.
-// - Otherwise one 16-wave workgroup per CU.
+// - Otherwise one 16-wave workgroup per CU (batches of more row tiles per CU, larger x, E2M1
+//   with fp16 x, rotated batches).
 bool make_plan(const fb_shape_t* s, int cus, Plan& pl) {
   const int GS = (s->K / 128 + 3) / 4;
   const int T = (s->N + 15) / 16;
