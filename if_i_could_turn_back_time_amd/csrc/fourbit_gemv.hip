@@ -1458,8 +1458,9 @@ size_t plan_lds(const fb_shape_t* s, int tpw, int SPL) {
 //   4096 -> 11008 8.77 -> 8.19; E2M1 8192 -> 28672 20.58 -> 20.28; the rest within 0.1.
 //   Rotated, against 16 waves on the rotated kernel's max-ILP copy: 4096^2 7.27 -> 6.96,
 //   4096 -> 11008 10.58 -> 10.06, 11008 -> 4096 10.35 -> 9.60, 8192^2 14.45 -> 13.95.
-// - Unrotated GF4 (and E2M1 with bf16 x) at batch 2-16 with at most 2 row tiles per CU,
-//   whose x fits one K-slice, or two of at most 4 units per wave each: the same (one 8-wave
+// - Unrotated GF4 (and E2M1 with bf16 x, exact or on the native FP4 path) at batch 2-16 with
+//   at most 2 row tiles per CU, whose x fits one K-slice, or two of at most 4 units per wave
+//   each: the same (one 8-wave
 //   workgroup per CU on the max-ILP copy, x preloaded 16 chunks per thread where it needs
 //   them).  Measured against 16 waves, same box, median us (bitwise-equal outputs):
 //   - GF4, one slice: 8192^2 B=2 12.71 -> 11.61, B=4 12.92 -> 11.85, B=8 13.63 -> 12.87;
@@ -1472,6 +1473,9 @@ size_t plan_lds(const fb_shape_t* s, int tpw, int SPL) {
 //     4.89 -> 4.32, 11008 -> 4096 B=8 9.48 -> 9.14 (an earlier build's 8-wave E2M1, with x
 //     past an 8-chunk preload loaded behind the first unit, had been slower: 8192^2 B=8
 //     8.90 / 9.48);
+//   - the native FP4 path (fb_gemv_mx, split included), another box: 8192^2 B=16 14.79 ->
+//     13.99, 11008 -> 4096 B=8 12.30 -> 11.61, 4096^2 B=4 6.81 -> 6.26, B=8 7.33 -> 7.19;
+//     8192^2 B=2 9.82 -> 9.76, B=4 10.13 -> 10.20, B=8 10.96 -> 11.17;
 //   - with more row tiles per CU 16 waves were faster (GF4 8192 -> 28672 B=2 30.53 / 30.68,
 //     B=4 30.71 / 31.39).
 // - The native FP4 path's batch-1 layers with few row tiles per CU (at most 2) and LDS that
@@ -1483,7 +1487,8 @@ bool make_plan(const fb_shape_t* s, int cus, Plan& pl) {
   const int T = (s->N + 15) / 16;
   const bool one8 = (s->B == 1 && s->fmt != kFmtMx) ||
                     ((s->fmt == FB_FMT_GF4 && s->x_dtype == FB_DT_F16) ||
-                     (s->fmt == FB_FMT_E2M1 && s->x_dtype == FB_DT_BF16)) &&
+                     (s->fmt == FB_FMT_E2M1 && s->x_dtype == FB_DT_BF16) ||
+                     (s->fmt == kFmtMx && s->B >= 2)) &&
                      !s->fwht_block && s->B <= 16 && T <= 2 * cus;
   const bool half = one8 || (!s->fwht_block && s->B == 1 && T <= 2 * cus);
   for (int pass = half ? 0 : 1; pass < 2; ++pass) {
@@ -1633,9 +1638,15 @@ int launch_mode(int mode, const void* wdev, const void* x, void* y, const fb_sha
   const bool deep = pl.xp >= 8;
   // fb_ilp::launch starts these kernels (instantiated in the max-ILP unit, not here)
   constexpr bool ilp = FMT != kFmtMx;
+  // the native FP4 path's 8-wave batch 2-16 plan (its batch-1 layers, two 8-wave workgroups
+  // per CU, run below in this unit)
+  if constexpr (FMT == kFmtMx)
+    if ((mode == kFlat || mode == kSliced) && pl.nw == kWaves / 2)
+      return fb_ilp::launch(FMT, XDT, mode, wdev, x, y, s, pl.grid, pl.SPL, pl.GS, pl.tq, pl.tr,
+                            pl.S, pl.lds, pl.xp, stream);
   // the max-ILP copies: the rotated batch-1 kernel, the 8-wave batch-1 one and the 8-wave
-  // batch 2-16 ones of GF4 and of E2M1 with bf16 x (one workgroup per CU: the GF4 copies'
-  // registers leave room for no second)
+  // batch 2-16 ones of GF4, of E2M1 with bf16 x and of the native FP4 path (one workgroup per
+  // CU: the GF4 copies' registers leave room for no second)
   if constexpr (ilp) {
     if ((mode == kRot1 || mode == kFlat1 ||
          ((mode == kFlat || mode == kSliced) && (FMT == FB_FMT_GF4 || XDT == FB_DT_BF16))) &&
@@ -2016,6 +2027,15 @@ int launch(int fmt, int xdt, int mode, const void* wdev, const void* x, void* y,
     return fmt == FB_FMT_GF4
                ? launch_gemv<FB_FMT_GF4, FB_DT_F16, kRotDAall, kWaves / 2, 4>(wdev, x, y, s, pl, stream)
                : launch_gemv<FB_FMT_E2M1, FB_DT_F16, kRotDAall, kWaves / 2, 4>(wdev, x, y, s, pl, stream);
+  }
+  if ((mode == kSliced || mode == kFlat) && fmt == kFmtMx) {
+    if (mode == kSliced)
+      return xp == 4 ? launch_gemv<kFmtMx, FB_DT_BF16, kSliced, kWaves / 2, 4>(wdev, x, y, s, pl, stream)
+           : xp == 8 ? launch_gemv<kFmtMx, FB_DT_BF16, kSliced, kWaves / 2, 8>(wdev, x, y, s, pl, stream)
+                     : launch_gemv<kFmtMx, FB_DT_BF16, kSliced, kWaves / 2, 16>(wdev, x, y, s, pl, stream);
+    return xp == 4 ? launch_gemv<kFmtMx, FB_DT_BF16, kFlat, kWaves / 2, 4>(wdev, x, y, s, pl, stream)
+         : xp == 8 ? launch_gemv<kFmtMx, FB_DT_BF16, kFlat, kWaves / 2, 8>(wdev, x, y, s, pl, stream)
+                   : launch_gemv<kFmtMx, FB_DT_BF16, kFlat, kWaves / 2, 16>(wdev, x, y, s, pl, stream);
   }
   if (mode == kSliced && fmt == FB_FMT_E2M1) {
     if (xdt != FB_DT_BF16) return FB_ERR_DTYPE;
