@@ -1186,13 +1186,15 @@ __global__ __launch_bounds__(NW * 64) void gemv_kernel(
       // first weight unit arrive later: wait for x first
       if constexpr (rot) __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
       if (rot && s == 0) PH_MARK(kPhXArrived);
-      // E2M1 at batch >= 2, and GF4 in one K-slice on 8 waves with at most 4 units per wave:
-      // the workgroup's x requests all enter the CU's load queue before any weight request
-      // (a wave that starts late would otherwise queue its x behind the others' first units,
-      // and the staging barrier waits for it).  With more units per wave the first unit's
-      // delay costs more than x gains.
+      // E2M1 at batch >= 2 (K-sliced, or in one slice with at most 4 units per wave), and GF4
+      // in one K-slice on 8 waves with at most 4 units per wave: the workgroup's x requests
+      // all enter the CU's load queue before any weight request (a wave that starts late
+      // would otherwise queue its x behind the others' first units, and the staging barrier
+      // waits for it).  With more units per wave in one slice the first unit's delay costs
+      // more than x gains.
       if constexpr (!rot && !flat1 && (FMT == FB_FMT_E2M1 || (NW == 8 && MODE == kFlat)))
-        if (s == s_begin && (FMT == FB_FMT_E2M1 || nu <= 4 * NW)) __builtin_amdgcn_s_barrier();
+        if (s == s_begin && ((FMT == FB_FMT_E2M1 && MODE != kFlat) || nu <= 4 * NW))
+          __builtin_amdgcn_s_barrier();
       issue(s, u0, ring[0]);
       if (s == 0) PH_MARK(kPhU0Issued);
       // The next slice's x (into registers) and first weight unit are requested before the
