@@ -1462,7 +1462,7 @@ size_t plan_lds(const fb_shape_t* s, int tpw, int SPL) {
 //   4096 -> 11008 8.77 -> 8.19; E2M1 8192 -> 28672 20.58 -> 20.28; the rest within 0.1.
 //   Rotated, against 16 waves on the rotated kernel's max-ILP copy: 4096^2 7.27 -> 6.96,
 //   4096 -> 11008 10.58 -> 10.06, 11008 -> 4096 10.35 -> 9.60, 8192^2 14.45 -> 13.95.
-// - Unrotated GF4 (and E2M1 with bf16 x, exact or on the native FP4 path) at batch 2-16 with
+// - Unrotated GF4 (and E2M1, exact or on the native FP4 path) at batch 2-16 with
 //   at most 2 row tiles per CU, whose x fits one K-slice, or two of at most 4 units per wave
 //   each: the same (one 8-wave
 //   workgroup per CU on the max-ILP copy, x preloaded 16 chunks per thread where it needs
@@ -1476,7 +1476,8 @@ size_t plan_lds(const fb_shape_t* s, int tpw, int SPL) {
 //   - E2M1 (bf16 x), another box: 8192^2 B=8 9.04 -> 8.75, B=16 11.92 -> 11.67, 4096^2 B=4
 //     4.89 -> 4.32, 11008 -> 4096 B=8 9.48 -> 9.14 (an earlier build's 8-wave E2M1, with x
 //     past an 8-chunk preload loaded behind the first unit, had been slower: 8192^2 B=8
-//     8.90 / 9.48);
+//     8.90 / 9.48); with fp16 x: 8192^2 B=2 8.44 -> 7.96, B=8 8.89 -> 8.71, B=16 11.84 ->
+//     11.66, 4096^2 B=4 4.81 -> 4.33;
 //   - the native FP4 path (fb_gemv_mx, split included), another box: 8192^2 B=16 14.79 ->
 //     13.99, 11008 -> 4096 B=8 12.30 -> 11.61, 4096^2 B=4 6.81 -> 6.26, B=8 7.33 -> 7.19;
 //     8192^2 B=2 9.82 -> 9.76, B=4 10.13 -> 10.20, B=8 10.96 -> 11.17;
@@ -1491,7 +1492,7 @@ bool make_plan(const fb_shape_t* s, int cus, Plan& pl) {
   const int T = (s->N + 15) / 16;
   const bool one8 = (s->B == 1 && s->fmt != kFmtMx) ||
                     ((s->fmt == FB_FMT_GF4 && s->x_dtype == FB_DT_F16) ||
-                     (s->fmt == FB_FMT_E2M1 && s->x_dtype == FB_DT_BF16) ||
+                     s->fmt == FB_FMT_E2M1 ||
                      (s->fmt == kFmtMx && s->B >= 2)) &&
                      !s->fwht_block && s->B <= 16 && T <= 2 * cus;
   const bool half = one8 || (!s->fwht_block && s->B == 1 && T <= 2 * cus);
@@ -1649,11 +1650,11 @@ int launch_mode(int mode, const void* wdev, const void* x, void* y, const fb_sha
       return fb_ilp::launch(FMT, XDT, mode, wdev, x, y, s, pl.grid, pl.SPL, pl.GS, pl.tq, pl.tr,
                             pl.S, pl.lds, pl.xp, stream);
   // the max-ILP copies: the rotated batch-1 kernel, the 8-wave batch-1 one and the 8-wave
-  // batch 2-16 ones of GF4, of E2M1 with bf16 x and of the native FP4 path (one workgroup per
-  // CU: the GF4 copies' registers leave room for no second)
+  // batch 2-16 ones of GF4, E2M1 and the native FP4 path (one workgroup per CU: the GF4
+  // copies' registers leave room for no second)
   if constexpr (ilp) {
     if ((mode == kRot1 || mode == kFlat1 ||
-         ((mode == kFlat || mode == kSliced) && (FMT == FB_FMT_GF4 || XDT == FB_DT_BF16))) &&
+         mode == kFlat || mode == kSliced) &&
         pl.nw == kWaves / 2)
       return fb_ilp::launch(FMT, XDT,
                             mode != kRot1 ? mode : pl.da_all ? kRotDAall : pl.da ? kRotDA : mode,
@@ -2001,6 +2002,15 @@ void* scratch_ptr(int dev) {
 
 #ifdef FB_GEMV_ILP_TU
 namespace fb_ilp {
+// The 8-wave E2M1 kernels of batches 2-16 at x preload depth xp (4, 8 or 16).
+template <int XDT, int MODE>
+int launch_e2m1_batch8(const void* wdev, const void* x, void* y, const fb_shape_t* s,
+                       const Plan& pl, int xp, hipStream_t stream) {
+  if (xp == 4) return launch_gemv<FB_FMT_E2M1, XDT, MODE, kWaves / 2, 4>(wdev, x, y, s, pl, stream);
+  if (xp == 8) return launch_gemv<FB_FMT_E2M1, XDT, MODE, kWaves / 2, 8>(wdev, x, y, s, pl, stream);
+  return launch_gemv<FB_FMT_E2M1, XDT, MODE, kWaves / 2, 16>(wdev, x, y, s, pl, stream);
+}
+
 int launch(int fmt, int xdt, int mode, const void* wdev, const void* x, void* y,
            const fb_shape_t* s, int grid, int SPL, int GS, int tq, int tr, int S, size_t lds,
            int xp, hipStream_t stream) {
@@ -2041,17 +2051,12 @@ int launch(int fmt, int xdt, int mode, const void* wdev, const void* x, void* y,
          : xp == 8 ? launch_gemv<kFmtMx, FB_DT_BF16, kFlat, kWaves / 2, 8>(wdev, x, y, s, pl, stream)
                    : launch_gemv<kFmtMx, FB_DT_BF16, kFlat, kWaves / 2, 16>(wdev, x, y, s, pl, stream);
   }
-  if (mode == kSliced && fmt == FB_FMT_E2M1) {
-    if (xdt != FB_DT_BF16) return FB_ERR_DTYPE;
-    if (xp == 4) return launch_gemv<FB_FMT_E2M1, FB_DT_BF16, kSliced, kWaves / 2, 4>(wdev, x, y, s, pl, stream);
-    if (xp == 8) return launch_gemv<FB_FMT_E2M1, FB_DT_BF16, kSliced, kWaves / 2, 8>(wdev, x, y, s, pl, stream);
-    return launch_gemv<FB_FMT_E2M1, FB_DT_BF16, kSliced, kWaves / 2, 16>(wdev, x, y, s, pl, stream);
-  }
-  if (mode == kFlat && fmt == FB_FMT_E2M1) {
-    if (xdt != FB_DT_BF16) return FB_ERR_DTYPE;
-    if (xp == 4) return launch_gemv<FB_FMT_E2M1, FB_DT_BF16, kFlat, kWaves / 2, 4>(wdev, x, y, s, pl, stream);
-    if (xp == 8) return launch_gemv<FB_FMT_E2M1, FB_DT_BF16, kFlat, kWaves / 2, 8>(wdev, x, y, s, pl, stream);
-    return launch_gemv<FB_FMT_E2M1, FB_DT_BF16, kFlat, kWaves / 2, 16>(wdev, x, y, s, pl, stream);
+  if ((mode == kSliced || mode == kFlat) && fmt == FB_FMT_E2M1) {
+    if (xdt == FB_DT_BF16)
+      return mode == kSliced ? launch_e2m1_batch8<FB_DT_BF16, kSliced>(wdev, x, y, s, pl, xp, stream)
+                             : launch_e2m1_batch8<FB_DT_BF16, kFlat>(wdev, x, y, s, pl, xp, stream);
+    return mode == kSliced ? launch_e2m1_batch8<FB_DT_F16, kSliced>(wdev, x, y, s, pl, xp, stream)
+                           : launch_e2m1_batch8<FB_DT_F16, kFlat>(wdev, x, y, s, pl, xp, stream);
   }
   if (mode == kSliced) {
     if (fmt != FB_FMT_GF4 || xdt != FB_DT_F16) return FB_ERR_DTYPE;
