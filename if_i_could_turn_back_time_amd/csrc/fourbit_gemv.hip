@@ -1462,9 +1462,9 @@ size_t plan_lds(const fb_shape_t* s, int tpw, int SPL) {
 //   4096 -> 11008 8.77 -> 8.19; E2M1 8192 -> 28672 20.58 -> 20.28; the rest within 0.1.
 //   Rotated, against 16 waves on the rotated kernel's max-ILP copy: 4096^2 7.27 -> 6.96,
 //   4096 -> 11008 10.58 -> 10.06, 11008 -> 4096 10.35 -> 9.60, 8192^2 14.45 -> 13.95.
-// - Unrotated GF4 (and E2M1, exact or on the native FP4 path) at batch 2-16 with
-//   at most 2 row tiles per CU, whose x fits one K-slice, or two of at most 4 units per wave
-//   each: the same (one 8-wave
+// - Unrotated GF4 (and E2M1, exact or on the native FP4 path) at batch 2-16 with at most 2
+//   row tiles per CU (GF4: or at most 64 units per workgroup), whose x fits one K-slice, or
+//   two of at most 2 units per wave each: the same (one 8-wave
 //   workgroup per CU on the max-ILP copy, x preloaded 16 chunks per thread where it needs
 //   them).  Measured against 16 waves, same box, median us (bitwise-equal outputs):
 //   - GF4, one slice: 8192^2 B=2 12.71 -> 11.61, B=4 12.92 -> 11.85, B=8 13.63 -> 12.87;
@@ -1481,8 +1481,14 @@ size_t plan_lds(const fb_shape_t* s, int tpw, int SPL) {
 //   - the native FP4 path (fb_gemv_mx, split included), another box: 8192^2 B=16 14.79 ->
 //     13.99, 11008 -> 4096 B=8 12.30 -> 11.61, 4096^2 B=4 6.81 -> 6.26, B=8 7.33 -> 7.19;
 //     8192^2 B=2 9.82 -> 9.76, B=4 10.13 -> 10.20, B=8 10.96 -> 11.17;
-//   - with more row tiles per CU 16 waves were faster (GF4 8192 -> 28672 B=2 30.53 / 30.68,
-//     B=4 30.71 / 31.39).
+//   - GF4 on 3-7 row tiles per CU of short rows (at most 64 units per workgroup):
+//     4096 -> 11008 B=4 10.31 -> 8.79, B=8 10.43 -> 9.20, B=16 12.13 -> 11.53; 4096 -> 28672
+//     B=2 18.07 -> 17.36, B=4 18.23 -> 17.40; 8192 -> 16384 B=4 20.43 -> 19.91; 8192 ->
+//     14336 B=2 18.33 -> 18.02; but two slices of more than 2 units per wave were slower
+//     (4096 -> 28672 B=16 21.99 / 22.62, 8192 -> 14336 B=8 20.75 / 21.17), and so was E2M1
+//     there (4096 -> 28672 B=8 12.39 / 12.67);
+//   - with more units per workgroup 16 waves were faster (GF4 8192 -> 28672, 112 units:
+//     B=2 30.53 / 30.68, B=4 30.71 / 31.39).
 // - The native FP4 path's batch-1 layers with few row tiles per CU (at most 2) and LDS that
 //   fits twice in a CU: two 8-wave workgroups per CU.
 // - Otherwise one 16-wave workgroup per CU (batches of more row tiles per CU, larger x, E2M1
@@ -1494,7 +1500,8 @@ bool make_plan(const fb_shape_t* s, int cus, Plan& pl) {
                     ((s->fmt == FB_FMT_GF4 && s->x_dtype == FB_DT_F16) ||
                      s->fmt == FB_FMT_E2M1 ||
                      (s->fmt == kFmtMx && s->B >= 2)) &&
-                     !s->fwht_block && s->B <= 16 && T <= 2 * cus;
+                     !s->fwht_block && s->B <= 16 &&
+                     (T <= 2 * cus || (s->fmt == FB_FMT_GF4 && (T + cus - 1) / cus * GS <= 64));
   const bool half = one8 || (!s->fwht_block && s->B == 1 && T <= 2 * cus);
   for (int pass = half ? 0 : 1; pass < 2; ++pass) {
     const int nw = pass == 0 ? kWaves / 2 : kWaves;
@@ -1511,7 +1518,7 @@ bool make_plan(const fb_shape_t* s, int cus, Plan& pl) {
       // 8-wave workgroups with one K-slice at batch 1, at most two at batch 2-16
       if (pass == 0 && S > (s->B == 1 ? 1 : 2)) break;
       // two slices only where each wave has few units per slice
-      if (pass == 0 && S == 2 && tpw * SPL > 4 * nw) break;
+      if (pass == 0 && S == 2 && tpw * SPL > 2 * nw) break;
       const size_t lds = plan_lds(s, tpw, SPL);
       if (lds > limit) continue;
       pl.S = S;

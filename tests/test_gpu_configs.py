@@ -98,6 +98,16 @@ def test_config5_small_batch(fmt, K, N, kind, B):
     check_layer(fmt, K, N, B, kind)
 
 
+# Batches 2-16 on the 8-wave plan with several row tiles per workgroup (GF4, short rows: up to
+# 64 units per workgroup), one K-slice and two: 4096 -> 11008 owns 2-3 row tiles per workgroup,
+# 4096 -> 28672 seven.
+@pytest.mark.parametrize("K,N,B", [(4096, 11008, 4), (4096, 11008, 16), (4096, 28672, 2)],
+                         ids=lambda v: str(v))
+def test_gf4_batch_several_tiles_per_8wave_workgroup(K, N, B):
+    say("gf4 8-wave batch", K, N, B)
+    check_layer("gf4", K, N, B, "cfg1")
+
+
 # Config 4: the 70B MLP shapes with the 0.5% heavy tail at 8 sigma (wide Jenks codebooks).
 @pytest.mark.parametrize("K,N,B", [
     (8192, 28672, 1), (8192, 28672, 2), (8192, 28672, 4),

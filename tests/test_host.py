@@ -98,9 +98,10 @@ def test_batch1_plans_over_a_shape_sweep():
 
 def test_small_batch_wave_plans():
     """Batches 2-16 (fb_phase_plan, host-side, 256 CUs): unrotated GF4 and E2M1 layers of at
-    most 2 row tiles per CU whose x fits one K-slice, or two of at most 4 units per wave
-    each, run one 8-wave workgroup per CU; layers of more row tiles per CU, rotated layers
-    and x that needs more or larger K-slices keep 16-wave workgroups."""
+    most 2 row tiles per CU (GF4: or at most 64 units per workgroup) whose x fits one
+    K-slice, or two of at most 2 units per wave each, run one 8-wave workgroup per CU;
+    layers of more units, rotated layers and x that needs more or larger K-slices keep
+    16-wave workgroups."""
     T_lib = ctypes.CDLL(str(Path(C.__file__).resolve().parent / "libfourbit_trace.so"))
     ip = ctypes.POINTER(ctypes.c_int)
     T_lib.fb_phase_plan.argtypes = [ctypes.POINTER(C.FbShape), ip, ip, ip, ip, ip, ip]
@@ -117,7 +118,12 @@ def test_small_batch_wave_plans():
         assert plan(C.FMT_GF4, K, N, B) == (8, 1), (K, N, B)
         assert plan(C.FMT_E2M1, K, N, B) == (8, 1), (K, N, B)
         assert plan(C.FMT_E2M1, K, N, B, xdt=C.DT_F16) == (8, 1), (K, N, B)
-    assert plan(C.FMT_GF4, 8192, 28672, 2)[0] == 16  # 7 row tiles per CU
+    assert plan(C.FMT_GF4, 8192, 28672, 2)[0] == 16  # 7 row tiles of 16 spans: 112 units
+    assert plan(C.FMT_GF4, 4096, 11008, 4) == (8, 1)  # 3 row tiles of 8 spans: 24 units
+    assert plan(C.FMT_GF4, 4096, 28672, 4) == (8, 1)  # 56 units
+    assert plan(C.FMT_GF4, 4096, 11008, 16) == (8, 2)  # 12 units per slice
+    assert plan(C.FMT_GF4, 4096, 28672, 16)[0] == 16  # 28 units per slice
+    assert plan(C.FMT_E2M1, 4096, 11008, 4)[0] == 16  # E2M1: at most 2 row tiles per CU
     assert plan(C.FMT_GF4, 8192, 8192, 16) == (8, 2)  # batch 16: two K-slices
     assert plan(C.FMT_GF4, 11008, 4096, 8) == (8, 2)  # two K-slices
     assert plan(C.FMT_E2M1, 8192, 8192, 16) == (8, 2)
