@@ -58,10 +58,10 @@ def packed(fmt, K, N, kind):
     return _CACHE[key]
 
 
-def check_layer(fmt, K, N, B, kind):
+def check_layer(fmt, K, N, B, kind, xdt=None):
     pw, W, rows, host = packed(fmt, K, N, kind)
     g = torch.Generator().manual_seed(1000 + B)
-    x = WL.synth_x(kind, B, K, g).to(WL.x_dtype(fmt))
+    x = WL.synth_x(kind, B, K, g).to(xdt or WL.x_dtype(fmt))
     xd = x.to(DEV)
     y = pw.gemv(xd, out_dtype=torch.float32)
     y16 = pw.gemv(xd, out_dtype=x.dtype)
@@ -106,6 +106,13 @@ def test_config5_small_batch(fmt, K, N, kind, B):
 def test_gf4_batch_several_tiles_per_8wave_workgroup(K, N, B):
     say("gf4 8-wave batch", K, N, B)
     check_layer("gf4", K, N, B, "cfg1")
+
+
+# E2M1 with fp16 activations on the 8-wave batch plan, one K-slice and two.
+@pytest.mark.parametrize("B", [8, 16])
+def test_e2m1_fp16_x_batch_8wave(B):
+    say("e2m1 fp16 x 8-wave batch", B)
+    check_layer("e2m1", 8192, 8192, B, "cfg2", xdt=torch.float16)
 
 
 # Config 4: the 70B MLP shapes with the 0.5% heavy tail at 8 sigma (wide Jenks codebooks).
