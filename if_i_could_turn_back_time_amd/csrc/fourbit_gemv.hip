@@ -1599,8 +1599,12 @@ int splitk_parts(const fb_shape_t* s, int cus, Plan* out) {
     out->GS = GS;
     out->tq = T / gx;
     out->tr = T % gx;
-    out->nw = kWaves;
-    out->xp = (s->B * SPL + kWaves - 1) / kWaves <= 4 ? 4 : 8;
+    // 8-wave workgroups on the max-ILP copy (each owns a few row tiles of one part); measured
+    // against 16 waves, same box, median us: E2M1 11008 -> 4096 B=16 10.27 -> 9.94 and 10.32
+    // -> 10.06, with fp16 x 10.28 -> 9.88; GF4 13.89 / 13.84, 13.80 / 13.78 (bitwise equal)
+    out->nw = s->fmt == kFmtMx ? kWaves : kWaves / 2;
+    const int chunks = (s->B * SPL + out->nw - 1) / out->nw;
+    out->xp = chunks <= 4 ? 4 : chunks <= 8 ? 8 : 16;
     out->lds = lds;
     out->P = P;
   }
@@ -1668,6 +1672,10 @@ int launch_mode(int mode, const void* wdev, const void* x, void* y, const fb_sha
                             wdev, x, y, s, pl.grid, pl.SPL, pl.GS, pl.tq, pl.tr, pl.S, pl.lds,
                             pl.xp, stream);
   }
+  if constexpr (ilp)
+    if (mode == kSplitK && pl.nw == kWaves / 2)
+      return fb_ilp::launch(FMT, XDT, kSplitK, wdev, x, y, s, pl.grid, pl.SPL, pl.GS, pl.tq, pl.tr,
+                            pl.S, pl.lds, pl.xp, stream);
   if (mode == kSplitK)
     return deep ? launch_gemv<FMT, XDT, kSplitK, kWaves, 8>(wdev, x, y, s, pl, stream)
                 : launch_gemv<FMT, XDT, kSplitK, kWaves, 4>(wdev, x, y, s, pl, stream);
@@ -2048,6 +2056,16 @@ int launch(int fmt, int xdt, int mode, const void* wdev, const void* x, void* y,
     return fmt == FB_FMT_GF4
                ? launch_gemv<FB_FMT_GF4, FB_DT_F16, kRotDAall, kWaves / 2, 4>(wdev, x, y, s, pl, stream)
                : launch_gemv<FB_FMT_E2M1, FB_DT_F16, kRotDAall, kWaves / 2, 4>(wdev, x, y, s, pl, stream);
+  }
+  if (mode == kSplitK) {
+    pl.P = S;
+    if (fmt == FB_FMT_GF4)
+      return xp == 4 ? launch_gemv<FB_FMT_GF4, FB_DT_F16, kSplitK, kWaves / 2, 4>(wdev, x, y, s, pl, stream)
+           : xp == 8 ? launch_gemv<FB_FMT_GF4, FB_DT_F16, kSplitK, kWaves / 2, 8>(wdev, x, y, s, pl, stream)
+                     : launch_gemv<FB_FMT_GF4, FB_DT_F16, kSplitK, kWaves / 2, 16>(wdev, x, y, s, pl, stream);
+    if (xdt == FB_DT_BF16)
+      return launch_e2m1_batch8<FB_DT_BF16, kSplitK>(wdev, x, y, s, pl, xp, stream);
+    return launch_e2m1_batch8<FB_DT_F16, kSplitK>(wdev, x, y, s, pl, xp, stream);
   }
   if ((mode == kSliced || mode == kFlat) && fmt == kFmtMx) {
     if (mode == kSliced)
