@@ -132,6 +132,35 @@ def test_small_batch_wave_plans():
     assert plan(C.FMT_GF4, 4096, 4096, 2, fb=4096)[0] == 16  # rotated in the kernel
 
 
+def test_batch_plans_over_a_shape_sweep():
+    """Every valid batch 2-16 shape gets a plan (fb_phase_plan, host-side, 256 CUs): the row
+    tiles are split evenly over the grid, 8-wave workgroups take at most two K-slices and no
+    split-K parts, and split-K plans (K >= 10240 only) run 2, 4 or 8 parts."""
+    T_lib = ctypes.CDLL(str(Path(C.__file__).resolve().parent / "libfourbit_trace.so"))
+    ip = ctypes.POINTER(ctypes.c_int)
+    T_lib.fb_phase_plan.argtypes = [ctypes.POINTER(C.FbShape), ip, ip, ip, ip, ip, ip]
+    seen = set()
+    for fmt, xdt in ((C.FMT_GF4, C.DT_F16), (C.FMT_E2M1, C.DT_BF16), (C.FMT_E2M1, C.DT_F16)):
+        for B in (2, 3, 4, 8, 16):
+            for K in (128, 512, 4096, 8192, 11008, 28672):
+                for N in (1, 64, 4096, 11008, 28672):
+                    s = C.make_shape(N, K, B, fmt, 0, xdt, C.DT_F16)
+                    v = [ctypes.c_int() for _ in range(6)]
+                    assert T_lib.fb_phase_plan(ctypes.byref(s), *[ctypes.byref(a) for a in v]) == 0
+                    grid, waves, slices, tq, tr, parts = (a.value for a in v)
+                    T = (N + 15) // 16
+                    assert waves in (8, 16) and slices >= 1, (fmt, B, K, N)
+                    assert grid * tq + tr == T and 0 <= tr < grid, (fmt, B, K, N)
+                    if waves == 8 and not parts:
+                        assert slices <= 2, (fmt, B, K, N)
+                    if parts:
+                        assert K >= 10240 and parts in (2, 4, 8), (fmt, B, K, N)
+                    seen.add((waves, slices > 1, bool(parts)))
+    # every kind of plan occurs in the sweep
+    assert {(8, False, False), (8, True, False), (16, False, False), (16, True, False)} <= seen
+    assert any(p for _, _, p in seen)
+
+
 @pytest.mark.parametrize("kw,err", [
     (dict(K=100), -2), (dict(K=0), -2), (dict(N=0), -2), (dict(B=0), -2),
     (dict(group=64), -3), (dict(fmt=7), -4), (dict(x_dtype=C.DT_BF16), -5),
