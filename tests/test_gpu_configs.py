@@ -101,7 +101,8 @@ def test_config5_small_batch(fmt, K, N, kind, B):
 # Batches 2-16 on the 8-wave plan with several row tiles per workgroup (GF4, short rows: up to
 # 64 units per workgroup), one K-slice and two: 4096 -> 11008 owns 2-3 row tiles per workgroup,
 # 4096 -> 28672 seven.
-@pytest.mark.parametrize("K,N,B", [(4096, 11008, 4), (4096, 11008, 16), (4096, 28672, 2)],
+@pytest.mark.parametrize("K,N,B", [(4096, 11008, 4), (4096, 11008, 16), (4096, 28672, 2),
+                                   (3968, 11003, 3)],  # ragged rows, K not a multiple of 512
                          ids=lambda v: str(v))
 def test_gf4_batch_several_tiles_per_8wave_workgroup(K, N, B):
     say("gf4 8-wave batch", K, N, B)
