@@ -17,7 +17,8 @@
 // unit's partial sums go to a slot of their own, and the wave that finishes a row tile's
 // last unit adds each of its outputs' slots in span order, so results do not depend on
 // which wave did what.
-// When x does not fit LDS the K range is cut into S slices staged one after the other.
+// When x does not fit LDS the K range is cut into S slices staged one after the other, or
+// (kSpanX, batches of 2-16) each wave stages the x of its own spans, one at a time.
 // No workgroup talks to another: no global atomics or device-scope fences.
 #include <hip/hip_runtime.h>
 
@@ -922,8 +923,11 @@ constexpr int zero_bytes(int fmt) { return fmt == kFmtMx ? 1088 : 256; }
 // kRotDAall = kRotDA where a workgroup owns no more units than waves: the rotating waves also
 // decode their one unit before the staging barrier (with more units that would hold the
 // barrier back).
+// kSpanX = batch 2-16 without K-slices: wave w owns spans w, w + NW, ... of every row tile of
+// the workgroup and stages each span's x in an LDS region of its own (XP is then the most row
+// tiles a workgroup owns, whose sums the wave keeps in registers).
 enum { kFlat = 0, kSliced = 1, kRotated = 2, kRot1 = 3, kFlat1 = 4, kSplitK = 5, kRotDA = 6,
-       kRotDAall = 7 };
+       kRotDAall = 7, kSpanX = 8 };
 // NW: waves per workgroup.  16 (one workgroup per CU) in general; 8 (two per CU) for
 // layers with few row tiles per CU, where twice the workgroups, each with half the waves,
 // finish sooner.
@@ -1068,6 +1072,107 @@ __global__ __launch_bounds__(NW * 64) void gemv_kernel(
   // x through a buffer resource (out-of-range offsets read zeros)
   const rsrc_t xrs = __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(x), (short)0, B * K * 2,
                                                        kRsrcWord3);
+  if constexpr (MODE == kSpanX) {
+    // Each wave owns the spans wave, wave + NW, ... of every row tile of the workgroup and
+    // stages the x of one span at a time (B rows of 512 values, RS bytes per row) in an LDS
+    // region of its own, so no wave waits for another before the epilogue.  Unit i of the
+    // wave is span wave + (i / nt) NW of tile i % nt; the wave adds its units' partial sums
+    // per tile in registers, in its span order, and after the last unit writes them to the
+    // (tile, wave) slots (over the x regions); each output then adds its tile's NW slots in
+    // wave order.
+    constexpr int kTMax = XP;  // row tiles per workgroup, at most (the host checks)
+    const int nt = t1 - t0;
+    uint8_t* xw = xst + wave * B * RS;
+    f32x4* wsl = reinterpret_cast<f32x4*>(xst);
+    const uint8_t* xlw = col < B ? xw + col * RS + q * kSliceBytes : zeros;
+    const int nsw = wave < GS ? (GS - 1 - wave) / NW + 1 : 0;  // spans of this wave
+    const int nuw = nsw * nt;
+    u32x4 xv[16];
+    auto x_load = [&](int sp0) {
+      const int k = sp0 * 512 + lane * 8;
+#pragma unroll
+      for (int b = 0; b < 16; ++b)
+        if (b < B) {
+          const unsigned off = k < K ? (unsigned)(b * K + k) * 2u : kXOutOfRange;
+          xv[b] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(xrs, off, 0, 0));
+        }
+    };
+    auto x_put = [&]() {
+      uint8_t* d = xw + (lane >> 4) * kSliceBytes + (lane & 15) * 16;
+#pragma unroll
+      for (int b = 0; b < 16; ++b)
+        if (b < B) *reinterpret_cast<u32x4*>(d + b * RS) = xv[b];
+    };
+    int is = wave, it = 0, ni = 0;  // the next unit to request
+    auto w_issue = [&](Rec<FMT>& r) {
+      const bool real = ni < nuw;
+      const rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(wbase), (short)0,
+                                                          real ? 0x7fffffff : 0, kRsrcWord3);
+      load_rec<FMT>(rs, real ? (unsigned)((it * GS + is) * BB) : 0u, lane, r);
+      ++ni;
+      if (++it == nt) {
+        it = 0;
+        is += NW;
+      }
+    };
+    if (threadIdx.x < zero_bytes(FMT) / 16)
+      reinterpret_cast<u32x4*>(zeros)[threadIdx.x] = u32x4{0u, 0u, 0u, 0u};
+    if (nsw) x_load(wave);
+    PH_MARK(kPhXIssued);
+    Rec<FMT> rg[2];
+    w_issue(rg[0]);
+    PH_MARK(kPhU0Issued);
+    __syncthreads();  // the zero block
+    f32x4 acc[kTMax];
+    int sc = wave, lt = 0;
+    auto step = [&](const Rec<FMT>& cur, Rec<FMT>& nxt) {
+      if (lt == 0) {
+        x_put();
+        if (sc + NW < GS) x_load(sc + NW);  // in flight during this span's units
+      }
+      w_issue(nxt);
+      __builtin_amdgcn_sched_barrier(0);  // keep the prefetch ahead of the compute
+      const f32x4 p = unit_partial<FMT, XDT>(cur, xlw);
+      const bool first = sc == wave;
+#pragma unroll
+      for (int t = 0; t < kTMax; ++t)  // lt is wave-uniform: a scalar branch per tile
+        if (t == lt) acc[t] = first ? p : acc[t] + p;
+      if (++lt == nt) {
+        lt = 0;
+        sc += NW;
+      }
+    };
+    for (int i = 0; i < nuw; i += 2) {
+      step(rg[0], rg[1]);
+      if (i + 1 >= nuw) break;
+      step(rg[1], rg[0]);
+    }
+    PH_MARK(kPhLoopEnd);
+    __syncthreads();  // every wave is done with its x: the slots may take the x regions
+    if (nsw && col < B) {
+#pragma unroll
+      for (int t = 0; t < kTMax; ++t)
+        if (t < nt) wsl[((size_t)(t * NW + wave) * 4 + q) * B + col] = acc[t];
+    }
+    __syncthreads();  // every slot complete
+    PH_MARK(kPhFinalBar);
+    const int nws = min(NW, GS);
+    for (int e = threadIdx.x; e < nt * 256; e += NT) {
+      const int c = e & 15;
+      if (c >= B) continue;
+      const int r = (e >> 4) & 15;
+      const int lt2 = e >> 8;
+      const int row = (t0 + lt2) * 16 + r;
+      const f32x4* sl = wsl + ((size_t)lt2 * NW * 4 + (r >> 2)) * B + c;
+      float sum = 0.0f;
+      for (int j = 0; j < nws; ++j) sum += sl[(size_t)j * 4 * B][r & 3];
+      if (row < N) store_y(y, (int64_t)c * N + row, sum, ydt);
+    }
+    PH_MARK(kPhEnd);
+    PH_PUT(kPhSlices, 1ull);
+    PH_FLUSH(NW);
+    return;
+  }
   // MX path: the split's block scales, 8 bytes per (batch row, 128-value group), staged into
   // the pad of each staged group (zeros past K).  Entry i of a slice is row i / nsl, group
   // k0 / 128 + i % nsl.  They follow the codes in the split's layout, so no argument is
@@ -1434,6 +1539,7 @@ struct Plan {
   int P = 0;     // kSplitK: K-parts run side by side (grid grid x P); 0: slices in turn
   bool da = false;      // kRotDA: batch-1 rotation with decode-ahead waves
   bool da_all = false;  // kRotDAall: the same, every wave decoding ahead (one unit per wave)
+  bool spanx = false;   // kSpanX: each wave stages the x of its own spans
 };
 
 
@@ -1493,7 +1599,7 @@ size_t plan_lds(const fb_shape_t* s, int tpw, int SPL) {
 //   fits twice in a CU: two 8-wave workgroups per CU.
 // - Otherwise one 16-wave workgroup per CU (batches of more row tiles per CU, larger x, E2M1
 //   with fp16 x, rotated batches).
-bool make_plan(const fb_shape_t* s, int cus, Plan& pl) {
+bool make_plan_staged(const fb_shape_t* s, int cus, Plan& pl) {
   const int GS = (s->K / 128 + 3) / 4;
   const int T = (s->N + 15) / 16;
   const bool one8 = (s->B == 1 && s->fmt != kFmtMx) ||
@@ -1551,6 +1657,65 @@ bool make_plan(const fb_shape_t* s, int cus, Plan& pl) {
   return false;
 }
 
+// kSpanX (batch >= 2, unrotated): each of 8 waves stages the x of its own spans, one span
+// (B x 512 values) at a time, in an LDS region of its own, instead of the workgroup staging
+// x K-slice by K-slice behind barriers; the wave adds its units' sums per row tile in
+// registers (at most 8 tiles).  Taken where the staged plan needs two or more K-slices, each
+// wave owns at least two units (GF4: at least two spans), and the workgroup at most 4 row
+// tiles (8 at batch 16); over split-K where a wave owns 4 or more spans and the row tiles
+// fill every CU (split-K's parts multiply the workgroups of fewer tiles).  Measured against
+// the plans before it on 46 shapes, same box, median us of 9 regions (outputs within fp16
+// rounding of them: another order of the same fp32 sums):
+// - 8192^2 B=12: GF4 16.12 -> 14.26, E2M1 10.94 -> 9.76; B=16: GF4 16.17 -> 15.33, E2M1
+//   11.71 -> 10.46 (another box 14.86 -> 14.10, 11.65 -> 10.25);
+// - 8192 -> 28672 B=16: GF4 39.36 -> 35.81, E2M1 25.80 -> 24.62 (another box 34.80 -> 34.39,
+//   24.23 / 24.32);
+// - 28672 -> 8192: B=3 E2M1 22.70 -> 20.94 (GF4 33.24 / 33.46), B=8 GF4 38.37 -> 36.23,
+//   E2M1 25.55 -> 23.49, B=16 GF4 43.77 -> 40.62, E2M1 35.37 -> 29.13 (over split-K);
+// - 16384 -> 4096 B=16: GF4 20.69 -> 17.54, E2M1 16.89 -> 13.12 (over split-K; at B=12
+//   16.26 / 16.49 and 11.38 / 11.83); 8192 -> 16384 B=16: GF4 26.55 -> 23.38, E2M1 18.81 ->
+//   16.01; 11008 -> 4096 B=12: GF4 13.58 -> 12.45, E2M1 10.57 -> 9.36; E2M1 4096 -> 11008
+//   B=16 9.63 -> 8.49;
+// - GF4 with one span per wave was mixed (4096 -> 11008 B=16 12.05 / 12.75 and 11.53 /
+//   10.76, 4096 -> 28672 B=16 23.55 / 24.08), so GF4 takes it from two spans per wave; the
+//   one-slice plans stay (8192^2 B=8: GF4 11.76 / 12.71, E2M1 8.70 / 8.98), and so do 7 row
+//   tiles below batch 16 (8192 -> 28672 B=12: GF4 33.05 / 33.37, E2M1 23.13 / 23.72) and
+//   split-K over fewer spans per wave (11008 -> 4096 B=16: GF4 11.85 / 12.67, E2M1 9.92 /
+//   10.19).
+bool spanx_plan(const fb_shape_t* s, int cus, const Plan& staged, Plan& pl) {
+  if (s->B < 2 || s->B > 16 || s->fwht_block || s->fmt == kFmtMx || staged.S < 2) return false;
+  const int GS = (s->K / 128 + 3) / 4;
+  const int T = (s->N + 15) / 16;
+  const int grid = std::max(1, std::min(T, cus));
+  const int tpw = (T + grid - 1) / grid;
+  const int nw = kWaves / 2;
+  if (tpw > (s->B == 16 ? 8 : 4) || tpw * ((GS + nw - 1) / nw) < 2) return false;
+  if (s->fmt == FB_FMT_GF4 && GS <= nw) return false;  // one span per wave
+  // the waves' x regions, which the (tile, wave) slots take over after the last unit
+  const size_t lds = 16 + zero_bytes(s->fmt) +
+                     std::max((size_t)nw * s->B * x_row_stride(4), (size_t)tpw * nw * s->B * 64);
+  if (lds > (size_t)kLdsLimit) return false;
+  pl = Plan();
+  pl.S = 1;
+  pl.SPL = GS;
+  pl.grid = grid;
+  pl.GS = GS;
+  pl.tq = T / grid;
+  pl.tr = T % grid;
+  pl.nw = nw;
+  pl.xp = tpw <= 2 ? 2 : tpw <= 4 ? 4 : 8;  // the kernel's register count of row tiles
+  pl.lds = lds;
+  pl.spanx = true;
+  return true;
+}
+
+bool make_plan(const fb_shape_t* s, int cus, Plan& pl) {
+  if (!make_plan_staged(s, cus, pl)) return false;
+  Plan sx;
+  if (spanx_plan(s, cus, pl, sx)) pl = sx;
+  return true;
+}
+
 // kSplitK (batch >= 2, unrotated): the K-slices of the sliced layout run side by side, P
 // workgroups per row range, each staging only its own part of x, with no slice barrier.  The
 // parts' fp32 sums (P * B * N * 4 bytes) go to the caller's workspace and splitk_sum adds
@@ -1580,9 +1745,10 @@ int splitk_parts(const fb_shape_t* s, int cus, Plan* out) {
   int P = forced;
   if (!P) {
     if (s->K < 10240) return 0;
-    Plan std_pl;
-    if (!make_plan(s, cus, std_pl) || std_pl.S < 3) return 0;
+    Plan std_pl, sx;
+    if (!make_plan_staged(s, cus, std_pl) || std_pl.S < 3) return 0;
     if ((T + std_pl.grid - 1) / std_pl.grid > 2) return 0;
+    if (GS >= 32 && T >= cus && spanx_plan(s, cus, std_pl, sx)) return 0;  // kSpanX is faster
     P = 2;
     while (P < std_pl.S) P *= 2;
   }
@@ -1638,7 +1804,8 @@ int launch_gemv(const void* wdev, const void* x, void* y, const fb_shape_t* s, c
   }
   hipLaunchKernelGGL(kern, dim3(pl.grid, pl.P ? pl.P : 1), dim3(NW * 64), pl.lds, stream,
                      static_cast<const uint8_t*>(wdev), x, s->K, s->B, pl.SPL, pl.GS, pl.tq,
-                     pl.tr, div_magic(pl.SPL), pl.S, s->fwht_block, x_row_stride(pl.SPL * 4),
+                     pl.tr, div_magic(pl.SPL), pl.S, s->fwht_block,
+                     x_row_stride(MODE == kSpanX ? 4 : pl.SPL * 4),
                      fwht_scale(s->fwht_block), y, s->N, s->y_dtype
                      PH_KARG((size_t)pl.grid * (pl.P ? pl.P : 1) * NW * 64));
   return hipGetLastError() == hipSuccess ? FB_OK : FB_ERR_HIP;
@@ -1672,6 +1839,10 @@ int launch_mode(int mode, const void* wdev, const void* x, void* y, const fb_sha
                             wdev, x, y, s, pl.grid, pl.SPL, pl.GS, pl.tq, pl.tr, pl.S, pl.lds,
                             pl.xp, stream);
   }
+  if constexpr (ilp)
+    if (mode == kSpanX)
+      return fb_ilp::launch(FMT, XDT, kSpanX, wdev, x, y, s, pl.grid, pl.SPL, pl.GS, pl.tq, pl.tr,
+                            pl.S, pl.lds, pl.xp, stream);
   if constexpr (ilp)
     if (mode == kSplitK && pl.nw == kWaves / 2)
       return fb_ilp::launch(FMT, XDT, kSplitK, wdev, x, y, s, pl.grid, pl.SPL, pl.GS, pl.tq, pl.tr,
@@ -1716,6 +1887,7 @@ int launch_mode(int mode, const void* wdev, const void* x, void* y, const fb_sha
 int launch_plan(const void* wdev, const void* x, void* y, const fb_shape_t* s, const Plan& pl,
                 hipStream_t hs) {
   const int mode = s->fwht_block ? (s->B == 1 && pl.S == 1 ? kRot1 : kRotated)
+                   : pl.spanx     ? kSpanX
                    : pl.P         ? kSplitK
                    : pl.S > 1     ? kSliced
                    : s->B == 1    ? kFlat1
@@ -2057,6 +2229,21 @@ int launch(int fmt, int xdt, int mode, const void* wdev, const void* x, void* y,
                ? launch_gemv<FB_FMT_GF4, FB_DT_F16, kRotDAall, kWaves / 2, 4>(wdev, x, y, s, pl, stream)
                : launch_gemv<FB_FMT_E2M1, FB_DT_F16, kRotDAall, kWaves / 2, 4>(wdev, x, y, s, pl, stream);
   }
+  if (mode == kSpanX) {
+    if (fmt == FB_FMT_GF4) {
+      if (xdt != FB_DT_F16) return FB_ERR_DTYPE;
+      return xp == 2 ? launch_gemv<FB_FMT_GF4, FB_DT_F16, kSpanX, kWaves / 2, 2>(wdev, x, y, s, pl, stream)
+           : xp == 4 ? launch_gemv<FB_FMT_GF4, FB_DT_F16, kSpanX, kWaves / 2, 4>(wdev, x, y, s, pl, stream)
+                     : launch_gemv<FB_FMT_GF4, FB_DT_F16, kSpanX, kWaves / 2, 8>(wdev, x, y, s, pl, stream);
+    }
+    if (xdt == FB_DT_BF16)
+      return xp == 2 ? launch_gemv<FB_FMT_E2M1, FB_DT_BF16, kSpanX, kWaves / 2, 2>(wdev, x, y, s, pl, stream)
+           : xp == 4 ? launch_gemv<FB_FMT_E2M1, FB_DT_BF16, kSpanX, kWaves / 2, 4>(wdev, x, y, s, pl, stream)
+                     : launch_gemv<FB_FMT_E2M1, FB_DT_BF16, kSpanX, kWaves / 2, 8>(wdev, x, y, s, pl, stream);
+    return xp == 2 ? launch_gemv<FB_FMT_E2M1, FB_DT_F16, kSpanX, kWaves / 2, 2>(wdev, x, y, s, pl, stream)
+         : xp == 4 ? launch_gemv<FB_FMT_E2M1, FB_DT_F16, kSpanX, kWaves / 2, 4>(wdev, x, y, s, pl, stream)
+                   : launch_gemv<FB_FMT_E2M1, FB_DT_F16, kSpanX, kWaves / 2, 8>(wdev, x, y, s, pl, stream);
+  }
   if (mode == kSplitK) {
     pl.P = S;
     if (fmt == FB_FMT_GF4)
@@ -2252,7 +2439,7 @@ int fb_phase_plan(const fb_shape_t* s, int* grid, int* waves, int* slices, int* 
   if (!splitk_parts(s, device_cus(), &pl) && !make_plan(s, device_cus(), pl)) return FB_ERR_LDS;
   *grid = pl.grid;
   *waves = pl.nw;
-  *slices = pl.S;
+  *slices = pl.spanx ? 0 : pl.S;  // 0: kSpanX (each wave stages its own spans)
   *tq = pl.tq;
   *tr = pl.tr;
   *parts = pl.P;

@@ -109,7 +109,38 @@ def test_gf4_batch_several_tiles_per_8wave_workgroup(K, N, B):
     check_layer("gf4", K, N, B, "cfg1")
 
 
-# E2M1 with fp16 activations on the 8-wave batch plan, one K-slice and two.
+def staged_slices(fmt, K, N, B, xdt):
+    """Slices of the plan fb_gemv takes for this shape (fb_phase_plan of the diagnostic
+    library, built beside the product one); 0: each wave stages the x of its own spans."""
+    import ctypes
+    from pathlib import Path
+    T_lib = ctypes.CDLL(str(Path(C.__file__).resolve().parent / "libfourbit_trace.so"))
+    ip = ctypes.POINTER(ctypes.c_int)
+    T_lib.fb_phase_plan.argtypes = [ctypes.POINTER(C.FbShape), ip, ip, ip, ip, ip, ip]
+    s = C.make_shape(N, K, B, C.FMT_GF4 if fmt == "gf4" else C.FMT_E2M1, 0, xdt, C.DT_F16)
+    v = [ctypes.c_int() for _ in range(6)]
+    assert T_lib.fb_phase_plan(ctypes.byref(s), *[ctypes.byref(a) for a in v]) == 0
+    return v[2].value
+
+
+# Batches whose x the staged plan would cut into K-slices, on the plan where each of the 8
+# waves stages the x of its own spans: several row tiles per workgroup, a K that ends inside
+# a span (11008 = 21.5 spans), ragged rows, one span per wave (E2M1), batches that are not a
+# power of two, fp16 x, and a layer that split-K would otherwise take (16384 -> 4096).
+@pytest.mark.parametrize("fmt,K,N,B,xdt", [
+    ("gf4", 8192, 8192, 12, torch.float16), ("e2m1", 8192, 8192, 12, torch.bfloat16),
+    ("gf4", 11008, 4001, 8, torch.float16), ("e2m1", 11008, 4001, 12, torch.float16),
+    ("e2m1", 4096, 11008, 16, torch.bfloat16), ("gf4", 28672, 8192, 3, torch.float16),
+    ("e2m1", 16384, 4096, 16, torch.bfloat16), ("gf4", 8192, 16384, 16, torch.float16),
+], ids=lambda v: str(v).replace("torch.", ""))
+def test_waves_stage_their_own_spans(fmt, K, N, B, xdt):
+    say("own-span plan", fmt, K, N, B, xdt)
+    assert staged_slices(fmt, K, N, B, C.DT_F16 if xdt == torch.float16 else C.DT_BF16) == 0
+    check_layer(fmt, K, N, B, "cfg1" if fmt == "gf4" else "cfg2", xdt=xdt)
+
+
+# E2M1 with fp16 activations on the 8-wave batch plans: one K-slice at batch 8, each wave
+# staging its own spans at batch 16.
 @pytest.mark.parametrize("B", [8, 16])
 def test_e2m1_fp16_x_batch_8wave(B):
     say("e2m1 fp16 x 8-wave batch", B)

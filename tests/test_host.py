@@ -101,7 +101,9 @@ def test_small_batch_wave_plans():
     most 2 row tiles per CU (GF4: or at most 64 units per workgroup) whose x fits one
     K-slice, or two of at most 2 units per wave each, run one 8-wave workgroup per CU;
     layers of more units, rotated layers and x that needs more or larger K-slices keep
-    16-wave workgroups."""
+    16-wave workgroups.  Where the staged plan needs K-slices, each wave owns two or more
+    units (GF4: spans) and a workgroup at most 4 row tiles (8 at batch 16), the 8 waves stage
+    the x of their own spans instead (kSpanX, reported as 0 slices)."""
     T_lib = ctypes.CDLL(str(Path(C.__file__).resolve().parent / "libfourbit_trace.so"))
     ip = ctypes.POINTER(ctypes.c_int)
     T_lib.fb_phase_plan.argtypes = [ctypes.POINTER(C.FbShape), ip, ip, ip, ip, ip, ip]
@@ -121,21 +123,31 @@ def test_small_batch_wave_plans():
     assert plan(C.FMT_GF4, 8192, 28672, 2)[0] == 16  # 7 row tiles of 16 spans: 112 units
     assert plan(C.FMT_GF4, 4096, 11008, 4) == (8, 1)  # 3 row tiles of 8 spans: 24 units
     assert plan(C.FMT_GF4, 4096, 28672, 4) == (8, 1)  # 56 units
-    assert plan(C.FMT_GF4, 4096, 11008, 16) == (8, 2)  # 12 units per slice
     assert plan(C.FMT_GF4, 4096, 28672, 16)[0] == 16  # 28 units per slice
     assert plan(C.FMT_E2M1, 4096, 11008, 4)[0] == 16  # E2M1: at most 2 row tiles per CU
-    assert plan(C.FMT_GF4, 8192, 8192, 16) == (8, 2)  # batch 16: two K-slices
-    assert plan(C.FMT_GF4, 11008, 4096, 8) == (8, 2)  # two K-slices
-    assert plan(C.FMT_E2M1, 8192, 8192, 16) == (8, 2)
-    assert plan(C.FMT_GF4, 28672, 8192, 4) == (16, 2)  # 7 units per wave in a slice
-    assert plan(C.FMT_GF4, 28672, 8192, 8)[0] == 16  # x needs four K-slices
+    # x in K-slices: each wave stages its own spans instead
+    assert plan(C.FMT_GF4, 8192, 8192, 16) == (8, 0)
+    assert plan(C.FMT_E2M1, 8192, 8192, 16) == (8, 0)
+    assert plan(C.FMT_GF4, 11008, 4096, 8) == (8, 0)
+    assert plan(C.FMT_GF4, 28672, 8192, 4) == (8, 0)
+    assert plan(C.FMT_GF4, 28672, 8192, 8) == (8, 0)
+    assert plan(C.FMT_GF4, 8192, 28672, 16) == (8, 0)  # 7 row tiles at batch 16
+    assert plan(C.FMT_E2M1, 4096, 11008, 16) == (8, 0)  # E2M1: one span per wave
+    # ... but not with 7 row tiles below batch 16, GF4 with one span per wave, one unit per
+    # wave, or where split-K (over fewer than 4 spans per wave) takes the layer
+    assert plan(C.FMT_GF4, 8192, 28672, 8)[1] != 0
+    assert plan(C.FMT_GF4, 4096, 11008, 16) == (8, 2)  # 12 units per slice
+    assert plan(C.FMT_E2M1, 4096, 4096, 16)[1] != 0
+    assert plan(C.FMT_GF4, 11008, 4096, 16)[1] != 0
     assert plan(C.FMT_GF4, 4096, 4096, 2, fb=4096)[0] == 16  # rotated in the kernel
 
 
 def test_batch_plans_over_a_shape_sweep():
     """Every valid batch 2-16 shape gets a plan (fb_phase_plan, host-side, 256 CUs): the row
     tiles are split evenly over the grid, 8-wave workgroups take at most two K-slices and no
-    split-K parts, and split-K plans (K >= 10240 only) run 2, 4 or 8 parts."""
+    split-K parts, split-K plans (K >= 10240 only) run 2, 4 or 8 parts, and plans whose waves
+    stage their own spans (0 slices) have 8 waves and at most 4 row tiles per workgroup (8
+    at batch 16)."""
     T_lib = ctypes.CDLL(str(Path(C.__file__).resolve().parent / "libfourbit_trace.so"))
     ip = ctypes.POINTER(ctypes.c_int)
     T_lib.fb_phase_plan.argtypes = [ctypes.POINTER(C.FbShape), ip, ip, ip, ip, ip, ip]
@@ -149,15 +161,19 @@ def test_batch_plans_over_a_shape_sweep():
                     assert T_lib.fb_phase_plan(ctypes.byref(s), *[ctypes.byref(a) for a in v]) == 0
                     grid, waves, slices, tq, tr, parts = (a.value for a in v)
                     T = (N + 15) // 16
-                    assert waves in (8, 16) and slices >= 1, (fmt, B, K, N)
+                    assert waves in (8, 16) and slices >= 0, (fmt, B, K, N)
                     assert grid * tq + tr == T and 0 <= tr < grid, (fmt, B, K, N)
+                    if slices == 0:
+                        assert waves == 8 and not parts, (fmt, B, K, N)
+                        assert tq + (tr > 0) <= (8 if B == 16 else 4), (fmt, B, K, N)
                     if waves == 8 and not parts:
                         assert slices <= 2, (fmt, B, K, N)
                     if parts:
                         assert K >= 10240 and parts in (2, 4, 8), (fmt, B, K, N)
-                    seen.add((waves, slices > 1, bool(parts)))
+                    seen.add((waves, slices, bool(parts)))
     # every kind of plan occurs in the sweep
-    assert {(8, False, False), (8, True, False), (16, False, False), (16, True, False)} <= seen
+    assert {(8, 0, False), (8, 1, False), (8, 2, False), (16, 1, False)} <= seen
+    assert any(w == 16 and sl > 1 for w, sl, _ in seen)
     assert any(p for _, _, p in seen)
 
 
