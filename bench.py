@@ -496,6 +496,11 @@ def phase_trace(name: str, calls: int, packer: str, parts: int = 0) -> dict:
             [np.corrcoef(np.argsort(np.argsort(wg_end[c])), np.argsort(np.argsort(wg_end[c + 1])))[0, 1]
              for c in range(calls - 1)])), 3) if calls > 1 else None,
         "workgroup_start_us": stats(us(start.min(axis=2) - g0[:, :, 0])),
+        # each phase after the workgroup's first wave start, median by wave index (the SIMDs
+        # issue a workgroup's older waves first)
+        "phase_by_wave_us": {label: [round(float(np.median(us(t[:, :, i, k] - start.min(axis=2))[
+            t[:, :, i, k] != 0])), 3) if (t[:, :, i, k] != 0).any() else None for i in range(nw)]
+            for k, label in PHASES.items() if (t[..., k] != 0).any()},
         "corr_start_end": round(float(np.corrcoef(us(start.min(axis=2) - g0[:, :, 0]).ravel(),
                                                   wg_end.ravel())[0, 1]), 3),
     }

@@ -1128,12 +1128,14 @@ __global__ __launch_bounds__(NW * 64) void gemv_kernel(
     auto step = [&](const Rec<FMT>& cur, Rec<FMT>& nxt) {
       if (lt == 0) {
         x_put();
+        PH_MARK(sc == wave ? kPhStaged : sc == wave + NW ? kPhStaged1 : kPhStaged2);
         if (sc + NW < GS) x_load(sc + NW);  // in flight during this span's units
       }
       w_issue(nxt);
       __builtin_amdgcn_sched_barrier(0);  // keep the prefetch ahead of the compute
       const f32x4 p = unit_partial<FMT, XDT>(cur, xlw);
       const bool first = sc == wave;
+      if (first && lt == 0) PH_MARK(kPhUnit0);
 #pragma unroll
       for (int t = 0; t < kTMax; ++t)  // lt is wave-uniform: a scalar branch per tile
         if (t == lt) acc[t] = first ? p : acc[t] + p;
