@@ -1151,14 +1151,14 @@ __global__ __launch_bounds__(NW * 64) void gemv_kernel(
     }
     PH_MARK(kPhLoopEnd);
     __syncthreads();  // every wave is done with its x: the slots may take the x regions
-    if (nsw && col < B) {
+    if (col < B) {  // a wave without spans (GS < NW) adds zeros
 #pragma unroll
       for (int t = 0; t < kTMax; ++t)
-        if (t < nt) wsl[((size_t)(t * NW + wave) * 4 + q) * B + col] = acc[t];
+        if (t < nt)
+          wsl[((size_t)(t * NW + wave) * 4 + q) * B + col] = nsw ? acc[t] : f32x4{0.f, 0.f, 0.f, 0.f};
     }
     __syncthreads();  // every slot complete
     PH_MARK(kPhFinalBar);
-    const int nws = min(NW, GS);
     for (int e = threadIdx.x; e < nt * 256; e += NT) {
       const int c = e & 15;
       if (c >= B) continue;
@@ -1166,8 +1166,13 @@ __global__ __launch_bounds__(NW * 64) void gemv_kernel(
       const int lt2 = e >> 8;
       const int row = (t0 + lt2) * 16 + r;
       const f32x4* sl = wsl + ((size_t)lt2 * NW * 4 + (r >> 2)) * B + c;
+      // a fixed count, so the NW reads are issued together before the adds
+      float v[NW];
+#pragma unroll
+      for (int j = 0; j < NW; ++j) v[j] = sl[(size_t)j * 4 * B][r & 3];
       float sum = 0.0f;
-      for (int j = 0; j < nws; ++j) sum += sl[(size_t)j * 4 * B][r & 3];
+#pragma unroll
+      for (int j = 0; j < NW; ++j) sum += v[j];
       if (row < N) store_y(y, (int64_t)c * N + row, sum, ydt);
     }
     PH_MARK(kPhEnd);
