@@ -1669,7 +1669,7 @@ bool make_plan_staged(const fb_shape_t* s, int cus, Plan& pl) {
 // x K-slice by K-slice behind barriers; the wave adds its units' sums per row tile in
 // registers (at most 8 tiles).  Taken where the staged plan needs two or more K-slices, each
 // wave owns at least two units (GF4: at least two spans), and the workgroup at most 4 row
-// tiles (8 at batch 16); over split-K where a wave owns 4 or more spans and the row tiles
+// tiles (8 at batch 8-16); over split-K where a wave owns 4 or more spans and the row tiles
 // fill every CU (split-K's parts multiply the workgroups of fewer tiles).  Measured against
 // the plans before it on 46 shapes, same box, median us of 9 regions (outputs within fp16
 // rounding of them: another order of the same fp32 sums):
@@ -1685,10 +1685,13 @@ bool make_plan_staged(const fb_shape_t* s, int cus, Plan& pl) {
 //   B=16 9.63 -> 8.49;
 // - GF4 with one span per wave was mixed (4096 -> 11008 B=16 12.05 / 12.75 and 11.53 /
 //   10.76, 4096 -> 28672 B=16 23.55 / 24.08), so GF4 takes it from two spans per wave; the
-//   one-slice plans stay (8192^2 B=8: GF4 11.76 / 12.71, E2M1 8.70 / 8.98), and so do 7 row
-//   tiles below batch 16 (8192 -> 28672 B=12: GF4 33.05 / 33.37, E2M1 23.13 / 23.72) and
+//   one-slice plans stay (8192^2 B=8: GF4 11.76 / 12.71, E2M1 8.70 / 8.98), and so does
 //   split-K over fewer spans per wave (11008 -> 4096 B=16: GF4 11.85 / 12.67, E2M1 9.92 /
-//   10.19).
+//   10.19);
+// - 7 row tiles at batch 8-12, measured after the epilogue's slot reads were batched (they
+//   are the same sums in the same order as the two staged K-slices there, so the bits are
+//   equal): 8192 -> 28672 B=8 GF4 32.80 -> 32.54, E2M1 22.41 / 22.47; B=12 GF4 34.40 ->
+//   33.74, E2M1 23.36 -> 23.10.
 bool spanx_plan(const fb_shape_t* s, int cus, const Plan& staged, Plan& pl) {
   if (s->B < 2 || s->B > 16 || s->fwht_block || s->fmt == kFmtMx || staged.S < 2) return false;
   const int GS = (s->K / 128 + 3) / 4;
@@ -1696,7 +1699,7 @@ bool spanx_plan(const fb_shape_t* s, int cus, const Plan& staged, Plan& pl) {
   const int grid = std::max(1, std::min(T, cus));
   const int tpw = (T + grid - 1) / grid;
   const int nw = kWaves / 2;
-  if (tpw > (s->B == 16 ? 8 : 4) || tpw * ((GS + nw - 1) / nw) < 2) return false;
+  if (tpw > (s->B >= 8 ? 8 : 4) || tpw * ((GS + nw - 1) / nw) < 2) return false;
   if (s->fmt == FB_FMT_GF4 && GS <= nw) return false;  // one span per wave
   // the waves' x regions, which the (tile, wave) slots take over after the last unit
   const size_t lds = 16 + zero_bytes(s->fmt) +

@@ -124,7 +124,7 @@ def staged_slices(fmt, K, N, B, xdt):
 
 
 # Batches whose x the staged plan would cut into K-slices, on the plan where each of the 8
-# waves stages the x of its own spans: several row tiles per workgroup, a K that ends inside
+# waves stages the x of its own spans: several row tiles per workgroup (up to 7), a K that ends inside
 # a span (11008 = 21.5 spans), ragged rows, one span per wave (E2M1), batches that are not a
 # power of two, fp16 x, and a layer that split-K would otherwise take (16384 -> 4096).
 @pytest.mark.parametrize("fmt,K,N,B,xdt", [
@@ -132,6 +132,7 @@ def staged_slices(fmt, K, N, B, xdt):
     ("gf4", 11008, 4001, 8, torch.float16), ("e2m1", 11008, 4001, 12, torch.float16),
     ("e2m1", 4096, 11008, 16, torch.bfloat16), ("gf4", 28672, 8192, 3, torch.float16),
     ("e2m1", 16384, 4096, 16, torch.bfloat16), ("gf4", 8192, 16384, 16, torch.float16),
+    ("e2m1", 8192, 28672, 12, torch.bfloat16),  # 7 row tiles per workgroup
 ], ids=lambda v: str(v).replace("torch.", ""))
 def test_waves_stage_their_own_spans(fmt, K, N, B, xdt):
     say("own-span plan", fmt, K, N, B, xdt)
