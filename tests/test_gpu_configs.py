@@ -133,6 +133,7 @@ def staged_slices(fmt, K, N, B, xdt):
     ("e2m1", 4096, 11008, 16, torch.bfloat16), ("gf4", 28672, 8192, 3, torch.float16),
     ("e2m1", 16384, 4096, 16, torch.bfloat16), ("gf4", 8192, 16384, 16, torch.float16),
     ("e2m1", 8192, 28672, 12, torch.bfloat16),  # 7 row tiles per workgroup
+    ("e2m1", 3584, 28672, 16, torch.bfloat16),  # 7 spans: wave 7 owns none (zero slots)
 ], ids=lambda v: str(v).replace("torch.", ""))
 def test_waves_stage_their_own_spans(fmt, K, N, B, xdt):
     say("own-span plan", fmt, K, N, B, xdt)

@@ -134,6 +134,7 @@ def test_small_batch_wave_plans():
     assert plan(C.FMT_GF4, 8192, 28672, 16) == (8, 0)  # 7 row tiles at batch 16
     assert plan(C.FMT_E2M1, 4096, 11008, 16) == (8, 0)  # E2M1: one span per wave
     assert plan(C.FMT_GF4, 8192, 28672, 8) == (8, 0)  # 7 row tiles at batch 8
+    assert plan(C.FMT_E2M1, 3584, 28672, 16) == (8, 0)  # 7 spans: one wave owns none
     # ... but not with more than 4 row tiles below batch 8, GF4 with one span per wave, one
     # unit per wave, or where split-K (over fewer than 4 spans per wave) takes the layer
     assert plan(C.FMT_GF4, 28672, 28672, 4)[1] != 0
