@@ -82,8 +82,9 @@ size_t fb_device_bytes(const fb_shape_t* s);
  *    once into the workspace by its own small kernel before the GEMV;
  *  - plus P*B*N*4 (rounded up to 256) where the GEMV runs its K-parts side by side (batch
  *    >= 2 over a long K whose staged x would need 3 or more K-slices on few row tiles, e.g.
- *    11008 -> 4096 at batch 16, P = 4): each part's fp32 sums, added by one more small
- *    kernel in part order.
+ *    11008 -> 4096 at batch 16, P = 4; not where each wave staging the x of its own spans
+ *    is faster, 4 or more spans per wave on at least as many row tiles as CUs): each
+ *    part's fp32 sums, added by one more small kernel in part order.
  * The contents need no initialisation and are not kept between calls. */
 size_t fb_workspace_bytes(const fb_shape_t* s);
 
@@ -158,8 +159,9 @@ int fb_dequant_host(const uint8_t* codes, const void* meta, float* w_out, const 
  * a rotated call of B*K >= 16384 values rotates x once into ws (one extra small kernel)
  * and runs the unrotated GEMV on it, and a split-K shape runs its K-parts side by side with
  * their sums in ws; without it (NULL, too small or misaligned) every workgroup rotates x in
- * its prologue and the K-slices run in turn, which gives the same results within the
- * tolerance (each plan is deterministic) and is slower for such shapes.  Calls that share a
+ * its prologue and the K-parts run within one launch (K-slices in turn, or each wave
+ * staging the x of its own spans), which gives the same results within the tolerance (each
+ * plan is deterministic) and is slower for such shapes.  Calls that share a
  * workspace must not overlap.
  * A batch whose staged activations do not fit LDS at once (a 4096-wide rotation done in
  * the prologue keeps an fp32 copy of every batch row) runs as several launches over row
@@ -177,7 +179,8 @@ int fb_gemv(const void* wdev, const void* x, void* y, const fb_shape_t* s, void*
  * calls that overlap on one GPU (several streams or host threads) race; serialise them.
  * Split-K shapes keep their parts' sums in the array after the rotated x where they fit.
  * Results equal fb_gemv's with a workspace bit for bit, except for split-K shapes whose sums
- * do not fit: those run the K-slices in turn, within the tolerance of fb_gemv's result. */
+ * do not fit: those run their K-parts within one launch, as fb_gemv does without a
+ * workspace, within the tolerance of fb_gemv's result. */
 int fb_gemv_noalloc(const void* wdev, const void* x, void* y, const fb_shape_t* s,
                     void* stream);
 
