@@ -1072,6 +1072,24 @@ __global__ __launch_bounds__(NW * 64) void gemv_kernel(
   // x through a buffer resource (out-of-range offsets read zeros)
   const rsrc_t xrs = __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(x), (short)0, B * K * 2,
                                                        kRsrcWord3);
+  // MX path: the split's block scales, 8 bytes per (batch row, 128-value group), staged into
+  // the pad of each staged group (zeros past K).  Entry i of a slice is row i / nsl, group
+  // k0 / 128 + i % nsl.  They follow the codes in the split's layout, so no argument is
+  // needed for them.
+  const int G = K / 128;
+  const uint8_t* xsc = static_cast<const uint8_t*>(x) + mx_scale_offset(Bin, K);
+  const rsrc_t srs = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(xsc), (short)0,
+                                                       mx ? B * G * 8 : 0, kRsrcWord3);
+  auto sc_load = [&](int i, int k0) -> uint2 {
+    const int b = fdiv(i >> 2, SPL, spl_m);  // i / nsl, nsl = 4 SPL
+    const int gi = k0 / 128 + i - b * nsl;
+    const unsigned off = gi < G ? (unsigned)(b * G + gi) * 8u : kXOutOfRange;
+    return __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(srs, off, 0, 0));
+  };
+  auto sc_store = [&](int i, uint2 v) {
+    const int b = fdiv(i >> 2, SPL, spl_m);
+    *reinterpret_cast<uint2*>(xst + b * RS + (i - b * nsl) * kSliceBytes + 256) = v;
+  };
   if constexpr (MODE == kSpanX) {
     // Each wave owns the spans wave, wave + NW, ... of every row tile of the workgroup and
     // stages the x of one span at a time (B rows of 512 values, RS bytes per row) in an LDS
@@ -1084,10 +1102,14 @@ __global__ __launch_bounds__(NW * 64) void gemv_kernel(
     const int nt = t1 - t0;
     uint8_t* xw = xst + wave * B * RS;
     f32x4* wsl = reinterpret_cast<f32x4*>(xst);
-    const uint8_t* xlw = col < B ? xw + col * RS + q * kSliceBytes : zeros;
+    const uint8_t* xlw = col < B ? xw + col * RS + (mx ? 0 : q * kSliceBytes) : zeros;
     const int nsw = wave < GS ? (GS - 1 - wave) / NW + 1 : 0;  // spans of this wave
     const int nuw = nsw * nt;
+    // the native FP4 path stages the split's two E4M3 terms where bf16 x would be (the same
+    // bytes per value) and the group scales in each group's pad: lane 4 b + g takes batch
+    // row b's group g of the span
     u32x4 xv[16];
+    uint2 xsv = {0u, 0u};
     auto x_load = [&](int sp0) {
       const int k = sp0 * 512 + lane * 8;
 #pragma unroll
@@ -1096,12 +1118,21 @@ __global__ __launch_bounds__(NW * 64) void gemv_kernel(
           const unsigned off = k < K ? (unsigned)(b * K + k) * 2u : kXOutOfRange;
           xv[b] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(xrs, off, 0, 0));
         }
+      if constexpr (mx) {
+        const int gi = sp0 * 4 + (lane & 3);
+        const unsigned off = gi < G ? (unsigned)((lane >> 2) * G + gi) * 8u : kXOutOfRange;
+        if ((lane >> 2) < B)
+          xsv = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(srs, off, 0, 0));
+      }
     };
     auto x_put = [&]() {
       uint8_t* d = xw + (lane >> 4) * kSliceBytes + (lane & 15) * 16;
 #pragma unroll
       for (int b = 0; b < 16; ++b)
         if (b < B) *reinterpret_cast<u32x4*>(d + b * RS) = xv[b];
+      if constexpr (mx)
+        if ((lane >> 2) < B)
+          *reinterpret_cast<uint2*>(xw + (lane >> 2) * RS + (lane & 3) * kSliceBytes + 256) = xsv;
     };
     int is = wave, it = 0, ni = 0;  // the next unit to request
     auto w_issue = [&](Rec<FMT>& r) {
@@ -1133,7 +1164,11 @@ __global__ __launch_bounds__(NW * 64) void gemv_kernel(
       }
       w_issue(nxt);
       __builtin_amdgcn_sched_barrier(0);  // keep the prefetch ahead of the compute
-      const f32x4 p = unit_partial<FMT, XDT>(cur, xlw);
+      f32x4 p;
+      if constexpr (mx)
+        p = unit_partial_mx(cur, xlw, q);
+      else
+        p = unit_partial<FMT, XDT>(cur, xlw);
       const bool first = sc == wave;
       if (first && lt == 0) PH_MARK(kPhUnit0);
 #pragma unroll
@@ -1180,24 +1215,6 @@ __global__ __launch_bounds__(NW * 64) void gemv_kernel(
     PH_FLUSH(NW);
     return;
   }
-  // MX path: the split's block scales, 8 bytes per (batch row, 128-value group), staged into
-  // the pad of each staged group (zeros past K).  Entry i of a slice is row i / nsl, group
-  // k0 / 128 + i % nsl.  They follow the codes in the split's layout, so no argument is
-  // needed for them.
-  const int G = K / 128;
-  const uint8_t* xsc = static_cast<const uint8_t*>(x) + mx_scale_offset(Bin, K);
-  const rsrc_t srs = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(xsc), (short)0,
-                                                       mx ? B * G * 8 : 0, kRsrcWord3);
-  auto sc_load = [&](int i, int k0) -> uint2 {
-    const int b = fdiv(i >> 2, SPL, spl_m);  // i / nsl, nsl = 4 SPL
-    const int gi = k0 / 128 + i - b * nsl;
-    const unsigned off = gi < G ? (unsigned)(b * G + gi) * 8u : kXOutOfRange;
-    return __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(srs, off, 0, 0));
-  };
-  auto sc_store = [&](int i, uint2 v) {
-    const int b = fdiv(i >> 2, SPL, spl_m);
-    *reinterpret_cast<uint2*>(xst + b * RS + (i - b * nsl) * kSliceBytes + 256) = v;
-  };
   // Each wave's first two units are static (wave, wave + NW); the counter hands out
   // the rest.
   constexpr bool rot = MODE == kRotated || rot1;
@@ -1691,15 +1708,21 @@ bool make_plan_staged(const fb_shape_t* s, int cus, Plan& pl) {
 // - 7 row tiles at batch 8-12, measured after the epilogue's slot reads were batched (they
 //   are the same sums in the same order as the two staged K-slices there, so the bits are
 //   equal): 8192 -> 28672 B=8 GF4 32.80 -> 32.54, E2M1 22.41 / 22.47; B=12 GF4 34.40 ->
-//   33.74, E2M1 23.36 -> 23.10.
+//   33.74, E2M1 23.36 -> 23.10;
+// - the native FP4 path (fb_gemv_mx, split per call), same box: 8192^2 B=16 13.92 -> 13.16,
+//   4096 -> 11008 B=16 11.85 -> 9.97, 28672 -> 8192 B=8 28.50 -> 27.53, 11008 -> 4096 B=8
+//   11.63 -> 11.19, 8192 -> 28672 B=16 26.48 -> 26.32; but 7 row tiles at batch 8 slower
+//   (8192 -> 28672 B=8 23.75 / 24.72), so there it takes 8 row tiles at batch 16 only.
 bool spanx_plan(const fb_shape_t* s, int cus, const Plan& staged, Plan& pl) {
-  if (s->B < 2 || s->B > 16 || s->fwht_block || s->fmt == kFmtMx || staged.S < 2) return false;
+  if (s->B < 2 || s->B > 16 || s->fwht_block || staged.S < 2) return false;
   const int GS = (s->K / 128 + 3) / 4;
   const int T = (s->N + 15) / 16;
   const int grid = std::max(1, std::min(T, cus));
   const int tpw = (T + grid - 1) / grid;
   const int nw = kWaves / 2;
-  if (tpw > (s->B >= 8 ? 8 : 4) || tpw * ((GS + nw - 1) / nw) < 2) return false;
+  // at most 4 row tiles per workgroup; 8 at batch 8-16 (the native FP4 path: at batch 16)
+  const int tmax = s->B == 16 || (s->B >= 8 && s->fmt != kFmtMx) ? 8 : 4;
+  if (tpw > tmax || tpw * ((GS + nw - 1) / nw) < 2) return false;
   if (s->fmt == FB_FMT_GF4 && GS <= nw) return false;  // one span per wave
   // the waves' x regions, which the (tile, wave) slots take over after the last unit
   const size_t lds = 16 + zero_bytes(s->fmt) +
@@ -1834,7 +1857,7 @@ int launch_mode(int mode, const void* wdev, const void* x, void* y, const fb_sha
   // the native FP4 path's 8-wave batch 2-16 plan (its batch-1 layers, two 8-wave workgroups
   // per CU, run below in this unit)
   if constexpr (FMT == kFmtMx)
-    if ((mode == kFlat || mode == kSliced) && pl.nw == kWaves / 2)
+    if (((mode == kFlat || mode == kSliced) && pl.nw == kWaves / 2) || mode == kSpanX)
       return fb_ilp::launch(FMT, XDT, mode, wdev, x, y, s, pl.grid, pl.SPL, pl.GS, pl.tq, pl.tr,
                             pl.S, pl.lds, pl.xp, stream);
   // the max-ILP copies: the rotated batch-1 kernel, the 8-wave batch-1 one and the 8-wave
@@ -2240,6 +2263,10 @@ int launch(int fmt, int xdt, int mode, const void* wdev, const void* x, void* y,
                : launch_gemv<FB_FMT_E2M1, FB_DT_F16, kRotDAall, kWaves / 2, 4>(wdev, x, y, s, pl, stream);
   }
   if (mode == kSpanX) {
+    if (fmt == kFmtMx)
+      return xp == 2 ? launch_gemv<kFmtMx, FB_DT_BF16, kSpanX, kWaves / 2, 2>(wdev, x, y, s, pl, stream)
+           : xp == 4 ? launch_gemv<kFmtMx, FB_DT_BF16, kSpanX, kWaves / 2, 4>(wdev, x, y, s, pl, stream)
+                     : launch_gemv<kFmtMx, FB_DT_BF16, kSpanX, kWaves / 2, 8>(wdev, x, y, s, pl, stream);
     if (fmt == FB_FMT_GF4) {
       if (xdt != FB_DT_F16) return FB_ERR_DTYPE;
       return xp == 2 ? launch_gemv<FB_FMT_GF4, FB_DT_F16, kSpanX, kWaves / 2, 2>(wdev, x, y, s, pl, stream)
