@@ -1148,6 +1148,11 @@ __global__ __launch_bounds__(NW * 64) void gemv_kernel(
     };
     if (threadIdx.x < zero_bytes(FMT) / 16)
       reinterpret_cast<u32x4*>(zeros)[threadIdx.x] = u32x4{0u, 0u, 0u, 0u};
+    // GF4: units finished per wave, after the x regions / slots
+    int* prog = reinterpret_cast<int*>(xst + max(NW * B * RS, nt * NW * B * 64));
+    if constexpr (FMT == FB_FMT_GF4)
+      if (threadIdx.x < NW) prog[threadIdx.x] = 0;
+    int done = 0;
     if (nsw) x_load(wave);
     PH_MARK(kPhXIssued);
     Rec<FMT> rg[2];
@@ -1157,6 +1162,16 @@ __global__ __launch_bounds__(NW * 64) void gemv_kernel(
     f32x4 acc[kTMax];
     int sc = wave, lt = 0;
     auto step = [&](const Rec<FMT>& cur, Rec<FMT>& nxt) {
+      // GF4 (whose decode keeps the SIMDs busy): waves w and w + 4 share a SIMD, which issues
+      // the older one first; the one that has finished fewer units takes the higher priority
+      if constexpr (FMT == FB_FMT_GF4) {
+        const int pd = __builtin_amdgcn_readfirstlane(
+            __hip_atomic_load(prog + (wave ^ 4), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP));
+        if (done < pd)
+          __builtin_amdgcn_s_setprio(1);
+        else
+          __builtin_amdgcn_s_setprio(0);
+      }
       if (lt == 0) {
         x_put();
         PH_MARK(sc == wave ? kPhStaged : sc == wave + NW ? kPhStaged1 : kPhStaged2);
@@ -1171,6 +1186,11 @@ __global__ __launch_bounds__(NW * 64) void gemv_kernel(
         p = unit_partial<FMT, XDT>(cur, xlw);
       const bool first = sc == wave;
       if (first && lt == 0) PH_MARK(kPhUnit0);
+      if constexpr (FMT == FB_FMT_GF4) {
+        ++done;
+        if (lane == 0)
+          __hip_atomic_store(prog + wave, done, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+      }
 #pragma unroll
       for (int t = 0; t < kTMax; ++t)  // lt is wave-uniform: a scalar branch per tile
         if (t == lt) acc[t] = first ? p : acc[t] + p;
@@ -1184,6 +1204,7 @@ __global__ __launch_bounds__(NW * 64) void gemv_kernel(
       if (i + 1 >= nuw) break;
       step(rg[1], rg[0]);
     }
+    if constexpr (FMT == FB_FMT_GF4) __builtin_amdgcn_s_setprio(0);
     PH_MARK(kPhLoopEnd);
     __syncthreads();  // every wave is done with its x: the slots may take the x regions
     if (col < B) {  // a wave without spans (GS < NW) adds zeros
@@ -1726,7 +1747,8 @@ bool spanx_plan(const fb_shape_t* s, int cus, const Plan& staged, Plan& pl) {
   if (s->fmt == FB_FMT_GF4 && GS <= nw) return false;  // one span per wave
   // the waves' x regions, which the (tile, wave) slots take over after the last unit
   const size_t lds = 16 + zero_bytes(s->fmt) +
-                     std::max((size_t)nw * s->B * x_row_stride(4), (size_t)tpw * nw * s->B * 64);
+                     std::max((size_t)nw * s->B * x_row_stride(4), (size_t)tpw * nw * s->B * 64) +
+                     nw * 4;  // the waves' unit counts
   if (lds > (size_t)kLdsLimit) return false;
   pl = Plan();
   pl.S = 1;
